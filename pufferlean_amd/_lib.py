@@ -1,0 +1,76 @@
+"""ctypes binding of libpufferhip.so (the C ABI declared in include/pufferhip.h).
+
+The library is built in-tree by ``python -m pufferlean_amd.build``. Loading fails loudly when it
+is missing: there is no CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpufferhip.so"
+
+PH_OK, PH_ERR_ARG, PH_ERR_HIP, PH_ERR_NOMEM, PH_ERR_UNSUPPORTED = 0, -1, -2, -3, -4
+PH_F32, PH_F64, PH_BF16, PH_I32 = 0, 1, 2, 3
+PH_MATH_BF16, PH_MATH_F32 = 0, 1
+PH_EPI_NONE, PH_EPI_BIAS, PH_EPI_BIAS_RELU, PH_EPI_RELU_MASK, PH_EPI_AXPBY = 0, 1, 2, 3, 4
+
+vp, sz, dbl, flt, i32, i64, u8, u64 = (C.c_void_p, C.c_size_t, C.c_double, C.c_float, C.c_int,
+                                       C.c_long, C.c_uint8, C.c_uint64)
+dptr = C.POINTER(C.c_double)
+fptr = C.POINTER(C.c_float)
+szptr = C.POINTER(C.c_size_t)
+
+# name -> argtypes (all return int status unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "ph_last_error": [],
+    "ph_version": [],
+    "ph_device_count": [],
+    "ph_synchronize": [vp],
+    "ph_vtrace": [i32, vp, vp, vp, vp, vp, sz, sz, i32, i32, i32, i32, dbl, dbl, dbl, dbl, vp, vp, vp],
+    "ph_adv_normalize": [i32, vp, sz, vp, vp, vp],
+    "ph_colsum": [vp, sz, sz, sz, vp, flt, i32, vp],
+    "ph_convert": [i32, vp, i32, vp, sz, vp],
+    "ph_ppo_grad": [vp, sz, vp, sz, vp, vp, vp, vp, vp, sz, sz, flt, flt, flt, flt, i32, vp, sz,
+                    vp, sz, vp, vp, vp, vp],
+    "ph_gemm": [i32, i32, i32, i32, i32, i32, vp, i64, i32, vp, i64, i32, vp, i64, i32, i32, vp,
+                vp, i64, flt, flt, vp, i64, i32, i32, vp],
+}
+_RESTYPES = {"ph_last_error": C.c_char_p}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class PufferHipError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """The loaded library with argtypes set. Raises if the .so was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise PufferHipError(
+                    f"{LIB_PATH} is missing; build it with `python -m pufferlean_amd.build`")
+            h = C.CDLL(str(LIB_PATH), mode=C.RTLD_GLOBAL)
+            for name, args in SIGNATURES.items():
+                fn = getattr(h, name)
+                fn.argtypes = args
+                fn.restype = _RESTYPES.get(name, C.c_int)
+            _lib = h
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != PH_OK:
+        msg = lib().ph_last_error()
+        raise PufferHipError(f"{what} failed with status {status}: {msg.decode() if msg else ''}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

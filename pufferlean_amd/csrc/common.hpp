@@ -1,0 +1,68 @@
+// Shared helpers for the pufferhip library (gfx950 / CDNA4 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/pufferhip.h"
+
+namespace ph {
+
+// Last-error text of the calling thread (read through ph_last_error()).
+void set_error(const char* fmt, ...);
+
+#define PH_CHECK_HIP(expr)                                                                  \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) {                                                                 \
+      ::ph::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,      \
+                      __LINE__);                                                            \
+      return PH_ERR_HIP;                                                                    \
+    }                                                                                       \
+  } while (0)
+
+#define PH_REQUIRE(cond, ...)                                                               \
+  do {                                                                                      \
+    if (!(cond)) {                                                                          \
+      ::ph::set_error(__VA_ARGS__);                                                         \
+      return PH_ERR_ARG;                                                                    \
+    }                                                                                       \
+  } while (0)
+
+#define PH_TRY(expr)                                                                        \
+  do {                                                                                      \
+    int s_ = (expr);                                                                        \
+    if (s_ != PH_OK) return s_;                                                             \
+  } while (0)
+
+// Launch-error check right after a <<<>>> launch.
+#define PH_LAUNCH_CHECK() PH_CHECK_HIP(hipGetLastError())
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+// Growable per-slot device buffers owned by the library (allocated on first use, reused across
+// calls, freed at process exit). Slot ids are private to each translation unit's range.
+void* scratch(int slot, size_t bytes);
+
+// bf16 <-> f32 with round-to-nearest-even (IEEE bit trick; NaN kept quiet).
+__host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  uint32_t u = ((uint32_t)h) << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+}  // namespace ph

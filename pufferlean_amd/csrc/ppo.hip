@@ -1,0 +1,207 @@
+// Fused PPO loss gradient (one lane per row; bandwidth-bound, exp/log in registers).
+//
+// Per row: log-sum-exp over the A policy logits (optionally max-shifted), p_k, log p(a), the
+// importance ratio against the behaviour log-prob, the clipped-surrogate subgradient, the entropy
+// gradient, and PufferLib's clipped value-loss gradient; ascent sign (puffercuda.cu:692-744,
+// 4910-4930; pufferblas.c:726-736). Optionally the 7 dashboard losses are reduced deterministically
+// (per-block partials in f64, the last block folds them in block order).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ph {
+namespace {
+
+constexpr int kMaxA = 64;
+
+__device__ inline float vloss_grad(float vnew, float ret, float vold, bool has_old, float vfClip) {
+  if (vfClip <= 0.f || !has_old) return vnew - ret;
+  const float dd = vnew - vold;
+  const float vc = vold + (dd < -vfClip ? -vfClip : (dd > vfClip ? vfClip : dd));
+  const float du = (vnew - ret) * (vnew - ret), cc = (vc - ret) * (vc - ret);
+  if (du >= cc) return vnew - ret;
+  if (dd > -vfClip && dd < vfClip) return vnew - ret;
+  return 0.f;
+}
+
+template <int AMAX>
+__global__ void __launch_bounds__(256) k_ppo_grad(
+    const float* __restrict__ logits, int ldl, const float* __restrict__ values, int ldv,
+    const int* __restrict__ act, const float* __restrict__ adv, const float* __restrict__ ret,
+    const float* __restrict__ old, const float* __restrict__ ov, int N, int A, float vfCoef,
+    float entCoef, float clipEps, float vfClip, int max_shift, float* __restrict__ dlogits, int ldd,
+    float* __restrict__ dvalues, int lddv, float* __restrict__ newlp, float* __restrict__ newval,
+    double* __restrict__ part, unsigned* counter, double* __restrict__ losses) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  double lsum[6] = {0, 0, 0, 0, 0, 0};  // pg, v, ent, old_kl, kl, nclip
+  if (n < N) {
+    const float* lg = logits + (size_t)n * ldl;
+    float x[AMAX];
+#pragma unroll
+    for (int k = 0; k < AMAX; k++) x[k] = k < A ? lg[k] : 0.f;
+    float lse;
+    if (max_shift) {
+      float mx = x[0];
+#pragma unroll
+      for (int k = 1; k < AMAX; k++) if (k < A && x[k] > mx) mx = x[k];
+      float se = 0.f;
+#pragma unroll
+      for (int k = 0; k < AMAX; k++) if (k < A) se += expf(x[k] - mx);
+      lse = mx + logf(se);
+    } else {
+      float se = 0.f;
+#pragma unroll
+      for (int k = 0; k < AMAX; k++) if (k < A) se += expf(x[k]);
+      lse = logf(se);
+    }
+    float pk[AMAX];
+    float pout = 0.f;
+#pragma unroll
+    for (int k = 0; k < AMAX; k++) {
+      pk[k] = k < A ? expf(x[k] - lse) : 0.f;
+      if (k < A) pout += pk[k] * x[k];
+    }
+    const int a = act[n];
+    const float av = adv[n], rv = ret[n], ol = old[n];
+    float xa = 0.f;
+#pragma unroll
+    for (int k = 0; k < AMAX; k++) if (k == a) xa = x[k];
+    const float logpA = xa - lse;
+    const float ratio = expf(logpA - ol);
+    const float lo = 1.f - clipEps, hi = 1.f + clipEps;
+    const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+    const float s1 = av * ratio, s2 = av * rc;
+    float dpol;
+    if (s1 <= s2) dpol = av * ratio;
+    else dpol = av * ((lo < ratio && ratio < hi) ? 1.f : 0.f) * ratio;
+    float* dl = dlogits + (size_t)n * ldd;
+#pragma unroll
+    for (int k = 0; k < AMAX; k++)
+      if (k < A) dl[k] = dpol * ((k == a ? 1.f : 0.f) - pk[k]) + entCoef * pk[k] * (pout - x[k]);
+    const float vnew = values[(size_t)n * ldv];
+    const float vold = ov ? ov[n] : 0.f;
+    dvalues[(size_t)n * lddv] = -vfCoef * vloss_grad(vnew, rv, vold, ov != nullptr, vfClip);
+    if (newlp) newlp[n] = logpA;
+    if (newval) newval[n] = vnew;
+    if (losses) {
+      const double lr = (double)logpA - (double)ol;
+      const double r = exp(lr);
+      const double dlo = 1.0 - (double)clipEps, dhi = 1.0 + (double)clipEps;
+      const double rcd = r < dlo ? dlo : (r > dhi ? dhi : r);
+      const double p1 = -(double)av * r, p2 = -(double)av * rcd;
+      lsum[0] = p1 > p2 ? p1 : p2;
+      const double du = ((double)vnew - rv) * ((double)vnew - rv);
+      double vl = du;
+      if (vfClip > 0.f && ov) {
+        const double dd = (double)vnew - vold;
+        const double vc = vold + (dd < -vfClip ? -(double)vfClip : (dd > vfClip ? (double)vfClip : dd));
+        const double cc = (vc - rv) * (vc - rv);
+        if (cc > du) vl = cc;
+      }
+      lsum[1] = 0.5 * vl;
+      double ent = 0.0;
+#pragma unroll
+      for (int k = 0; k < AMAX; k++)
+        if (k < A) {
+          const double lp = (double)x[k] - (double)lse;
+          ent -= exp(lp) * lp;
+        }
+      lsum[2] = ent;
+      lsum[3] = -lr;
+      lsum[4] = (r - 1.0) - lr;
+      lsum[5] = (r < dlo || r > dhi) ? 1.0 : 0.0;
+    }
+  }
+  if (!losses) return;
+  // Deterministic block reduction of the 6 sums, then last-block fold over blocks in order.
+  __shared__ double sh[6][256];
+  __shared__ bool last;
+#pragma unroll
+  for (int q = 0; q < 6; q++) sh[q][threadIdx.x] = lsum[q];
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s)
+#pragma unroll
+      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int q = 0; q < 6; q++) part[(size_t)blockIdx.x * 6 + q] = sh[q][0];
+    __threadfence();
+    last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x < 6) {
+    double s = 0.0;
+    for (unsigned b = 0; b < gridDim.x; b++)
+      s += __hip_atomic_load(&part[(size_t)b * 6 + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh[threadIdx.x][0] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double dn = (double)(N > 0 ? N : 1);
+    const double pg = sh[0][0] / dn, vl = sh[1][0] / dn, en = sh[2][0] / dn;
+    losses[0] = pg;
+    losses[1] = vl;
+    losses[2] = en;
+    losses[3] = pg + (double)vfCoef * vl - (double)entCoef * en;
+    losses[4] = sh[3][0] / dn;
+    losses[5] = sh[4][0] / dn;
+    losses[6] = sh[5][0] / dn;
+    *counter = 0u;
+  }
+}
+
+}  // namespace
+
+int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, const int* act,
+             const float* adv, const float* ret, const float* old, const float* ov, size_t N,
+             size_t A, float vfCoef, float entCoef, float clipEps, float vfClip, int max_shift,
+             float* dlogits, size_t ldd, float* dvalues, size_t lddv, float* newlp, float* newval,
+             double* losses, hipStream_t st) {
+  if (N == 0) return PH_OK;
+  PH_REQUIRE(A >= 1 && A <= (size_t)kMaxA, "ppo_grad: action count %zu outside [1,%d]", A, kMaxA);
+  const unsigned grid = ceil_div(N, 256);
+  double* part = nullptr;
+  unsigned* counter = nullptr;
+  if (losses) {
+    part = (double*)scratch(kSlotPpoPart, (size_t)grid * 6 * 8);
+    counter = (unsigned*)scratch(kSlotPpoCounter, 256);
+    if (!part || !counter) return PH_ERR_NOMEM;
+    PH_TRY(ensure_zeroed_counter(counter, st));
+  }
+#define PH_PPO(AM)                                                                              \
+  k_ppo_grad<AM><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv, ret, old, ov, \
+                                       (int)N, (int)A, vfCoef, entCoef, clipEps, vfClip, max_shift, \
+                                       dlogits, (int)ldd, dvalues, (int)lddv, newlp, newval, part,  \
+                                       counter, losses)
+  if (A <= 2) PH_PPO(2);
+  else if (A <= 4) PH_PPO(4);
+  else if (A <= 8) PH_PPO(8);
+  else if (A <= 16) PH_PPO(16);
+  else if (A <= 32) PH_PPO(32);
+  else PH_PPO(64);
+#undef PH_PPO
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+}  // namespace ph
+
+using namespace ph;
+
+extern "C" int ph_ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv,
+                           const int* act, const float* adv, const float* ret, const float* old,
+                           const float* ov, size_t N, size_t A, float vfCoef, float entCoef,
+                           float clipEps, float vfClip, int max_shift, float* dlogits, size_t ldd,
+                           float* dvalues, size_t lddv, float* newlp, float* newval,
+                           double* losses, void* stream) {
+  PH_REQUIRE(N <= (size_t)INT32_MAX, "ph_ppo_grad: N exceeds int32");
+  PH_REQUIRE(N == 0 || (logits && values && act && adv && ret && old && dlogits && dvalues),
+             "ph_ppo_grad: null pointer");
+  return ppo_grad(logits, ldl, values, ldv, act, adv, ret, old, ov, N, A, vfCoef, entCoef, clipEps,
+                  vfClip, max_shift, dlogits, ldd, dvalues, lddv, newlp, newval, losses,
+                  as_stream(stream));
+}

@@ -1,0 +1,204 @@
+// Deterministic reductions and small elementwise kernels: advantage normalisation, column sums,
+// dtype conversion, minibatch gathers. Every reduction uses a fixed partition and a fixed tree, so
+// results are reproducible run to run (no float atomics).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ph {
+
+// Block-wide sum of one value per thread (256 threads) in a fixed tree; result valid in thread 0.
+template <typename R>
+__device__ inline R block_sum_256(R v, R* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+#pragma unroll
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) sh[threadIdx.x] += sh[threadIdx.x + s];
+    __syncthreads();
+  }
+  return sh[0];
+}
+
+namespace {
+
+// Stage of a two-pass mean/std over x[0..n): each block sums a contiguous chunk (mode 0: x, mode 1:
+// (x-mean)^2); the last block to finish reduces the per-block partials in index order and writes
+// stats[mode] (mode 0: mean, mode 1: sqrt(var)+eps). The arrival counter is reset by that block.
+template <typename R>
+__global__ void __launch_bounds__(256) k_moments(const R* __restrict__ x, size_t n, size_t chunk,
+                                                 R* __restrict__ part, unsigned* counter,
+                                                 R* __restrict__ stats, int mode, R eps) {
+  __shared__ R sh[256];
+  __shared__ bool last;
+  const size_t lo = (size_t)blockIdx.x * chunk;
+  const size_t hi = lo + chunk < n ? lo + chunk : n;
+  const R mean = mode ? stats[0] : R(0);
+  R acc = 0;
+  for (size_t i = lo + threadIdx.x; i < hi; i += 256) {
+    R v = x[i];
+    if (mode) {
+      R d = v - mean;
+      acc += d * d;
+    } else {
+      acc += v;
+    }
+  }
+  R s = block_sum_256(acc, sh);
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = s;
+    __threadfence();
+    unsigned prev = atomicAdd(counter, 1u);
+    last = (prev == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  R a2 = 0;
+  for (unsigned i = threadIdx.x; i < gridDim.x; i += 256)
+    a2 += __hip_atomic_load(&part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  R tot = block_sum_256(a2, sh);
+  if (threadIdx.x == 0) {
+    const R dn = (R)(n > 0 ? n : 1);
+    if (mode == 0) stats[0] = tot / dn;
+    else stats[1] = sqrt(tot / dn) + eps;
+    *counter = 0u;
+  }
+}
+
+template <typename R>
+__global__ void k_normalize(const R* __restrict__ x, R* __restrict__ y, size_t n,
+                            const R* __restrict__ stats) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (x[i] - stats[0]) / stats[1];
+}
+
+// Column sums of a row-major [N x J] matrix: grid (ceil(J/64), G) tiles; each block sums a chunk of
+// rows for 64 columns (coalesced row reads), partials [G][J]; k_colsum_finish adds them in order.
+__global__ void __launch_bounds__(256) k_colsum_part(const float* __restrict__ X, size_t N, int J,
+                                                     size_t ld, size_t rows_per, float* __restrict__ part) {
+  __shared__ float sh[4][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int r0 = threadIdx.x >> 6;  // 4 row lanes
+  const size_t lo = (size_t)blockIdx.y * rows_per;
+  const size_t hi = lo + rows_per < N ? lo + rows_per : N;
+  float acc = 0.f;
+  if (c < J)
+    for (size_t r = lo + r0; r < hi; r += 4) acc += X[r * ld + c];
+  sh[r0][threadIdx.x & 63] = acc;
+  __syncthreads();
+  if (threadIdx.x < 64 && c < J) {
+    float s = ((sh[0][threadIdx.x] + sh[1][threadIdx.x]) + sh[2][threadIdx.x]) + sh[3][threadIdx.x];
+    part[(size_t)blockIdx.y * J + c] = s;
+  }
+}
+
+__global__ void k_colsum_finish(const float* __restrict__ part, int G, int J, float* __restrict__ out,
+                                float scale, int accumulate) {
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= J) return;
+  float s = 0.f;
+  for (int g = 0; g < G; g++) s += part[(size_t)g * J + c];
+  s *= scale;
+  out[c] = accumulate ? out[c] + s : s;
+}
+
+template <typename S, typename D>
+__global__ void k_convert(const S* __restrict__ x, D* __restrict__ y, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (D)x[i];
+}
+
+__global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = f32_to_bf16_rne(x[i]);
+}
+
+}  // namespace
+
+int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st) {
+  if (n == 0) return PH_OK;
+  const size_t chunk = 4096;
+  size_t G = (n + chunk - 1) / chunk;
+  const size_t es = dtype == PH_F64 ? 8 : 4;
+  void* part = scratch(kSlotMomentsPart, G * es);
+  unsigned* counter = (unsigned*)scratch(kSlotMomentsCounter, 256);
+  if (!part || !counter) return PH_ERR_NOMEM;
+  if (!stats) {
+    stats = scratch(kSlotMomentsStats, 16);
+    if (!stats) return PH_ERR_NOMEM;
+  }
+  PH_TRY(ensure_zeroed_counter(counter, st));  // every launch leaves it at zero afterwards
+  const unsigned g = (unsigned)G;
+  if (dtype == PH_F64) {
+    k_moments<double><<<g, 256, 0, st>>>((const double*)x, n, chunk, (double*)part, counter, (double*)stats, 0, 1e-8);
+    k_moments<double><<<g, 256, 0, st>>>((const double*)x, n, chunk, (double*)part, counter, (double*)stats, 1, 1e-8);
+    if (y) k_normalize<double><<<ceil_div(n, 256), 256, 0, st>>>((const double*)x, (double*)y, n, (const double*)stats);
+  } else {
+    k_moments<float><<<g, 256, 0, st>>>((const float*)x, n, chunk, (float*)part, counter, (float*)stats, 0, 1e-8f);
+    k_moments<float><<<g, 256, 0, st>>>((const float*)x, n, chunk, (float*)part, counter, (float*)stats, 1, 1e-8f);
+    if (y) k_normalize<float><<<ceil_div(n, 256), 256, 0, st>>>((const float*)x, (float*)y, n, (const float*)stats);
+  }
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int colsum_f32(const float* X, size_t N, int J, size_t ld, float* out, float scale, int accumulate,
+               hipStream_t st) {
+  if (J <= 0) return PH_OK;
+  size_t rows_per = 1024;
+  size_t G = (N + rows_per - 1) / rows_per;
+  if (G == 0) G = 1;
+  if (G > 512) {  // cap partial count; rows_per grows instead
+    G = 512;
+    rows_per = (N + G - 1) / G;
+  }
+  float* part = (float*)scratch(kSlotColsumPart, G * (size_t)J * 4);
+  if (!part) return PH_ERR_NOMEM;
+  dim3 grid(ceil_div(J, 64), (unsigned)G);
+  k_colsum_part<<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, part);
+  k_colsum_finish<<<ceil_div(J, 256), 256, 0, st>>>(part, (int)G, J, out, scale, accumulate);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st) {
+  if (n == 0) return PH_OK;
+  const unsigned g = ceil_div(n, 256);
+  if (src_dtype == PH_F64 && dst_dtype == PH_F32)
+    k_convert<double, float><<<g, 256, 0, st>>>((const double*)x, (float*)y, n);
+  else if (src_dtype == PH_F32 && dst_dtype == PH_F64)
+    k_convert<float, double><<<g, 256, 0, st>>>((const float*)x, (double*)y, n);
+  else if (src_dtype == PH_F64 && dst_dtype == PH_I32)
+    k_convert<double, int><<<g, 256, 0, st>>>((const double*)x, (int*)y, n);
+  else if (src_dtype == PH_F32 && dst_dtype == PH_BF16)
+    k_f32_to_bf16<<<g, 256, 0, st>>>((const float*)x, (uint16_t*)y, n);
+  else {
+    set_error("convert: unsupported dtype pair %d -> %d", src_dtype, dst_dtype);
+    return PH_ERR_ARG;
+  }
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+}  // namespace ph
+
+using namespace ph;
+
+extern "C" int ph_adv_normalize(int dtype, const void* adv, size_t n, void* out, void* stats,
+                                void* stream) {
+  PH_REQUIRE(dtype == PH_F32 || dtype == PH_F64, "ph_adv_normalize: dtype must be F32 or F64");
+  PH_REQUIRE(n == 0 || (adv && out), "ph_adv_normalize: null pointer");
+  return moments_normalize(dtype, adv, n, out, stats, as_stream(stream));
+}
+
+extern "C" int ph_colsum(const float* X, size_t N, size_t J, size_t ld, float* out, float scale,
+                         int accumulate, void* stream) {
+  PH_REQUIRE(J <= (size_t)INT32_MAX, "ph_colsum: too many columns");
+  PH_REQUIRE(N * J == 0 || (X && out), "ph_colsum: null pointer");
+  return colsum_f32(X, N, (int)J, ld ? ld : J, out, scale, accumulate, as_stream(stream));
+}
+
+extern "C" int ph_convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n,
+                          void* stream) {
+  return convert(src_dtype, x, dst_dtype, y, n, as_stream(stream));
+}

@@ -1,0 +1,95 @@
+// Library runtime: error channel, per-device growable buffers, device query.
+#include <cstdarg>
+#include <mutex>
+#include <set>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ph {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+namespace {
+constexpr int kMaxDev = 16;
+constexpr int kSlots = 128;
+struct SlotTable {
+  void* ptr[kSlots] = {};
+  size_t bytes[kSlots] = {};
+};
+SlotTable g_tables[kMaxDev];
+std::mutex g_mu;
+}  // namespace
+
+// Buffers only grow; a grown slot is freed after a device sync so no queued kernel still reads it.
+void* scratch(int slot, size_t bytes) {
+  if (slot < 0 || slot >= kSlots) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  SlotTable& tb = g_tables[dev];
+  if (bytes == 0) bytes = 1;
+  if (tb.bytes[slot] >= bytes) return tb.ptr[slot];
+  if (tb.ptr[slot]) {
+    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    (void)hipFree(tb.ptr[slot]);
+    tb.ptr[slot] = nullptr;
+    tb.bytes[slot] = 0;
+  }
+  size_t rounded = (bytes + 255) & ~(size_t)255;
+  void* p = nullptr;
+  if (hipMalloc(&p, rounded) != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("device allocation of %zu bytes failed (slot %d)", rounded, slot);
+    return nullptr;
+  }
+  tb.ptr[slot] = p;
+  tb.bytes[slot] = rounded;
+  return p;
+}
+
+namespace {
+__global__ void k_zero_words(unsigned* p, int n) {
+  int i = threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+std::set<void*> g_zeroed;
+}  // namespace
+
+int ensure_zeroed_counter(unsigned* counter, hipStream_t st) {
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_zeroed.count(counter)) return PH_OK;
+    g_zeroed.insert(counter);
+  }
+  k_zero_words<<<1, 64, 0, st>>>(counter, 64);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+}  // namespace ph
+
+extern "C" const char* ph_last_error(void) { return ph::g_err; }
+
+extern "C" int ph_version(void) { return PH_VERSION; }
+
+extern "C" int ph_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+extern "C" int ph_synchronize(void* stream) {
+  PH_CHECK_HIP(hipStreamSynchronize(ph::as_stream(stream)));
+  return PH_OK;
+}

@@ -1,0 +1,154 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) for the tests and the CPU baseline.
+
+The oracle is test infrastructure: it checks the GPU library and is never part of it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent.parent / "oracle"
+ORACLE_SO = ORACLE_DIR / "liboracle.so"
+
+d = C.c_double
+sz = C.c_size_t
+i = C.c_int
+vp = C.c_void_p
+
+_SIG = {
+    "orc_rng_next": ([C.POINTER(C.c_uint64)], C.c_uint64),
+    "orc_uniform01": ([C.c_uint64], d),
+    "orc_randf": ([vp, sz, d, d, C.POINTER(C.c_uint64)], None),
+    "orc_vtrace_vec": ([vp, vp, vp, vp, sz, sz, d, d, d, d, vp], None),
+    "orc_vtrace_mingru": ([vp, vp, vp, vp, vp, sz, sz, d, d, d, d, vp], None),
+    "orc_gae_soa": ([vp, vp, vp, sz, sz, d, d, vp], None),
+    "orc_gae_boot_norm": ([vp, vp, vp, vp, sz, sz, d, d, vp], None),
+    "orc_vtrace_f64": ([vp, vp, vp, vp, vp, sz, sz, i, i, i, i, d, d, d, d, vp, vp], None),
+    "orc_vtrace_f32": ([vp, vp, vp, vp, vp, sz, sz, i, i, i, i, C.c_float, C.c_float, C.c_float,
+                        C.c_float, vp, vp], None),
+    "orc_adv_normalize": ([vp, sz, vp], None),
+    "orc_ppo_grad": ([vp, sz, vp, sz, vp, vp, vp, vp, vp, sz, sz, d, d, d, d, i, vp, sz, vp, sz,
+                      vp, vp], None),
+    "orc_ppo_losses": ([vp, sz, vp, sz, vp, vp, vp, vp, vp, sz, sz, d, d, d, d, vp], None),
+    "orc_gemm": ([i, i, sz, sz, sz, d, vp, sz, vp, sz, d, vp, sz, i], None),
+    "orc_dense_forward": ([vp, vp, vp, sz, sz, sz, vp], None),
+    "orc_mlp_forward": ([vp, vp, sz, sz, sz, sz, vp], None),
+    "orc_mlp_ppo_grad": ([vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, d, d, d, vp, i], None),
+    "orc_newton_schulz": ([vp, i, i, vp, i, d, i, vp], None),
+    "orc_muon_mat": ([i, i, vp, vp, vp, vp, vp, d, d, d, d, d, vp, i, i], None),
+    "orc_stepvec": ([i, vp, vp, vp, vp, vp, d, d, d, d], None),
+    "orc_muon_step_mlp": ([vp, vp, sz, sz, sz, d, d, d, d, d, vp], None),
+    "orc_gclip": ([vp, sz, d, d], d),
+    "orc_mingru_ppo_grad_seq": ([vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d, d, d, d,
+                                 vp], None),
+    "orc_mingru_heinsen": ([vp, vp, sz, sz, vp], None),
+}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not ORACLE_SO.exists():
+            build()
+        h = C.CDLL(str(ORACLE_SO))
+        for name, (args, res) in _SIG.items():
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = h
+    return _lib
+
+
+def P(a: np.ndarray | None):
+    """Pointer to a C-contiguous numpy array (or NULL)."""
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle inputs must be C-contiguous"
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def f64(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- thin numpy wrappers -------------------------------------------------------------------------
+
+def coeffs_array(coeffs) -> np.ndarray:
+    return f64(np.asarray(coeffs, dtype=np.float64).reshape(-1, 3))
+
+
+REF_COEFFS = [(4.0848, -6.8946, 2.9270), (3.9505, -6.3029, 2.6377), (3.7418, -5.5913, 2.3037),
+              (2.8769, -3.1427, 1.2046), (2.8366, -3.0525, 1.2012)]
+BASELINE_COEFFS = [(3.4445, -4.7750, 2.0315)] * 5
+
+
+def vtrace(rew, val, term, rho, boot, B, T, *, variant, time_major, rho_is_log=False, clamp=True,
+           gamma=0.99, lam=0.95, rho_clip=1.0, c_clip=1.0, dtype=np.float64):
+    conv = f64 if dtype == np.float64 else f32
+    rew, val, term = conv(rew), conv(val), conv(term)
+    rho = None if rho is None else conv(rho)
+    boot = None if boot is None else conv(boot)
+    adv = np.zeros(B * T, dtype=dtype)
+    tgt = np.zeros(B * T, dtype=dtype)
+    fn = lib().orc_vtrace_f64 if dtype == np.float64 else lib().orc_vtrace_f32
+    fn(P(rew), P(val), P(term), P(rho), P(boot), B, T, variant, int(time_major), int(rho_is_log),
+       int(clamp), gamma, lam, rho_clip, c_clip, P(adv), P(tgt))
+    return adv, tgt
+
+
+def gemm(transA, transB, A, B, M, N, K, threads=1):
+    A, B = f64(A), f64(B)
+    lda = A.shape[1]
+    ldb = B.shape[1]
+    Cm = np.zeros((M, N))
+    lib().orc_gemm(int(transA), int(transB), M, N, K, 1.0, P(A), lda, P(B), ldb, 0.0, P(Cm), N,
+                   threads)
+    return Cm
+
+
+def newton_schulz(X0, coeffs, eps=1e-7, form=1):
+    X0 = f64(X0)
+    rows, cols = X0.shape
+    c = coeffs_array(coeffs)
+    out = np.zeros_like(X0)
+    lib().orc_newton_schulz(P(X0), rows, cols, P(c), c.shape[0], eps, form, P(out))
+    return out
+
+
+def ppo_grad(logits, values, act, adv, ret, old, ov=None, *, vf=0.5, ent=0.01, clip=0.2,
+             vfclip=0.0, max_shift=False):
+    logits = f64(logits)
+    N, A = logits.shape
+    values = f64(values)
+    dl = np.zeros((N, A))
+    dv = np.zeros(N)
+    nlp = np.zeros(N)
+    nv = np.zeros(N)
+    lib().orc_ppo_grad(P(logits), A, P(values), 1, P(f64(act)), P(f64(adv)), P(f64(ret)),
+                       P(f64(old)), P(None if ov is None else f64(ov)), N, A, vf, ent, clip,
+                       vfclip, int(max_shift), P(dl), A, P(dv), 1, P(nlp), P(nv))
+    return dl, dv, nlp, nv
+
+
+def ppo_losses(logits, values, act, adv, ret, old, ov=None, *, vf=0.5, ent=0.01, clip=0.2,
+               vfclip=0.0):
+    logits = f64(logits)
+    N, A = logits.shape
+    L = np.zeros(7)
+    lib().orc_ppo_losses(P(logits), A, P(f64(values)), 1, P(f64(act)), P(f64(adv)), P(f64(ret)),
+                         P(f64(old)), P(None if ov is None else f64(ov)), N, A, vf, ent, clip,
+                         vfclip, P(L))
+    return L

@@ -1,0 +1,123 @@
+"""MFMA GEMMs vs the f64 oracle GEMM: all transpose forms, dtypes, epilogues, edge shapes.
+
+Tolerances (relative Frobenius): fp32 math 1e-5 vs f64; bf16 math 1e-2 vs f64 on the unrounded
+inputs, and 1e-5 vs f64 on the bf16-rounded inputs (isolates the fp32 accumulation).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from pufferlean_amd import _lib as L
+from pufferlean_amd import device as D
+from pufferlean_amd import rng
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def bf16_round(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def operands(M, N, K, ta, tb, seed):
+    a = rng.normal(seed, M * K).reshape((K, M) if ta else (M, K)).astype(np.float32)
+    b = (rng.normal(seed + 1, K * N) / np.sqrt(K)).reshape((N, K) if tb else (K, N)).astype(np.float32)
+    return a, b
+
+
+def oracle(a, b, ta, tb, M, N, K):
+    return O.gemm(ta, tb, a, b, M, N, K, threads=8)
+
+
+FORMS = [(0, 0), (0, 1), (1, 0), (1, 1)]
+
+
+@pytest.mark.parametrize("ta,tb", FORMS)
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 136, 72), (64, 64, 512), (512, 512, 2048)])
+@pytest.mark.parametrize("math_", ["bf16", "f32"])
+def test_gemm_forms(gpu, ta, tb, M, N, K, math_):
+    a, b = operands(M, N, K, ta, tb, 100 + M + N + K)
+    ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), math=math_).cpu().numpy()
+    ref = oracle(a, b, ta, tb, M, N, K)
+    if math_ == "f32":
+        assert rel(c, ref) < 1e-5
+    else:
+        assert rel(c, ref) < 1e-2
+        ref_r = oracle(bf16_round(a), bf16_round(b), ta, tb, M, N, K)
+        assert rel(c, ref_r) < 1e-5
+
+
+@pytest.mark.parametrize("ta,tb", FORMS)
+def test_gemm_bf16_storage_and_output(gpu, ta, tb):
+    M, N, K = 384, 256, 320
+    a, b = operands(M, N, K, ta, tb, 7)
+    ga = torch.from_numpy(a).cuda().to(torch.bfloat16)
+    gb = torch.from_numpy(b).cuda().to(torch.bfloat16)
+    c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), out_dtype=torch.bfloat16).float().cpu().numpy()
+    ref_r = oracle(bf16_round(a), bf16_round(b), ta, tb, M, N, K)
+    assert rel(c, ref_r) < 4e-3  # one bf16 rounding of the output
+    assert rel(c, oracle(a, b, ta, tb, M, N, K)) < 1e-2
+
+
+def test_gemm_config2_full_size(gpu):
+    """16384 x 512 x 512 in the three policy forms; checked against the oracle on sampled rows
+    (forward/dgrad) and sampled columns (wgrad)."""
+    M, K, N = 16384, 512, 512
+    X = rng.normal(200, M * K).reshape(M, K).astype(np.float32)
+    W = (rng.normal(201, K * N) / np.sqrt(512)).reshape(N, K).astype(np.float32)  # [out][in]
+    dY = rng.normal(202, M * N).reshape(M, N).astype(np.float32)
+    gX, gW, gdY = (torch.from_numpy(v).cuda() for v in (X, W, dY))
+    rows = np.sort(rng.randint(203, 256, M))
+    cols = np.sort(rng.randint(204, 64, N))
+    for math_, tol in (("bf16", 1e-2), ("f32", 1e-5)):
+        # forward Y = X W^T
+        Y = D.gemm(gX, gW, trans_b=True, math=math_).cpu().numpy()
+        assert rel(Y[rows], O.gemm(0, 1, X[rows], W, len(rows), N, K)) < tol
+        # dgrad dX = dY W
+        dX = D.gemm(gdY, gW, math=math_).cpu().numpy()
+        assert rel(dX[rows], O.gemm(0, 0, dY[rows], W, len(rows), K, N)) < tol
+        # wgrad dW = dY^T X  ([N x K], reduction over the 16384 rows; split-K path)
+        dW = D.gemm(gdY, gX, trans_a=True, math=math_).cpu().numpy()
+        ref = O.gemm(1, 0, dY, np.ascontiguousarray(X[:, cols]), N, len(cols), M, threads=8)
+        assert rel(dW[:, cols], ref) < tol
+        dW2 = D.gemm(gdY, gX, trans_a=True, math=math_).cpu().numpy()
+        assert np.array_equal(dW, dW2)  # deterministic split-K fold
+
+
+def test_gemm_epilogues(gpu):
+    M, N, K = 200, 96, 64
+    a, b = operands(M, N, K, 0, 1, 9)
+    ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    bias = torch.from_numpy(rng.normal(10, N).astype(np.float32)).cuda()
+    ref = oracle(a, b, 0, 1, M, N, K)
+    bn = bias.cpu().numpy()
+    c = D.gemm(ga, gb, trans_b=True, math="f32", epilogue=L.PH_EPI_BIAS, bias=bias).cpu().numpy()
+    assert rel(c, ref + bn) < 1e-5
+    c = D.gemm(ga, gb, trans_b=True, math="f32", epilogue=L.PH_EPI_BIAS_RELU, bias=bias).cpu().numpy()
+    np.testing.assert_array_equal(c <= 0, (ref + bn) <= 0)
+    assert rel(c, np.maximum(ref + bn, 0)) < 1e-5
+    aux = torch.from_numpy(rng.normal(11, M * N).reshape(M, N).astype(np.float32)).cuda()
+    auxn = aux.cpu().numpy()
+    c = D.gemm(ga, gb, trans_b=True, math="f32", epilogue=L.PH_EPI_RELU_MASK, aux=aux).cpu().numpy()
+    np.testing.assert_array_equal(c == 0, (auxn <= 0) | (ref == 0))
+    assert rel(c, np.where(auxn > 0, ref, 0)) < 1e-5
+    c2 = torch.empty((N, M), device="cuda", dtype=torch.bfloat16)
+    c = D.gemm(ga, gb, trans_b=True, math="f32", epilogue=L.PH_EPI_AXPBY, aux=aux, alpha=-0.5,
+               beta=2.0, out2=c2, out2_trans=True).cpu().numpy()
+    assert rel(c, -0.5 * ref + 2.0 * auxn) < 1e-5
+    assert rel(c2.float().cpu().numpy(), c.T) < 4e-3
+
+
+@pytest.mark.parametrize("M,N,K", [(65536, 128, 4), (65536, 3, 128), (128, 4, 16384), (3, 128, 16384)])
+def test_gemm_small_dims_scalar_path(gpu, M, N, K):
+    # the CartPole policy's 4-wide input layer and 3-wide head take the scalar kernel
+    for ta, tb in FORMS:
+        a, b = operands(M, N, K, ta, tb, 13 + ta * 2 + tb)
+        ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), math="f32").cpu().numpy()
+        assert rel(c, oracle(a, b, ta, tb, M, N, K)) < 1e-5
