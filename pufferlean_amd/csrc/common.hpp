@@ -65,4 +65,13 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h) {
   return f;
 }
 
+// Device conversions on the gfx950 hardware converter (v_cvt_pk_bf16_f32, round-to-nearest-even).
+typedef __bf16 ph_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ph_floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  ph_floatx2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ph_bf16x2));
+}
+__device__ __forceinline__ uint16_t bf16_rne(float a) { return (uint16_t)(bf16x2_rne(a, 0.f) & 0xffffu); }
+
 }  // namespace ph

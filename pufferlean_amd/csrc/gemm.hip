@@ -19,6 +19,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace ph {
 namespace {
 
@@ -48,25 +50,41 @@ struct GemmArgs {
   int remap;     // XCD-aware tile order
 };
 
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
-}
-
-// 8 consecutive source elements -> 8 bf16 (raw bits in a uint4).
-__device__ inline uint4 load8_bf16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ inline uint4 load8_bf16(const float* p) {
-  const float4 x = reinterpret_cast<const float4*>(p)[0];
-  const float4 y = reinterpret_cast<const float4*>(p)[1];
-  uint4 r;
-  r.x = pack_bf16x2(x.x, x.y);
-  r.y = pack_bf16x2(x.z, x.w);
-  r.z = pack_bf16x2(y.x, y.y);
-  r.w = pack_bf16x2(y.z, y.w);
-  return r;
-}
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return bf16x2_rne(a, b); }
 
 __device__ inline float to_f32(uint16_t v) { return bf16_to_f32(v); }
 __device__ inline float to_f32(float v) { return v; }
+
+// Raw 8-element chunk as loaded (no conversion, so a prefetched load is not waited on until the
+// chunk is written to LDS).
+template <typename T> struct Raw8;
+template <> struct Raw8<uint16_t> { uint4 v; };
+template <> struct Raw8<float> { float4 a, b; };
+__device__ inline Raw8<uint16_t> load_raw8(const uint16_t* p) { return {*reinterpret_cast<const uint4*>(p)}; }
+__device__ inline Raw8<float> load_raw8(const float* p) {
+  return {reinterpret_cast<const float4*>(p)[0], reinterpret_cast<const float4*>(p)[1]};
+}
+__device__ inline Raw8<uint16_t> zero_raw8(const uint16_t*) { return {make_uint4(0, 0, 0, 0)}; }
+__device__ inline Raw8<float> zero_raw8(const float*) {
+  return {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+}
+__device__ inline uint4 to_bf16x8(const Raw8<uint16_t>& r) { return r.v; }
+__device__ inline uint4 to_bf16x8(const Raw8<float>& r) {
+  uint4 o;
+  o.x = pack_bf16x2(r.a.x, r.a.y);
+  o.y = pack_bf16x2(r.a.z, r.a.w);
+  o.z = pack_bf16x2(r.b.x, r.b.y);
+  o.w = pack_bf16x2(r.b.z, r.b.w);
+  return o;
+}
+
+// Workgroup barrier that orders LDS only: global loads still in flight (the prefetched k-tiles)
+// are not drained, unlike __syncthreads(), whose fence waits for every outstanding memory access.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Thread-block tile id -> (tile_m, tile_n). With remap, the blocks that land on one XCD (blocks are
 // dispatched round-robin over the 8 XCDs) get a contiguous run of tiles sharing the same A rows.
@@ -83,54 +101,231 @@ __device__ inline void store_out(TOut* p, float v);
 template <>
 __device__ inline void store_out<float>(float* p, float v) { *p = v; }
 template <>
-__device__ inline void store_out<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16_rne(v); }
+__device__ inline void store_out<uint16_t>(uint16_t* p, float v) { *p = bf16_rne(v); }
 
-template <typename TC>
-__device__ inline void epilogue_store(const GemmArgs& g, int row, int col, float acc) {
+template <int EPI, typename TC>
+__device__ __forceinline__ void epilogue_store_t(const GemmArgs& g, int row, int col, float acc) {
   if (row >= g.M || col >= g.N) return;
   float v = acc;
-  switch (g.epi) {
-    case PH_EPI_BIAS: v = acc + g.bias[col]; break;
-    case PH_EPI_BIAS_RELU: v = fmaxf(acc + g.bias[col], 0.f); break;
-    case PH_EPI_RELU_MASK: {
-      const float h = to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]);
-      v = h > 0.f ? acc : 0.f;
-      break;
-    }
-    case PH_EPI_AXPBY: {
-      const float x = g.aux ? to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]) : 0.f;
-      v = g.alpha * acc + g.beta * x;
-      break;
-    }
-    default: break;
+  if constexpr (EPI == PH_EPI_BIAS) v = acc + g.bias[col];
+  if constexpr (EPI == PH_EPI_BIAS_RELU) v = fmaxf(acc + g.bias[col], 0.f);
+  if constexpr (EPI == PH_EPI_RELU_MASK) {
+    const float h = to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]);
+    v = h > 0.f ? acc : 0.f;
+  }
+  if constexpr (EPI == PH_EPI_AXPBY) {
+    const float x = g.aux ? to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]) : 0.f;
+    v = g.alpha * acc + g.beta * x;
   }
   store_out<TC>(reinterpret_cast<TC*>(g.C) + (long)row * g.ldc + col, v);
   if (g.C2) {
     const long o = g.c2_trans ? (long)col * g.ldc2 + row : (long)row * g.ldc2 + col;
-    g.C2[o] = f32_to_bf16_rne(v);
+    g.C2[o] = bf16_rne(v);
+  }
+}
+
+template <typename TC>
+__device__ __forceinline__ void epilogue_store(const GemmArgs& g, int row, int col, float acc) {
+  switch (g.epi) {
+    case PH_EPI_BIAS: epilogue_store_t<PH_EPI_BIAS, TC>(g, row, col, acc); break;
+    case PH_EPI_BIAS_RELU: epilogue_store_t<PH_EPI_BIAS_RELU, TC>(g, row, col, acc); break;
+    case PH_EPI_RELU_MASK: epilogue_store_t<PH_EPI_RELU_MASK, TC>(g, row, col, acc); break;
+    case PH_EPI_AXPBY: epilogue_store_t<PH_EPI_AXPBY, TC>(g, row, col, acc); break;
+    default: epilogue_store_t<PH_EPI_NONE, TC>(g, row, col, acc); break;
+  }
+}
+
+// Writes a wave's SM x SN block of 32x32 accumulators (or the split-K partial). The epilogue
+// switch sits outside the element loops. Accumulator layout of a 32x32 MFMA: lane holds column
+// (lane & 31); element r sits in row 8*(r/4) + 4*(lane/32) + (r%4).
+template <int EPI, typename TC, int SM, int SN>
+__device__ __forceinline__ void write_tile_t(const GemmArgs& g, const floatx16 (&acc)[SM][SN], int r0, int c0,
+                                    int lane) {
+  const int hrow = (lane >> 5) * 4, lr = lane & 31;
+#pragma unroll
+  for (int i = 0; i < SM; i++)
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = r0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3);
+        const int col = c0 + j * 32 + lr;
+        if constexpr (EPI < 0) {
+          if (row < g.M && col < g.N) g.ws[((long)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][r];
+        } else {
+          epilogue_store_t<EPI, TC>(g, row, col, acc[i][j][r]);
+        }
+      }
+}
+
+template <typename TC, int SM, int SN>
+__device__ __forceinline__ void write_tile(const GemmArgs& g, const floatx16 (&acc)[SM][SN], int r0, int c0,
+                                  int lane) {
+  if (g.ws) { write_tile_t<-1, TC>(g, acc, r0, c0, lane); return; }
+  switch (g.epi) {
+    case PH_EPI_BIAS: write_tile_t<PH_EPI_BIAS, TC>(g, acc, r0, c0, lane); break;
+    case PH_EPI_BIAS_RELU: write_tile_t<PH_EPI_BIAS_RELU, TC>(g, acc, r0, c0, lane); break;
+    case PH_EPI_RELU_MASK: write_tile_t<PH_EPI_RELU_MASK, TC>(g, acc, r0, c0, lane); break;
+    case PH_EPI_AXPBY: write_tile_t<PH_EPI_AXPBY, TC>(g, acc, r0, c0, lane); break;
+    default: write_tile_t<PH_EPI_NONE, TC>(g, acc, r0, c0, lane); break;
+  }
+}
+
+// LDS-staged epilogue. The block's fp32 accumulators are first written to an LDS tile
+// [BM][BN+4]; the whole block then walks it in 4-column chunks, applies the epilogue with vector
+// loads of bias/aux, and writes each chunk with one 16-byte (fp32) or 8-byte (bf16) store, so a
+// wavefront's stores cover whole contiguous row segments.
+template <int SM, int SN, int LDC>
+__device__ __forceinline__ void stage_acc(float* sC, const floatx16 (&acc)[SM][SN], int wm0, int wn0,
+                                          int lane) {
+  const int hrow = (lane >> 5) * 4, lr = lane & 31;
+#pragma unroll
+  for (int i = 0; i < SM; i++)
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        sC[(wm0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3)) * LDC + wn0 + j * 32 + lr] = acc[i][j][r];
+}
+
+__device__ __forceinline__ float4 load4_f32(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4_f32(const uint16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(bf16_to_f32(u.x & 0xffffu), bf16_to_f32(u.x >> 16), bf16_to_f32(u.y & 0xffffu),
+                     bf16_to_f32(u.y >> 16));
+}
+__device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void store4(uint16_t* p, float4 v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+}
+
+template <int EPI, typename TC>
+__device__ __forceinline__ float4 apply_epi4(const GemmArgs& g, int row, int col, float4 v) {
+  if constexpr (EPI == PH_EPI_BIAS || EPI == PH_EPI_BIAS_RELU) {
+    const float4 b = load4_f32(g.bias + col);
+    v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+    if constexpr (EPI == PH_EPI_BIAS_RELU) {
+      v.x = fmaxf(v.x, 0.f); v.y = fmaxf(v.y, 0.f); v.z = fmaxf(v.z, 0.f); v.w = fmaxf(v.w, 0.f);
+    }
+  }
+  if constexpr (EPI == PH_EPI_RELU_MASK) {
+    const float4 h = load4_f32(reinterpret_cast<const TC*>(g.aux) + (long)row * g.ldaux + col);
+    v.x = h.x > 0.f ? v.x : 0.f; v.y = h.y > 0.f ? v.y : 0.f;
+    v.z = h.z > 0.f ? v.z : 0.f; v.w = h.w > 0.f ? v.w : 0.f;
+  }
+  if constexpr (EPI == PH_EPI_AXPBY) {
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g.aux) x = load4_f32(reinterpret_cast<const TC*>(g.aux) + (long)row * g.ldaux + col);
+    v.x = g.alpha * v.x + g.beta * x.x; v.y = g.alpha * v.y + g.beta * x.y;
+    v.z = g.alpha * v.z + g.beta * x.z; v.w = g.alpha * v.w + g.beta * x.w;
+  }
+  return v;
+}
+
+template <int EPI, typename TC, int BM, int BN, int NT, int LDC>
+__device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m0, int n0, bool vec) {
+  constexpr int CPR = BN / 4;               // 4-column chunks per row
+  constexpr int NCH = BM * CPR / NT;        // chunks per thread
+  static_assert(NCH * NT == BM * CPR, "C tile / threads");
+  if (vec) {
+    // all LDS reads first (one wait), then one vector store per chunk
+    float4 v[NCH];
+#pragma unroll
+    for (int q = 0; q < NCH; q++) {
+      const int c = threadIdx.x + q * NT;
+      v[q] = *reinterpret_cast<const float4*>(&sC[(c / CPR) * LDC + (c % CPR) * 4]);
+    }
+#pragma unroll
+    for (int q = 0; q < NCH; q++) {
+      const int c = threadIdx.x + q * NT;
+      const int lr = c / CPR, lc = (c % CPR) * 4;
+      const int row = m0 + lr, col = n0 + lc;
+      if (row >= g.M || col >= g.N) continue;
+      if constexpr (EPI < 0) {
+        store4(g.ws + ((long)blockIdx.z * g.M + row) * g.N + col, v[q]);
+      } else {
+        const float4 w = apply_epi4<EPI, TC>(g, row, col, v[q]);
+        store4(reinterpret_cast<TC*>(g.C) + (long)row * g.ldc + col, w);
+        if (g.C2 && !g.c2_trans) store4(g.C2 + (long)row * g.ldc2 + col, w);
+        if (g.C2 && g.c2_trans) *reinterpret_cast<float4*>(&sC[lr * LDC + lc]) = w;
+      }
+    }
+  } else {
+    // unaligned or ragged shapes: element stores
+#pragma unroll 1
+    for (int c = threadIdx.x; c < BM * BN; c += NT) {
+      const int lr = c / BN, lc = c % BN;
+      const int row = m0 + lr, col = n0 + lc;
+      if (row >= g.M || col >= g.N) continue;
+      const float e = sC[lr * LDC + lc];
+      if constexpr (EPI < 0) g.ws[((long)blockIdx.z * g.M + row) * g.N + col] = e;
+      else epilogue_store_t<EPI, TC>(g, row, col, e);
+    }
+  }
+  if constexpr (EPI >= 0) {
+    if (vec && g.C2 && g.c2_trans) {
+      // transposed bf16 copy: chunks of 4 consecutive rows of one column -> one 8-byte store
+      lds_barrier();
+      constexpr int CPC = BM / 4;
+      for (int c = threadIdx.x; c < BN * CPC; c += NT) {
+        const int lc = c / CPC, lr = (c % CPC) * 4;
+        const int row = m0 + lr, col = n0 + lc;
+        if (row >= g.M || col >= g.N) continue;
+        const float4 v = make_float4(sC[lr * LDC + lc], sC[(lr + 1) * LDC + lc],
+                                     sC[(lr + 2) * LDC + lc], sC[(lr + 3) * LDC + lc]);
+        store4(g.C2 + (long)col * g.ldc2 + row, v);
+      }
+    }
+  }
+}
+
+template <typename TC, int BM, int BN, int NT, int LDC>
+__device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0, int n0) {
+  // vector path: every 4-column chunk is whole and 16-byte (fp32) / 8-byte (bf16) aligned
+  const bool vec = (g.N % 4 == 0) && (g.ws ? true : (g.ldc % 4 == 0 && ((uintptr_t)g.C % 16) == 0)) &&
+                   (!g.aux || (g.ldaux % 4 == 0 && ((uintptr_t)g.aux % 16) == 0)) &&
+                   (!g.C2 || ((g.c2_trans ? g.M % 4 : g.ldc2 % 4) == 0 && ((uintptr_t)g.C2 % 8) == 0 &&
+                              (g.c2_trans ? g.ldc2 % 4 == 0 : true))) &&
+                   (!g.bias || ((uintptr_t)g.bias % 16) == 0);
+  if (g.ws) { flush_tile_t<-1, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); return; }
+  switch (g.epi) {
+    case PH_EPI_BIAS: flush_tile_t<PH_EPI_BIAS, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); break;
+    case PH_EPI_BIAS_RELU: flush_tile_t<PH_EPI_BIAS_RELU, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); break;
+    case PH_EPI_RELU_MASK: flush_tile_t<PH_EPI_RELU_MASK, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); break;
+    case PH_EPI_AXPBY: flush_tile_t<PH_EPI_AXPBY, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); break;
+    default: flush_tile_t<PH_EPI_NONE, TC, BM, BN, NT, LDC>(g, sC, m0, n0, vec); break;
   }
 }
 
 // ------------------------------------------------------------------------------------------------
-// bf16-math kernel.
-template <int BM, int BN, int BK, bool TA, bool TB, typename TIA, typename TIB, typename TC>
-__global__ void __launch_bounds__(256) k_gemm_bf16(GemmArgs g) {
+// bf16-math kernel. WGM x WGN wavefronts; prefetch distance 2: while k-tile kt is multiplied out of
+// LDS, tile kt+1 sits in registers and tile kt+2 is in flight from memory. The two register sets
+// alternate, so the k loop is unrolled by two to keep every register index static.
+template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, typename TIA, typename TIB,
+          typename TC>
+__global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
+  constexpr int NT = WGM * WGN * 64;
   constexpr int PAD = 8;
   constexpr int LDK = BK + PAD;             // LDS row pitch in bf16 elements
-  constexpr int WM = BM / 2, WN = BN / 2;   // per-wave tile
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int SM = WM / 32, SN = WN / 32; // 32x32 sub-tiles per wave
-  constexpr int CA = BM * BK / 8 / 256;     // 8-element chunks per thread (A)
-  constexpr int CB = BN * BK / 8 / 256;
-  static_assert(CA >= 1 && CB >= 1, "tile too small for 256 threads");
-  static_assert(BK % 32 == 0, "BK must be a multiple of 32");
+  constexpr int CA = BM * BK / 8 / NT;      // 8-element chunks per thread (A)
+  constexpr int CB = BN * BK / 8 / NT;
+  static_assert(CA >= 1 && CB >= 1 && CA * NT * 8 == BM * BK && CB * NT * 8 == BN * BK, "tile/threads");
+  static_assert(BK % 32 == 0 && SM >= 1 && SN >= 1, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDK];
+  constexpr int LDC = BN + 4;  // fp32 C staging pitch
+  constexpr int PIPE_BYTES = 2 * (BM + BN) * LDK * 2;
+  constexpr int C_BYTES = BM * LDC * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
+  uint16_t (*sA)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
+  uint16_t (*sB)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
+  float* sC = reinterpret_cast<float*>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   int bm, bn;
   tile_coords(tm, tn, g.remap, bm, bn);
@@ -142,52 +337,55 @@ __global__ void __launch_bounds__(256) k_gemm_bf16(GemmArgs g) {
   const TIA* A = reinterpret_cast<const TIA*>(g.A);
   const TIB* B = reinterpret_cast<const TIB*>(g.B);
 
-  uint4 ra[CA], rb[CB];
+  Raw8<TIA> ra[2][CA];
+  Raw8<TIB> rb[2][CB];
+  uint32_t va[2], vb[2];  // per-chunk validity bits of each register set
 
-  // Global -> registers for k-tile starting at k0. Out-of-range elements read as zero.
-  auto gload = [&](int k0) {
+  // Global -> register set for the k-tile starting at k0. Every load is issued unconditionally (an
+  // out-of-range chunk reads a clamped in-range address and is zeroed when written to LDS), so no
+  // branch separates the loads and the compiler can wait for exactly the set it needs.
+  auto gload = [&](Raw8<TIA> (&xa)[CA], Raw8<TIB> (&xb)[CB], uint32_t& ma, uint32_t& mb, int k0) {
+    ma = 0u;
+    mb = 0u;
 #pragma unroll
     for (int c = 0; c < CA; c++) {
-      const int id = tid + c * 256;
+      const int id = tid + c * NT;
       int r, k;
       if (!TA) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
       else { k = id / (BM / 8); r = (id % (BM / 8)) * 8; }
       const int gm = m0 + r, gk = k0 + k;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (!TA) {
-        if (gm < g.M && gk < kend) v = load8_bf16(A + (long)gm * g.lda + gk);
-      } else {
-        if (gk < kend && gm < g.M) v = load8_bf16(A + (long)gk * g.lda + gm);
-      }
-      ra[c] = v;
+      const bool ok = gm < g.M && gk < kend;
+      const long off = ok ? (!TA ? (long)gm * g.lda + gk : (long)gk * g.lda + gm) : 0;
+      xa[c] = load_raw8(A + off);
+      ma |= (ok ? 1u : 0u) << c;
     }
 #pragma unroll
     for (int c = 0; c < CB; c++) {
-      const int id = tid + c * 256;
+      const int id = tid + c * NT;
       int r, k;
       if (TB) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
       else { k = id / (BN / 8); r = (id % (BN / 8)) * 8; }
       const int gn = n0 + r, gk = k0 + k;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (TB) {
-        if (gn < g.N && gk < kend) v = load8_bf16(B + (long)gn * g.ldb + gk);
-      } else {
-        if (gk < kend && gn < g.N) v = load8_bf16(B + (long)gk * g.ldb + gn);
-      }
-      rb[c] = v;
+      const bool ok = gn < g.N && gk < kend;
+      const long off = ok ? (TB ? (long)gn * g.ldb + gk : (long)gk * g.ldb + gn) : 0;
+      xb[c] = load_raw8(B + off);
+      mb |= (ok ? 1u : 0u) << c;
     }
   };
-  // Registers -> LDS buffer `s` (transposing m/n-contiguous chunks).
-  auto sstore = [&](int s) {
+  // Register set -> LDS buffer `s` (transposing m/n-contiguous chunks).
+  auto sstore = [&](const Raw8<TIA> (&xa)[CA], const Raw8<TIB> (&xb)[CB], uint32_t ma, uint32_t mb,
+                    int s) {
 #pragma unroll
     for (int c = 0; c < CA; c++) {
-      const int id = tid + c * 256;
+      const int id = tid + c * NT;
+      uint4 v = to_bf16x8(xa[c]);
+      if (!((ma >> c) & 1u)) v = make_uint4(0, 0, 0, 0);
       if (!TA) {
         const int r = id / (BK / 8), k = (id % (BK / 8)) * 8;
-        *reinterpret_cast<uint4*>(&sA[s][r * LDK + k]) = ra[c];
+        *reinterpret_cast<uint4*>(&sA[s][r * LDK + k]) = v;
       } else {
         const int k = id / (BM / 8), r = (id % (BM / 8)) * 8;
-        const uint32_t w[4] = {ra[c].x, ra[c].y, ra[c].z, ra[c].w};
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           sA[s][(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
@@ -197,13 +395,15 @@ __global__ void __launch_bounds__(256) k_gemm_bf16(GemmArgs g) {
     }
 #pragma unroll
     for (int c = 0; c < CB; c++) {
-      const int id = tid + c * 256;
+      const int id = tid + c * NT;
+      uint4 v = to_bf16x8(xb[c]);
+      if (!((mb >> c) & 1u)) v = make_uint4(0, 0, 0, 0);
       if (TB) {
         const int r = id / (BK / 8), k = (id % (BK / 8)) * 8;
-        *reinterpret_cast<uint4*>(&sB[s][r * LDK + k]) = rb[c];
+        *reinterpret_cast<uint4*>(&sB[s][r * LDK + k]) = v;
       } else {
         const int k = id / (BN / 8), r = (id % (BN / 8)) * 8;
-        const uint32_t w[4] = {rb[c].x, rb[c].y, rb[c].z, rb[c].w};
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           sB[s][(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
@@ -224,14 +424,7 @@ __global__ void __launch_bounds__(256) k_gemm_bf16(GemmArgs g) {
   const int lr = lane & 31;         // row (A) / column (B) inside a 32x32 sub-tile
   const int lk = (lane >> 5) * 16;  // this lane's 16-wide k slice inside each 32-wide k block
 
-  if (nk > 0) {
-    gload(kbeg);
-    sstore(0);
-    __syncthreads();
-  }
-  for (int kt = 0; kt < nk; kt++) {
-    const int s = kt & 1;
-    if (kt + 1 < nk) gload(kbeg + (kt + 1) * BK);
+  auto compute = [&](int s) {
 #pragma unroll
     for (int kb = 0; kb < BK; kb += 32) {
       uint4 a0[SM], a1[SM], b0[SN], b1[SN];
@@ -247,37 +440,47 @@ __global__ void __launch_bounds__(256) k_gemm_bf16(GemmArgs g) {
         b0[j] = *reinterpret_cast<const uint4*>(p);
         b1[j] = *reinterpret_cast<const uint4*>(p + 8);
       }
+      // all accumulators once with the first k half, then once with the second: consecutive
+      // MFMAs never depend on each other
 #pragma unroll
       for (int i = 0; i < SM; i++)
 #pragma unroll
-        for (int j = 0; j < SN; j++) {
+        for (int j = 0; j < SN; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               __builtin_bit_cast(bf16x8_t, a0[i]), __builtin_bit_cast(bf16x8_t, b0[j]), acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < SM; i++)
+#pragma unroll
+        for (int j = 0; j < SN; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               __builtin_bit_cast(bf16x8_t, a1[i]), __builtin_bit_cast(bf16x8_t, b1[j]), acc[i][j], 0, 0, 0);
-        }
     }
-    if (kt + 1 < nk) sstore(s ^ 1);
-    __syncthreads();
+  };
+
+  // Prologue: tile 0 -> LDS buffer 0, tile 1 -> register set 1 (in flight).
+  if (nk > 0) {
+    gload(ra[0], rb[0], va[0], vb[0], kbeg);
+    if (nk > 1) gload(ra[1], rb[1], va[1], vb[1], kbeg + BK);
+    sstore(ra[0], rb[0], va[0], vb[0], 0);
+    lds_barrier();
+  }
+  // Step for tile kt held in LDS buffer P; register set P^1 holds tile kt+1; set P receives kt+2.
+  auto step = [&](int kt, auto Pc) {
+    constexpr int P = decltype(Pc)::value;
+    if (kt + 2 < nk) gload(ra[P], rb[P], va[P], vb[P], kbeg + (kt + 2) * BK);
+    compute(P);
+    if (kt + 1 < nk) sstore(ra[P ^ 1], rb[P ^ 1], va[P ^ 1], vb[P ^ 1], P ^ 1);
+    lds_barrier();
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
   }
 
-  // Accumulator layout of a 32x32 MFMA: lane holds column (lane & 31); element r sits in row
-  // 8*(r/4) + 4*(lane/32) + (r%4).
-  const int hrow = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < SM; i++)
-#pragma unroll
-    for (int j = 0; j < SN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3);
-        const int col = n0 + wn0 + j * 32 + lr;
-        if (g.ws) {
-          if (row < g.M && col < g.N) g.ws[((long)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][r];
-        } else {
-          epilogue_store<TC>(g, row, col, acc[i][j][r]);
-        }
-      }
+  // the last loop iteration ended with a barrier: the pipeline buffers are free for the C tile
+  stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
+  lds_barrier();
+  flush_tile<TC, BM, BN, NT, LDC>(g, sC, m0, n0);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -293,8 +496,13 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
   static_assert(CA >= 1 && CB >= 1, "tile too small");
   static_assert(BK % 8 == 0, "BK must be a multiple of 8");
 
-  __shared__ __attribute__((aligned(16))) float sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) float sB[2][BN * LDK];
+  constexpr int LDC = BN + 4;
+  constexpr int PIPE_BYTES = 2 * (BM + BN) * LDK * 4;
+  constexpr int C_BYTES = BM * LDC * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
+  float (*sA)[BM * LDK] = reinterpret_cast<float (*)[BM * LDK]>(smem);
+  float (*sB)[BN * LDK] = reinterpret_cast<float (*)[BN * LDK]>(smem + 2 * BM * LDK * 4);
+  float* sC = reinterpret_cast<float*>(smem);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
@@ -381,7 +589,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
   if (nk > 0) {
     gload(kbeg);
     sstore(0);
-    __syncthreads();
+    lds_barrier();
   }
   for (int kt = 0; kt < nk; kt++) {
     const int s = kt & 1;
@@ -404,23 +612,11 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
         }
     }
     if (kt + 1 < nk) sstore(s ^ 1);
-    __syncthreads();
+    lds_barrier();
   }
-  const int hrow = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < SM; i++)
-#pragma unroll
-    for (int j = 0; j < SN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3);
-        const int col = n0 + wn0 + j * 32 + lr;
-        if (g.ws) {
-          if (row < g.M && col < g.N) g.ws[((long)blockIdx.z * g.M + row) * g.N + col] = acc[i][j][r];
-        } else {
-          epilogue_store<TC>(g, row, col, acc[i][j][r]);
-        }
-      }
+  stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
+  lds_barrier();
+  flush_tile<TC, BM, BN, 256, LDC>(g, sC, m0, n0);
 }
 
 // Split-K fold: C = epilogue(sum over splits in order).
@@ -437,8 +633,8 @@ __global__ void k_splitk_reduce(GemmArgs g, int splits) {
 // ------------------------------------------------------------------------------------------------
 template <int BM, int BN, int BK, bool TA, bool TB, typename TIA, typename TIB>
 void launch_bf16(const GemmArgs& g, dim3 grid, hipStream_t st) {
-  if (g.c_bf16) k_gemm_bf16<BM, BN, BK, TA, TB, TIA, TIB, uint16_t><<<grid, 256, 0, st>>>(g);
-  else k_gemm_bf16<BM, BN, BK, TA, TB, TIA, TIB, float><<<grid, 256, 0, st>>>(g);
+  if (g.c_bf16) k_gemm_bf16<BM, BN, BK, 2, 2, TA, TB, TIA, TIB, uint16_t><<<grid, 256, 0, st>>>(g);
+  else k_gemm_bf16<BM, BN, BK, 2, 2, TA, TB, TIA, TIB, float><<<grid, 256, 0, st>>>(g);
 }
 
 template <int BM, int BN, int BK, typename TIA, typename TIB>
@@ -449,12 +645,14 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
   else launch_bf16<BM, BN, BK, true, true, TIA, TIB>(g, grid, st);
 }
 
-template <int BM, int BN, int BK>
+// fp32 operands are kept raw (8 floats per chunk) in the two prefetch register sets, so they use
+// half the k-tile of bf16 operands to stay within the register file.
+template <int BM, int BN>
 void dispatch_bf16(const GemmArgs& g, int a_dt, int b_dt, int ta, int tb, dim3 grid, hipStream_t st) {
-  if (a_dt == PH_BF16 && b_dt == PH_BF16) dispatch_bf16_t<BM, BN, BK, uint16_t, uint16_t>(g, ta, tb, grid, st);
-  else if (a_dt == PH_F32 && b_dt == PH_F32) dispatch_bf16_t<BM, BN, BK, float, float>(g, ta, tb, grid, st);
-  else if (a_dt == PH_BF16 && b_dt == PH_F32) dispatch_bf16_t<BM, BN, BK, uint16_t, float>(g, ta, tb, grid, st);
-  else dispatch_bf16_t<BM, BN, BK, float, uint16_t>(g, ta, tb, grid, st);
+  if (a_dt == PH_BF16 && b_dt == PH_BF16) dispatch_bf16_t<BM, BN, 64, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  else if (a_dt == PH_F32 && b_dt == PH_F32) dispatch_bf16_t<BM, BN, 32, float, float>(g, ta, tb, grid, st);
+  else if (a_dt == PH_BF16 && b_dt == PH_F32) dispatch_bf16_t<BM, BN, 32, uint16_t, float>(g, ta, tb, grid, st);
+  else dispatch_bf16_t<BM, BN, 32, float, uint16_t>(g, ta, tb, grid, st);
 }
 
 template <int BM, int BN, int BK>
@@ -485,8 +683,8 @@ __global__ void __launch_bounds__(256) k_gemm_scalar(GemmArgs g, int ta, int tb,
     float a = to_f32(ta ? A[(long)k * g.lda + row] : A[(long)row * g.lda + k]);
     float b = to_f32(tb ? B[(long)col * g.ldb + k] : B[(long)k * g.ldb + col]);
     if (bf) {
-      a = bf16_to_f32(f32_to_bf16_rne(a));
-      b = bf16_to_f32(f32_to_bf16_rne(b));
+      a = bf16_to_f32(bf16_rne(a));
+      b = bf16_to_f32(bf16_rne(b));
     }
     acc += a * b;
   }
@@ -561,7 +759,7 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
       if (splits < 1) splits = 1;
     }
   }
-  const int BK = d.math == PH_MATH_BF16 ? 64 : 32;
+  const int BK = 64;  // split granularity: a multiple of every k-tile in use
   int kps = (d.K + splits - 1) / splits;
   kps = (kps + BK - 1) / BK * BK;
   splits = kps > 0 ? (d.K + kps - 1) / kps : 1;
@@ -575,8 +773,8 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   const unsigned tiles = (unsigned)(((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn));
   dim3 grid(tiles, 1, splits);
   if (d.math == PH_MATH_BF16) {
-    if (small) dispatch_bf16<64, 64, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
-    else dispatch_bf16<128, 128, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
+    if (small) dispatch_bf16<64, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
+    else dispatch_bf16<128, 128>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
   } else {
     if (small) dispatch_f32<64, 64, 32>(g, d.trans_a, d.trans_b, grid, st);
     else dispatch_f32<128, 128, 32>(g, d.trans_a, d.trans_b, grid, st);

@@ -110,7 +110,7 @@ __global__ void k_convert(const S* __restrict__ x, D* __restrict__ y, size_t n) 
 
 __global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = f32_to_bf16_rne(x[i]);
+  if (i < n) y[i] = bf16_rne(x[i]);
 }
 
 }  // namespace
