@@ -33,7 +33,9 @@ typedef enum {
 } ph_status;
 
 typedef enum { PH_F32 = 0, PH_F64 = 1, PH_BF16 = 2, PH_I32 = 3 } ph_dtype;
-typedef enum { PH_MATH_BF16 = 0, PH_MATH_F32 = 1 } ph_math;
+/* PH_MATH_BF16X3: fp32 operands split into bf16 hi + lo, three MFMA products per k (hi*hi + hi*lo
+ * + lo*hi), close to fp32 accuracy on the bf16 matrix cores. */
+typedef enum { PH_MATH_BF16 = 0, PH_MATH_F32 = 1, PH_MATH_BF16X3 = 2 } ph_math;
 typedef enum {
   PH_EPI_NONE = 0,       /* C = acc */
   PH_EPI_BIAS = 1,       /* C = acc + bias[col] */
@@ -105,6 +107,78 @@ int ph_gemm(int trans_a, int trans_b, int M, int N, int K, int a_dtype, const vo
             int b_dtype, const void* B, long ldb, int c_dtype, void* C, long ldc, int math,
             int epilogue, const float* bias, const void* aux, long ldaux, float alpha, float beta,
             void* C2, long ldc2, int c2_trans, int splits, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Muon / Newton-Schulz.
+ * Exact tier (f64, device buffers): one Muon matrix step with the reference's op order, bit-exact
+ * with the CPU path (muon_mat_cpu, pufferblas.c:1369-1400; muon_mat_dev, puffercuda.cu:892-912).
+ * nW/nM may alias W/M. coeffs: nsteps rows of (a, b, c), host memory. */
+int ph_muon_mat_f64(int rows, int cols, const double* W, const double* G, const double* M,
+                    double* nW, double* nM, double gscale, double lr, double wd, double mu,
+                    double eps, const double* coeffs, int nsteps, void* stream);
+/* Bias step (stepvec_cpu, pufferblas.c:1403-1406; k_stepvec, puffercuda.cu:880-889). */
+int ph_stepvec_f64(size_t n, const double* b, const double* g, const double* m, double* nb,
+                   double* nm, double gscale, double lr, double wd, double mu, void* stream);
+/* Fast tier (fp32 state, bf16 or fp32 MFMA): in-place NS orthogonalisation of X (rows x cols),
+ * X <- NS(X/(|X|_F+eps)) with X <- aX + (bA + cA^2)X, A = XX^T, tall matrices transposed to wide
+ * (newtonSchulzWith, Puffer/Float/Muon.lean:73-89, on MFMA; replaces muon_mat_dev_bf,
+ * puffercuda.cu:942-966). coeffs: host float[nsteps][3]. */
+int ph_newton_schulz(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
+                     int math, void* stream);
+/* In-place Muon matrix step on fp32 state: M <- mu*M + gscale*G; U = gscale*G + mu*M;
+ * W <- (1-lr*wd)*W + lr*sqrt(max(1,rows/cols))*NS(U). */
+int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
+                float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
+                void* stream);
+/* In-place bias step on fp32 state. */
+int ph_stepvec(float* b, const float* g, float* m, size_t n, float gscale, float lr, float wd,
+               float mu, void* stream);
+/* Global grad-norm clip, in place: g <- g*sc*min(1, maxNorm/|g*sc|) (maxNorm <= 0: g*sc)
+ * (k_gclip_norm/k_gclip_scale, puffercuda.cu:5122-5131). */
+int ph_gclip(float* g, size_t n, float sc, float maxNorm, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
+/* MinGRU policy PPO+Muon minibatch step (the reference's MinGRU trainer chain: cudaMgVtracePrioFFI ->
+ * cudaMinGRUPpoGradFFI -> cudaMinGRUMuonResidentFFI, Puffer/RL/MinGRUTrain.lean:814-849;
+ * lean_cuda_mingru_ppo_grad puffercuda.cu:5206, lean_cuda_mingru_muon_resident puffercuda.cu:5727).
+ * Policy: obs D -> encoder H -> L MinGRU layers of H -> A-way categorical head + value head; params
+ * and momentum are fp32 [P] in the reference's flattenMG order [wEnc(H*D) | bEnc(H) | L x W(3H*H) |
+ * wDec(A*H) | bDec(A) | wVal(H) | bVal(1)]. All columns are time-major [T][B] (obs [T][B][D]); act is
+ * int32; done is 0/1. GEMMs run bf16 MFMA with fp32 accumulate; activations are stored bf16. */
+/* precision 0: bf16 activations and weight copies, bf16 MFMA (fp32 accumulate, fp32 master weights
+ * and gradient); 1: fp32 throughout on fp32 MFMA (the tight cross-check tier). */
+typedef struct { int B, T, D, H, L, A, precision; } ph_mingru_dims;
+typedef struct {
+  float gamma, lam, rho_clip, c_clip;        /* V-trace */
+  float clip_eps, vf_coef, ent_coef, vf_clip; /* PPO loss (vf_clip <= 0: unclipped value loss) */
+} ph_ppo_coefs;
+typedef struct {
+  float lr, wd, mu, eps;     /* Muon */
+  float max_grad_norm;       /* global grad-norm clip (<= 0: none) */
+  float gscale;              /* gradient scale applied with the clip (1/rows for a mean) */
+  int nsteps, math;          /* NS steps, PH_MATH_BF16 or PH_MATH_F32 */
+  const float* coeffs;       /* host float[nsteps][3] */
+} ph_muon_coefs;
+long ph_mingru_param_count(const ph_mingru_dims* d);
+/* Forward + backward over one minibatch: G (fp32 [P]) receives the summed gradient of the PPO
+ * objective (ascent sign, reference convention), newlp/newval the new log-prob of the taken action
+ * and the new value per row, losses (optional, device double[7]) the dashboard losses. adv is the
+ * normalised advantage, ret the value target. */
+int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c, const float* params,
+                       const float* obs, const int* act, const float* adv, const float* ret,
+                       const float* oldlp, const float* oldval, const float* done, float* G,
+                       float* newlp, float* newval, double* losses, void* stream);
+/* Grad-norm clip of G (scaled by gscale) then Muon on every matrix, stepvec on every bias, in place
+ * on params/mom (the matrices: wEnc, each W_l, wDec, wVal). */
+int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params, float* mom,
+                   float* G, void* stream);
+/* The whole minibatch step: V-trace (bootstrapped variant on oldval with boot[B]; logrho may be NULL
+ * for ratio 1) -> advantage normalisation -> ph_mingru_ppo_grad -> ph_mingru_muon. G is caller
+ * scratch of P floats (holds the clipped gradient afterwards). */
+int ph_mingru_step(const ph_mingru_dims* d, const ph_ppo_coefs* c, const ph_muon_coefs* m,
+                   float* params, float* mom, const float* obs, const int* act, const float* oldlp,
+                   const float* oldval, const float* rew, const float* done, const float* logrho,
+                   const float* boot, float* G, double* losses, void* stream);
 
 #ifdef __cplusplus
 }

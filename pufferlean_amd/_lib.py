@@ -13,7 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libpufferhip.so"
 
 PH_OK, PH_ERR_ARG, PH_ERR_HIP, PH_ERR_NOMEM, PH_ERR_UNSUPPORTED = 0, -1, -2, -3, -4
 PH_F32, PH_F64, PH_BF16, PH_I32 = 0, 1, 2, 3
-PH_MATH_BF16, PH_MATH_F32 = 0, 1
+PH_MATH_BF16, PH_MATH_F32, PH_MATH_BF16X3 = 0, 1, 2
 PH_EPI_NONE, PH_EPI_BIAS, PH_EPI_BIAS_RELU, PH_EPI_RELU_MASK, PH_EPI_AXPBY = 0, 1, 2, 3, 4
 
 vp, sz, dbl, flt, i32, i64, u8, u64 = (C.c_void_p, C.c_size_t, C.c_double, C.c_float, C.c_int,
@@ -21,6 +21,22 @@ vp, sz, dbl, flt, i32, i64, u8, u64 = (C.c_void_p, C.c_size_t, C.c_double, C.c_f
 dptr = C.POINTER(C.c_double)
 fptr = C.POINTER(C.c_float)
 szptr = C.POINTER(C.c_size_t)
+
+
+class MinGRUDims(C.Structure):
+    _fields_ = [("B", C.c_int), ("T", C.c_int), ("D", C.c_int), ("H", C.c_int), ("L", C.c_int),
+                ("A", C.c_int), ("precision", C.c_int)]
+
+
+class PPOCoefs(C.Structure):
+    _fields_ = [(n, C.c_float) for n in ("gamma", "lam", "rho_clip", "c_clip", "clip_eps", "vf_coef",
+                                         "ent_coef", "vf_clip")]
+
+
+class MuonCoefs(C.Structure):
+    _fields_ = [("lr", C.c_float), ("wd", C.c_float), ("mu", C.c_float), ("eps", C.c_float),
+                ("max_grad_norm", C.c_float), ("gscale", C.c_float), ("nsteps", C.c_int),
+                ("math", C.c_int), ("coeffs", C.c_void_p)]
 
 # name -> argtypes (all return int status unless listed in _RESTYPES)
 SIGNATURES: dict[str, list] = {
@@ -36,8 +52,18 @@ SIGNATURES: dict[str, list] = {
                     vp, sz, vp, vp, vp, vp],
     "ph_gemm": [i32, i32, i32, i32, i32, i32, vp, i64, i32, vp, i64, i32, vp, i64, i32, i32, vp,
                 vp, i64, flt, flt, vp, i64, i32, i32, vp],
+    "ph_muon_mat_f64": [i32, i32, vp, vp, vp, vp, vp, dbl, dbl, dbl, dbl, dbl, vp, i32, vp],
+    "ph_stepvec_f64": [sz, vp, vp, vp, vp, vp, dbl, dbl, dbl, dbl, vp],
+    "ph_newton_schulz": [vp, i32, i32, vp, i32, flt, i32, vp],
+    "ph_muon_mat": [vp, vp, vp, i32, i32, flt, flt, flt, flt, flt, vp, i32, i32, vp],
+    "ph_stepvec": [vp, vp, vp, sz, flt, flt, flt, flt, vp],
+    "ph_gclip": [vp, sz, flt, flt, vp],
+    "ph_mingru_param_count": [vp],
+    "ph_mingru_ppo_grad": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "ph_mingru_muon": [vp, vp, vp, vp, vp, vp],
+    "ph_mingru_step": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
 }
-_RESTYPES = {"ph_last_error": C.c_char_p}
+_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long}
 
 _lib = None
 _lock = threading.Lock()

@@ -78,6 +78,18 @@ __device__ inline uint4 to_bf16x8(const Raw8<float>& r) {
   return o;
 }
 
+// Low half of the split x = hi + lo: lo = bf16(x - hi) for the 8 elements of a chunk.
+__device__ inline uint4 lo_bf16x8(const Raw8<float>& r, const uint4& hi) {
+  auto h = [](uint32_t w, int q) { return bf16_to_f32((uint16_t)(q ? (w >> 16) : (w & 0xffffu))); };
+  uint4 o;
+  o.x = pack_bf16x2(r.a.x - h(hi.x, 0), r.a.y - h(hi.x, 1));
+  o.y = pack_bf16x2(r.a.z - h(hi.y, 0), r.a.w - h(hi.y, 1));
+  o.z = pack_bf16x2(r.b.x - h(hi.z, 0), r.b.y - h(hi.z, 1));
+  o.w = pack_bf16x2(r.b.z - h(hi.w, 0), r.b.w - h(hi.w, 1));
+  return o;
+}
+__device__ inline uint4 lo_bf16x8(const Raw8<uint16_t>&, const uint4&) { return make_uint4(0, 0, 0, 0); }
+
 // Workgroup barrier that orders LDS only: global loads still in flight (the prefetched k-tiles)
 // are not drained, unlike __syncthreads(), whose fence waits for every outstanding memory access.
 __device__ __forceinline__ void lds_barrier() {
@@ -302,8 +314,11 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
 // LDS, tile kt+1 sits in registers and tile kt+2 is in flight from memory. The two register sets
 // alternate, so the k loop is unrolled by two to keep every register index static.
 template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, typename TIA, typename TIB,
-          typename TC>
+          typename TC, bool X3 = false>
 __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
+  // X3: fp32 operands split as x = hi + lo (both bf16); acc += hi*hi + hi*lo + lo*hi
+  static_assert(!X3 || (sizeof(TIA) == 4 && sizeof(TIB) == 4), "split-bf16 needs fp32 operands");
+  constexpr int NSPLIT = X3 ? 2 : 1;
   constexpr int NT = WGM * WGN * 64;
   constexpr int PAD = 8;
   constexpr int LDK = BK + PAD;             // LDS row pitch in bf16 elements
@@ -315,11 +330,15 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   static_assert(BK % 32 == 0 && SM >= 1 && SN >= 1, "tile shape");
 
   constexpr int LDC = BN + 4;  // fp32 C staging pitch
-  constexpr int PIPE_BYTES = 2 * (BM + BN) * LDK * 2;
+  constexpr int PIPE_BYTES = 2 * NSPLIT * (BM + BN) * LDK * 2;
   constexpr int C_BYTES = BM * LDC * 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
   uint16_t (*sA)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
   uint16_t (*sB)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
+  // low halves of the split operands (X3 only)
+  uint16_t (*sAl)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem + 2 * (BM + BN) * LDK * 2);
+  uint16_t (*sBl)[BN * LDK] =
+      reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * (BM + BN) * LDK * 2 + 2 * BM * LDK * 2);
   float* sC = reinterpret_cast<float*>(smem);
 
   const int tid = threadIdx.x;
@@ -373,43 +392,41 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
     }
   };
   // Register set -> LDS buffer `s` (transposing m/n-contiguous chunks).
+  auto put = [&](uint16_t* dst, int r, int k, uint4 v, bool trans) {
+    if (!trans) {
+      *reinterpret_cast<uint4*>(&dst[r * LDK + k]) = v;
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        dst[(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
+        dst[(r + 2 * q + 1) * LDK + k] = (uint16_t)(w[q] >> 16);
+      }
+    }
+  };
   auto sstore = [&](const Raw8<TIA> (&xa)[CA], const Raw8<TIB> (&xb)[CB], uint32_t ma, uint32_t mb,
                     int s) {
 #pragma unroll
     for (int c = 0; c < CA; c++) {
       const int id = tid + c * NT;
-      uint4 v = to_bf16x8(xa[c]);
-      if (!((ma >> c) & 1u)) v = make_uint4(0, 0, 0, 0);
-      if (!TA) {
-        const int r = id / (BK / 8), k = (id % (BK / 8)) * 8;
-        *reinterpret_cast<uint4*>(&sA[s][r * LDK + k]) = v;
-      } else {
-        const int k = id / (BM / 8), r = (id % (BM / 8)) * 8;
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          sA[s][(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
-          sA[s][(r + 2 * q + 1) * LDK + k] = (uint16_t)(w[q] >> 16);
-        }
-      }
+      const bool ok = (ma >> c) & 1u;
+      int r, k;
+      if (!TA) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
+      else { k = id / (BM / 8); r = (id % (BM / 8)) * 8; }
+      uint4 v = ok ? to_bf16x8(xa[c]) : make_uint4(0, 0, 0, 0);
+      put(sA[s], r, k, v, TA);
+      if constexpr (X3) put(sAl[s], r, k, ok ? lo_bf16x8(xa[c], v) : make_uint4(0, 0, 0, 0), TA);
     }
 #pragma unroll
     for (int c = 0; c < CB; c++) {
       const int id = tid + c * NT;
-      uint4 v = to_bf16x8(xb[c]);
-      if (!((mb >> c) & 1u)) v = make_uint4(0, 0, 0, 0);
-      if (TB) {
-        const int r = id / (BK / 8), k = (id % (BK / 8)) * 8;
-        *reinterpret_cast<uint4*>(&sB[s][r * LDK + k]) = v;
-      } else {
-        const int k = id / (BN / 8), r = (id % (BN / 8)) * 8;
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          sB[s][(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
-          sB[s][(r + 2 * q + 1) * LDK + k] = (uint16_t)(w[q] >> 16);
-        }
-      }
+      const bool ok = (mb >> c) & 1u;
+      int r, k;
+      if (TB) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
+      else { k = id / (BN / 8); r = (id % (BN / 8)) * 8; }
+      uint4 v = ok ? to_bf16x8(xb[c]) : make_uint4(0, 0, 0, 0);
+      put(sB[s], r, k, v, !TB);
+      if constexpr (X3) put(sBl[s], r, k, ok ? lo_bf16x8(xb[c], v) : make_uint4(0, 0, 0, 0), !TB);
     }
   };
 
@@ -424,6 +441,10 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   const int lr = lane & 31;         // row (A) / column (B) inside a 32x32 sub-tile
   const int lk = (lane >> 5) * 16;  // this lane's 16-wide k slice inside each 32-wide k block
 
+  auto mfma = [&](floatx16& c, const uint4& a, const uint4& b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  };
   auto compute = [&](int s) {
 #pragma unroll
     for (int kb = 0; kb < BK; kb += 32) {
@@ -445,15 +466,44 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < SM; i++)
 #pragma unroll
-        for (int j = 0; j < SN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, a0[i]), __builtin_bit_cast(bf16x8_t, b0[j]), acc[i][j], 0, 0, 0);
+        for (int j = 0; j < SN; j++) mfma(acc[i][j], a0[i], b0[j]);
 #pragma unroll
       for (int i = 0; i < SM; i++)
 #pragma unroll
-        for (int j = 0; j < SN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, a1[i]), __builtin_bit_cast(bf16x8_t, b1[j]), acc[i][j], 0, 0, 0);
+        for (int j = 0; j < SN; j++) mfma(acc[i][j], a1[i], b1[j]);
+      if constexpr (X3) {
+        uint4 l0[SM > SN ? SM : SN], l1[SM > SN ? SM : SN];
+        // hi(A) * lo(B)
+#pragma unroll
+        for (int j = 0; j < SN; j++) {
+          const uint16_t* p = &sBl[s][(wn0 + j * 32 + lr) * LDK + kb + lk];
+          l0[j] = *reinterpret_cast<const uint4*>(p);
+          l1[j] = *reinterpret_cast<const uint4*>(p + 8);
+        }
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+          for (int j = 0; j < SN; j++) { mfma(acc[i][j], a0[i], l0[j]); }
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+          for (int j = 0; j < SN; j++) { mfma(acc[i][j], a1[i], l1[j]); }
+        // lo(A) * hi(B)
+#pragma unroll
+        for (int i = 0; i < SM; i++) {
+          const uint16_t* p = &sAl[s][(wm0 + i * 32 + lr) * LDK + kb + lk];
+          l0[i] = *reinterpret_cast<const uint4*>(p);
+          l1[i] = *reinterpret_cast<const uint4*>(p + 8);
+        }
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+          for (int j = 0; j < SN; j++) { mfma(acc[i][j], l0[i], b0[j]); }
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+          for (int j = 0; j < SN; j++) { mfma(acc[i][j], l1[i], b1[j]); }
+      }
     }
   };
 
@@ -631,6 +681,20 @@ __global__ void k_splitk_reduce(GemmArgs g, int splits) {
 }
 
 // ------------------------------------------------------------------------------------------------
+template <int BM, int BN, int BK, bool TA, bool TB>
+void launch_x3(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  if (g.c_bf16) k_gemm_bf16<BM, BN, BK, 2, 2, TA, TB, float, float, uint16_t, true><<<grid, 256, 0, st>>>(g);
+  else k_gemm_bf16<BM, BN, BK, 2, 2, TA, TB, float, float, float, true><<<grid, 256, 0, st>>>(g);
+}
+
+template <int BM, int BN>
+void dispatch_x3(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t st) {
+  if (!ta && !tb) launch_x3<BM, BN, 32, false, false>(g, grid, st);
+  else if (!ta && tb) launch_x3<BM, BN, 32, false, true>(g, grid, st);
+  else if (ta && !tb) launch_x3<BM, BN, 32, true, false>(g, grid, st);
+  else launch_x3<BM, BN, 32, true, true>(g, grid, st);
+}
+
 template <int BM, int BN, int BK, bool TA, bool TB, typename TIA, typename TIB>
 void launch_bf16(const GemmArgs& g, dim3 grid, hipStream_t st) {
   if (g.c_bf16) k_gemm_bf16<BM, BN, BK, 2, 2, TA, TB, TIA, TIB, uint16_t><<<grid, 256, 0, st>>>(g);
@@ -716,8 +780,10 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   PH_REQUIRE(d.a_dtype == PH_F32 || d.a_dtype == PH_BF16, "gemm: A dtype must be F32 or BF16");
   PH_REQUIRE(d.b_dtype == PH_F32 || d.b_dtype == PH_BF16, "gemm: B dtype must be F32 or BF16");
   PH_REQUIRE(d.c_dtype == PH_F32 || d.c_dtype == PH_BF16, "gemm: C dtype must be F32 or BF16");
+  PH_REQUIRE(d.math == PH_MATH_BF16 || d.math == PH_MATH_F32 || d.math == PH_MATH_BF16X3,
+             "gemm: unknown math %d", d.math);
   PH_REQUIRE(d.math == PH_MATH_BF16 || (d.a_dtype == PH_F32 && d.b_dtype == PH_F32),
-             "gemm: fp32 math needs fp32 inputs");
+             "gemm: fp32 and split-bf16 math need fp32 inputs");
   PH_REQUIRE(d.epi == PH_EPI_NONE || d.epi == PH_EPI_BIAS || d.epi == PH_EPI_BIAS_RELU ||
                  d.epi == PH_EPI_RELU_MASK || d.epi == PH_EPI_AXPBY,
              "gemm: unknown epilogue %d", d.epi);
@@ -736,21 +802,27 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   // Vector-load preconditions of the MFMA kernels: every 8 (bf16 math) or 4 (fp32 math) consecutive
   // elements along each operand's contiguous dimension, and along K, start on a multiple of that
   // count. Shapes that miss them (e.g. a 4-wide observation layer) take the scalar kernel.
-  const int vec = d.math == PH_MATH_BF16 ? 8 : 4;
+  const int vec = d.math == PH_MATH_F32 ? 4 : 8;
   const long a_contig = d.trans_a ? d.M : d.K, b_contig = d.trans_b ? d.K : d.N;
   const bool aligned = a_contig % vec == 0 && d.lda % vec == 0 && b_contig % vec == 0 &&
                        d.ldb % vec == 0 && d.K % vec == 0 && ((uintptr_t)d.A % 16) == 0 &&
                        ((uintptr_t)d.B % 16) == 0;
   if (!aligned) return gemm_scalar(g, d, st);
 
-  // Tile choice: 128x128 when that gives >= 128 tiles; else 64x64 tiles when those reach 128;
-  // else 128x128 with split-K up to 256 blocks, keeping >= 256 of k per split.
+  // Tile choice: 128x128 when that gives >= 128 tiles. Otherwise, for long reductions (the wgrad
+  // forms, K = rows of the minibatch) 128x128 with split-K up to ~512 blocks, >= 2048 of k each;
+  // for short ones 64x64 tiles when those reach 128, else split-K with >= 256 of k each.
   int splits = d.splits > 0 ? d.splits : 1;
   const long tiles128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
   bool small = false;
   if (d.splits <= 0 && tiles128 < 128) {
-    if (tiles64 >= 128 || d.K < 512) {
+    if (d.K >= 4096) {
+      const long want = (512 + tiles128 - 1) / (tiles128 > 0 ? tiles128 : 1);
+      const long maxs = d.K / 2048;
+      splits = (int)(want < maxs ? want : maxs);
+      if (splits < 1) splits = 1;
+    } else if (tiles64 >= 128 || d.K < 512) {
       small = true;
     } else {
       const long want = 256 / (tiles128 > 0 ? tiles128 : 1);
@@ -775,6 +847,9 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   if (d.math == PH_MATH_BF16) {
     if (small) dispatch_bf16<64, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
     else dispatch_bf16<128, 128>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
+  } else if (d.math == PH_MATH_BF16X3) {
+    if (small) dispatch_x3<64, 64>(g, d.trans_a, d.trans_b, grid, st);
+    else dispatch_x3<128, 128>(g, d.trans_a, d.trans_b, grid, st);
   } else {
     if (small) dispatch_f32<64, 64, 32>(g, d.trans_a, d.trans_b, grid, st);
     else dispatch_f32<128, 128, 32>(g, d.trans_a, d.trans_b, grid, st);

@@ -15,6 +15,12 @@ enum : int {
   kSlotGemmWs = 6,
   kSlotGemmCounter = 7,
   kSlotNs = 8,        // 8..15 Newton-Schulz
+  kSlotMuonExact = 16,
+  kSlotMuonFastU = 17,
+  kSlotGclip = 18,
+  kSlotMgColsum = 19,
+  kSlotMgBufs = 20,
+  kSlotMgZero = 21,
   kSlotLean = 32,     // 32..95 host-buffer entry points
   kSlotMlp = 96,      // 96..127 resident MLP step
 };
@@ -51,9 +57,30 @@ int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, c
              float* dlogits, size_t ldd, float* dvalues, size_t lddv, float* newlp, float* newval,
              double* losses, hipStream_t st);
 
+int vtrace_f32(const float* rew, const float* val, const float* term, const float* rho,
+               const float* boot, size_t B, size_t T, int variant, int time_major, int rho_is_log,
+               int clamp, double gamma, double lam, double rhoClip, double cClip, float* adv,
+               float* tgt, hipStream_t st);
+int transpose_bf16(const uint16_t* X, uint16_t* Xt, int rows, int cols, hipStream_t st);
+int muon_mat_exact(int rows, int cols, const double* W, const double* G, const double* M, double* nW,
+                   double* nM, double gscale, double lr, double wd, double mu, double eps,
+                   const double* coeffs, int nsteps, hipStream_t st);
+int stepvec_exact(long n, const double* b, const double* g, const double* m, double* nb, double* nm,
+                  double gscale, double lr, double wd, double mu, hipStream_t st);
+int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
+                       int math, int slot_base, hipStream_t st);
+int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
+              float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
+              hipStream_t st);
+int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
+                hipStream_t st);
+int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);
+
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st);
 int colsum_f32(const float* X, size_t N, int J, size_t ld, float* out, float scale, int accumulate,
                hipStream_t st);
 int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st);
+
+long mingru_param_count(const ph_mingru_dims& d);
 
 }  // namespace ph

@@ -1,0 +1,467 @@
+// MinGRU policy PPO step (the reference's MinGRU trainer minibatch: V-trace -> advantage
+// normalisation -> batched BPTT gradient -> grad-norm clip -> Muon; puffercuda.cu:443-466, 5206-5622,
+// 5727-5976; CPU twin pufferffi.c:763-876).
+//
+// Layout (time-major, row r = t*B + b): obs [TB][D] fp32; activations bf16: x_l [TB][H] (layer
+// inputs; x_L is the head input), cmb_l [TB][3H] (layer pre-activations, rows hid|gate|proj),
+// o_l [TB][H] (recurrent state). One big MFMA GEMM per stage over all TB rows; the recurrence itself
+// is a per-(b,j) scan over t with the state in registers (B*H independent chains), the done mask
+// applied there (state reset after a terminal; no gradient across it).
+//
+// Parameters are fp32 master weights in the reference's flat order [wEnc(H*D) | bEnc(H) |
+// L x W(3H*H) | wDec(A*H) | bDec(A) | wVal(H) | bVal(1)] (puffercuda.cu:5212). The policy and value
+// heads run as one zero-padded head of HP = 32 rows (policy rows 0..A-1, value row A), so every
+// head GEMM has an aligned reduction; padded rows stay zero.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ph {
+namespace {
+
+constexpr int HP = 32;  // padded head rows
+constexpr unsigned kB = 256;
+
+__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ float gact(float x) { return x >= 0.f ? x + 0.5f : sigm(x); }
+__device__ __forceinline__ float ld(const uint16_t* p) { return bf16_to_f32(*p); }
+__device__ __forceinline__ float ld(const float* p) { return *p; }
+__device__ __forceinline__ void st(uint16_t* p, float v) { *p = bf16_rne(v); }
+__device__ __forceinline__ void st(float* p, float v) { *p = v; }
+
+// Forward scan of one layer. Thread = (b, j); o = (1-z)*prev + z*g(hid), h = hg*o + (1-hg)*hin.
+template <typename TS>
+__global__ void __launch_bounds__(256) k_scan_fwd(const TS* __restrict__ cmb, const TS* __restrict__ hin,
+                                                  TS* __restrict__ hout, TS* __restrict__ oS,
+                                                  const float* __restrict__ done, int B, int H, int T) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)B * H) return;
+  const int b = (int)(idx / H), j = (int)(idx % H);
+  const long BH = (long)B * H, B3H = (long)B * 3 * H;
+  float state = 0.f;
+  const TS* y = cmb + (long)b * 3 * H + j;
+  for (int t = 0; t < T; t++) {
+    const long s = (long)t * BH + idx;
+    const TS* yt = y + (long)t * B3H;
+    const float hid = ld(yt), gate = ld(yt + H), proj = ld(yt + 2 * H);
+    const float z = sigm(gate), g = gact(hid), hg = sigm(proj);
+    const float o = (1.f - z) * state + z * g;
+    const float hi = ld(hin + s);
+    st(hout + s, hg * o + (1.f - hg) * hi);
+    st(oS + s, o);
+    state = o;
+    if (done[(long)t * B + b] != 0.f) state = 0.f;
+  }
+}
+
+// Backward scan of one layer (adjoint of k_scan_fwd). dhn: gradient w.r.t. this layer's output;
+// writes dy = d(hid,gate,proj) pre-activation gradients and dhx = dhn*(1-hg) (the direct part of
+// the gradient w.r.t. the layer input; the GEMM dy.W adds the rest).
+template <typename TS>
+__global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, const TS* __restrict__ oS,
+                                                  const TS* __restrict__ hin, const TS* __restrict__ dhn,
+                                                  TS* __restrict__ dy, TS* __restrict__ dhx,
+                                                  const float* __restrict__ done, int B, int H, int T) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)B * H || T <= 0) return;
+  const int b = (int)(idx / H), j = (int)(idx % H);
+  const long BH = (long)B * H, B3H = (long)B * 3 * H;
+  float dOn = 0.f;
+  for (int t = T - 1; t >= 0; t--) {
+    const long s = (long)t * BH + idx;
+    const long yo = (long)t * B3H + (long)b * 3 * H + j;
+    const float hid = ld(cmb + yo), gate = ld(cmb + yo + H), proj = ld(cmb + yo + 2 * H);
+    const float o = ld(oS + s), hi = ld(hin + s), dh = ld(dhn + s);
+    const bool keep_prev = t > 0 && done[(long)(t - 1) * B + b] == 0.f;
+    const float prev = keep_prev ? ld(oS + s - BH) : 0.f;
+    const float z = sigm(gate), hg = sigm(proj), g = gact(hid);
+    const float dhg = dh * (o - hi);
+    const float dox = dh * hg + dOn;
+    st(dhx + s, dh * (1.f - hg));
+    const float dz = dox * (g - prev);
+    const float dprev = dox * (1.f - z);
+    const float dg = dox * z;
+    const float sg = hid >= 0.f ? 1.f : sigm(hid) * (1.f - sigm(hid));
+    st(dy + yo, dg * sg);
+    st(dy + yo + H, dz * z * (1.f - z));
+    st(dy + yo + 2 * H, dhg * hg * (1.f - hg));
+    dOn = keep_prev ? dprev : 0.f;
+  }
+}
+
+// bf16 copies of the weights for the GEMMs: WEnc [H][D]; W_l [3H][H] and W_l^T [H][3H];
+// the padded head Wh [HP][H] (rows: wDec, wVal, zeros), its transpose WhT [H][HP] and bias bh [HP].
+template <typename TW>
+__global__ void k_prep_weights(const float* __restrict__ p, int D, int H, int L, int A,
+                               TW* __restrict__ wenc, TW* __restrict__ wl, TW* __restrict__ wlt,
+                               TW* __restrict__ wh, TW* __restrict__ wht, float* __restrict__ bh) {
+  const long szE = (long)H * D, szL = 3L * H * H;
+  const long nL = (long)L * szL, nH = (long)HP * H;
+  const long total = szE + nL + nH + HP;
+  const long offW = szE + H, offDec = offW + nL, offBDec = offDec + (long)A * H, offVal = offBDec + A,
+             offBVal = offVal + H;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    if (i < szE) {
+      st(wenc + i, p[i]);
+    } else if (i < szE + nL) {
+      const long q = i - szE;
+      const long l = q / szL, r = q % szL;
+      const int row = (int)(r / H), col = (int)(r % H);  // W_l[row][col], row < 3H
+      const float v = p[offW + q];
+      st(wl + q, v);
+      st(wlt + l * szL + (long)col * 3 * H + row, v);
+    } else if (i < szE + nL + nH) {
+      const long q = i - szE - nL;
+      const int row = (int)(q / H), col = (int)(q % H);
+      float v = 0.f;
+      if (row < A) v = p[offDec + (long)row * H + col];
+      else if (row == A) v = p[offVal + col];
+      st(wh + q, v);
+      st(wht + (long)col * HP + row, v);
+    } else {
+      const int k = (int)(i - szE - nL - nH);
+      bh[k] = k < A ? p[offBDec + k] : (k == A ? p[offBVal] : 0.f);
+    }
+  }
+}
+
+// Head gradient scatter: gh [HP][H] and gbh [HP] into the flat gradient (wDec, bDec, wVal, bVal).
+__global__ void k_head_scatter(const float* __restrict__ gh, const float* __restrict__ gbh, int H, int A,
+                               float* __restrict__ gDec) {
+  // gDec points at wDec's gradient; bDec follows it, then wVal, then bVal
+  const long n = (long)(A + 1) * H + A + 1;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    if (i < (long)A * H) gDec[i] = gh[i];                                     // wDec rows
+    else if (i < (long)A * H + A) gDec[i] = gbh[i - (long)A * H];              // bDec
+    else if (i < (long)A * H + A + H) gDec[i] = gh[(long)A * H + (i - (long)A * H - A)];  // wVal
+    else gDec[i] = gbh[A];                                                      // bVal
+  }
+}
+
+// V-trace outputs -> the minibatch columns the loss reads: ret = adv + V (already the target),
+// advantage normalised with the minibatch mean/std (stats[0], stats[1] = std + 1e-8).
+__global__ void k_norm_adv(const float* __restrict__ adv, const float* __restrict__ stats, long n,
+                           float* __restrict__ advn) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) advn[i] = (adv[i] - stats[0]) / stats[1];
+}
+
+__global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y, long n) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = bf16_rne(x[i]);
+}
+
+// Column sums of a bf16 [N][J] matrix in fixed row chunks (partials [G][J] fp32)
+__global__ void __launch_bounds__(256) k_colsum_bf16_part(const uint16_t* __restrict__ X, long N, int J,
+                                                          long rows_per, float* __restrict__ part) {
+  __shared__ float sh[4][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int r0 = threadIdx.x >> 6;
+  const long lo = (long)blockIdx.y * rows_per;
+  const long hi = lo + rows_per < N ? lo + rows_per : N;
+  float acc = 0.f;
+  if (c < J)
+    for (long r = lo + r0; r < hi; r += 4) acc += bf16_to_f32(X[r * J + c]);
+  sh[r0][threadIdx.x & 63] = acc;
+  __syncthreads();
+  if (threadIdx.x < 64 && c < J)
+    part[(long)blockIdx.y * J + c] = ((sh[0][threadIdx.x] + sh[1][threadIdx.x]) + sh[2][threadIdx.x]) + sh[3][threadIdx.x];
+}
+
+__global__ void k_colsum_fin(const float* __restrict__ part, int G, int J, float* __restrict__ out) {
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= J) return;
+  float s = 0.f;
+  for (int g = 0; g < G; g++) s += part[(long)g * J + c];
+  out[c] = s;
+}
+
+int colsum_bf16(const uint16_t* X, long N, int J, float* out, hipStream_t st) {
+  long rows_per = 1024;
+  long G = (N + rows_per - 1) / rows_per;
+  if (G > 512) { G = 512; rows_per = (N + G - 1) / G; }
+  if (G < 1) G = 1;
+  float* part = (float*)scratch(kSlotMgColsum, (size_t)G * J * 4);
+  if (!part) return PH_ERR_NOMEM;
+  k_colsum_bf16_part<<<dim3(ceil_div(J, 64), (unsigned)G), 256, 0, st>>>(X, N, J, rows_per, part);
+  k_colsum_fin<<<ceil_div(J, 256), 256, 0, st>>>(part, (int)G, J, out);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+// Activation and weight-copy buffers hold bf16 (precision 0) or fp32 (precision 1) elements; they
+// are sized for fp32 so one allocation serves both tiers.
+struct Bufs {
+  void *obsb, *x, *cmb, *o, *dy, *dh0, *dh1;
+  void *wenc, *wl, *wlt, *wh, *wht;
+  float *bh, *logit, *dl, *gh, *gbh, *adv, *advn, *tgt, *newlp, *newval, *stats;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+__global__ void k_zero_u32(uint32_t* p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+int fill_zero(void* p, size_t bytes, hipStream_t st) {
+  const long n = (long)(bytes / 4);
+  k_zero_u32<<<1024, 256, 0, st>>>((uint32_t*)p, n);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+// Carves the step's device buffers from one library-owned allocation.
+int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
+  const long TB = (long)d.T * d.B, H = d.H, L = d.L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
+  const size_t es = d.precision == 1 ? 4 : 2;
+  const size_t o_obsb = take((size_t)TB * d.D * 2);
+  const size_t o_x = take((size_t)(L + 1) * TB * H * es);
+  const size_t o_cmb = take((size_t)L * TB * 3 * H * es);
+  const size_t o_o = take((size_t)L * TB * H * es);
+  const size_t o_dy = take((size_t)TB * 3 * H * es);
+  const size_t o_dh0 = take((size_t)TB * H * es);
+  const size_t o_dh1 = take((size_t)TB * H * es);
+  const size_t o_wenc = take((size_t)H * d.D * es);
+  const size_t o_wl = take((size_t)L * 3 * H * H * es);
+  const size_t o_wlt = take((size_t)L * 3 * H * H * es);
+  const size_t o_wh = take((size_t)HP * H * es);
+  const size_t o_wht = take((size_t)HP * H * es);
+  const size_t o_bh = take(HP * 4);
+  const size_t o_logit = take((size_t)TB * HP * 4);
+  const size_t o_dl = take((size_t)TB * HP * 4);
+  const size_t o_gh = take((size_t)HP * H * 4);
+  const size_t o_gbh = take(HP * 4);
+  const size_t o_adv = take((size_t)TB * 4);
+  const size_t o_advn = take((size_t)TB * 4);
+  const size_t o_tgt = take((size_t)TB * 4);
+  const size_t o_newlp = take((size_t)TB * 4);
+  const size_t o_newval = take((size_t)TB * 4);
+  const size_t o_stats = take(64);
+  uint8_t* base = (uint8_t*)scratch(kSlotMgBufs, off);
+  if (!base) return PH_ERR_NOMEM;
+  // The padded head columns of dl are never written by the loss kernel and must read as zero:
+  // cleared with a fill kernel whenever this region moves (first use or a new shape).
+  static void* zeroed_at[16] = {};
+  static size_t zeroed_len[16] = {};
+  int dev = 0;
+  PH_CHECK_HIP(hipGetDevice(&dev));
+  const size_t dl_bytes = (size_t)TB * HP * 4;
+  if (zeroed_at[dev & 15] != (void*)(base + o_dl) || zeroed_len[dev & 15] != dl_bytes) {
+    PH_TRY(fill_zero(base + o_dl, dl_bytes, st));
+    zeroed_at[dev & 15] = base + o_dl;
+    zeroed_len[dev & 15] = dl_bytes;
+  }
+  b.obsb = base + o_obsb; b.x = base + o_x; b.cmb = base + o_cmb; b.o = base + o_o; b.dy = base + o_dy;
+  b.dh0 = base + o_dh0; b.dh1 = base + o_dh1; b.wenc = base + o_wenc; b.wl = base + o_wl;
+  b.wlt = base + o_wlt; b.wh = base + o_wh; b.wht = base + o_wht;
+  b.bh = (float*)(base + o_bh); b.logit = (float*)(base + o_logit); b.dl = (float*)(base + o_dl);
+  b.gh = (float*)(base + o_gh); b.gbh = (float*)(base + o_gbh); b.adv = (float*)(base + o_adv);
+  b.advn = (float*)(base + o_advn); b.tgt = (float*)(base + o_tgt); b.newlp = (float*)(base + o_newlp);
+  b.newval = (float*)(base + o_newval); b.stats = (float*)(base + o_stats);
+  return PH_OK;
+}
+
+PhGemmDesc gd(int ta, int tb, int M, int N, int K, int adt, const void* A, long lda, int bdt,
+              const void* B, long ldb, int cdt, void* C, long ldc, int math) {
+  PhGemmDesc d{};
+  d.trans_a = ta; d.trans_b = tb; d.M = M; d.N = N; d.K = K;
+  d.a_dtype = adt; d.A = A; d.lda = lda; d.b_dtype = bdt; d.B = B; d.ldb = ldb;
+  d.c_dtype = cdt; d.C = C; d.ldc = ldc; d.math = math; d.alpha = 1.f;
+  return d;
+}
+
+// Forward + backward over one minibatch: writes the summed gradient G[P] and new_logp/new_value.
+// TS: activation / weight-copy storage (uint16_t = bf16 with bf16 MFMA, float = fp32 MFMA).
+template <typename TS>
+int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float* params,
+                      const float* obs, const int* act, const float* advn, const float* ret,
+                      const float* oldlp, const float* oldval, const float* done, float* G,
+                      float* newlp, float* newval, double* losses, hipStream_t st) {
+  constexpr bool BF = sizeof(TS) == 2;
+  constexpr int DT = BF ? PH_BF16 : PH_F32;
+  constexpr int MATH = BF ? PH_MATH_BF16 : PH_MATH_F32;
+  const long TB = (long)d.T * d.B;
+  const int H = d.H, D = d.D, L = d.L, A = d.A;
+  Bufs b;
+  PH_TRY(get_bufs(d, b, st));
+  TS* x = (TS*)b.x;
+  TS* cmbs = (TS*)b.cmb;
+  TS* os = (TS*)b.o;
+  TS* dy = (TS*)b.dy;
+  TS* wl = (TS*)b.wl;
+  TS* wlt = (TS*)b.wlt;
+  const long szE = (long)H * D, szL = 3L * H * H;
+  const long offBEnc = szE, offW = szE + H, offDec = offW + (long)L * szL;
+
+  // GEMM copies of the weights (and bf16 observations)
+  k_prep_weights<TS><<<1024, kB, 0, st>>>(params, D, H, L, A, (TS*)b.wenc, wl, wlt, (TS*)b.wh,
+                                          (TS*)b.wht, b.bh);
+  const void* obsg = obs;
+  if (BF) {
+    k_f32_to_bf16_k<<<ceil_div(TB * D, kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D);
+    obsg = b.obsb;
+  }
+  PH_LAUNCH_CHECK();
+
+  // encoder: x0 = obs W_enc^T + b_enc
+  {
+    PhGemmDesc g = gd(0, 1, (int)TB, H, D, DT, obsg, D, DT, b.wenc, D, DT, x, H, MATH);
+    g.epi = PH_EPI_BIAS; g.bias = params + offBEnc;
+    PH_TRY(gemm(g, st));
+  }
+  // layers
+  for (int l = 0; l < L; l++) {
+    TS* xl = x + (long)l * TB * H;
+    TS* cmb = cmbs + (long)l * TB * 3 * H;
+    PhGemmDesc g = gd(0, 1, (int)TB, 3 * H, H, DT, xl, H, DT, wl + l * szL, H, DT, cmb, 3 * H, MATH);
+    PH_TRY(gemm(g, st));
+    k_scan_fwd<TS><<<ceil_div((long)d.B * H, kB), kB, 0, st>>>(cmb, xl, xl + TB * H, os + (long)l * TB * H,
+                                                             done, d.B, H, d.T);
+    PH_LAUNCH_CHECK();
+  }
+  TS* xL = x + (long)L * TB * H;
+  // heads: logits|value = x_L Wh^T + bh  ([TB][HP] fp32)
+  {
+    PhGemmDesc g = gd(0, 1, (int)TB, HP, H, DT, xL, H, DT, b.wh, H, PH_F32, b.logit, HP, MATH);
+    g.epi = PH_EPI_BIAS; g.bias = b.bh;
+    PH_TRY(gemm(g, st));
+  }
+  // fused PPO loss: dlogits into dl[:, :A], dvalue into dl[:, A]
+  PH_TRY(ppo_grad(b.logit, HP, b.logit + A, HP, act, advn, ret, oldlp, oldval, TB, A, c.vf_coef,
+                  c.ent_coef, c.clip_eps, c.vf_clip, 1, b.dl, HP, b.dl + A, HP, newlp, newval, losses, st));
+  // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh
+  {
+    PhGemmDesc g = gd(1, 0, HP, H, (int)TB, PH_F32, b.dl, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
+    PH_TRY(gemm(g, st));
+    PH_TRY(colsum_f32(b.dl, TB, HP, HP, b.gbh, 1.f, 0, st));
+    k_head_scatter<<<64, kB, 0, st>>>(b.gh, b.gbh, H, A, G + offDec);
+    PH_LAUNCH_CHECK();
+    PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, PH_F32, b.dl, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
+    PH_TRY(gemm(g2, st));
+  }
+  // layers backward
+  TS* dhn = (TS*)b.dh0;
+  TS* dhx = (TS*)b.dh1;
+  for (int l = L - 1; l >= 0; l--) {
+    TS* xl = x + (long)l * TB * H;
+    TS* cmb = cmbs + (long)l * TB * 3 * H;
+    k_scan_bwd<TS><<<ceil_div((long)d.B * H, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn, dy,
+                                                             dhx, done, d.B, H, d.T);
+    PH_LAUNCH_CHECK();
+    // gW_l = dy^T x_l  -> G
+    PhGemmDesc g = gd(1, 0, 3 * H, H, (int)TB, DT, dy, 3 * H, DT, xl, H, PH_F32,
+                      G + offW + (long)l * szL, H, MATH);
+    PH_TRY(gemm(g, st));
+    // dh_in = dhx + dy W_l   (W_l^T stored [H][3H])
+    PhGemmDesc g2 = gd(0, 1, (int)TB, H, 3 * H, DT, dy, 3 * H, DT, wlt + l * szL, 3 * H, DT, dhx, H, MATH);
+    g2.epi = PH_EPI_AXPBY; g2.alpha = 1.f; g2.beta = 1.f; g2.aux = dhx; g2.ldaux = H;
+    PH_TRY(gemm(g2, st));
+    TS* t = dhn; dhn = dhx; dhx = t;
+  }
+  // encoder backward: gbEnc = colsum(dh), gWEnc = dh^T obs
+  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, G + offBEnc, st));
+  else PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
+  {
+    PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, D, PH_F32, G, D, MATH);
+    PH_TRY(gemm(g, st));
+  }
+  return PH_OK;
+}
+
+}  // namespace
+
+long mingru_param_count(const ph_mingru_dims& d) {
+  return (long)d.H * d.D + d.H + (long)d.L * 3 * d.H * d.H + (long)d.A * d.H + d.A + d.H + 1;
+}
+
+int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float* params,
+                    const float* obs, const int* act, const float* advn, const float* ret,
+                    const float* oldlp, const float* oldval, const float* done, float* G,
+                    float* newlp, float* newval, double* losses, hipStream_t st) {
+  PH_REQUIRE(d.B > 0 && d.T > 0 && d.D > 0 && d.H > 0 && d.L > 0 && d.A > 0, "mingru: empty dims");
+  PH_REQUIRE(d.A + 1 <= HP, "mingru: at most %d actions", HP - 1);
+  PH_REQUIRE(d.H % 8 == 0 && d.D % 8 == 0, "mingru: hidden and obs sizes must be multiples of 8");
+  PH_REQUIRE(d.precision == 0 || d.precision == 1, "mingru: precision must be 0 (bf16) or 1 (fp32)");
+  PH_REQUIRE((long)d.T * d.B <= INT32_MAX, "mingru: T*B exceeds int32");
+  if (d.precision == 1)
+    return mingru_ppo_grad_t<float>(d, c, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
+                                    newval, losses, st);
+  return mingru_ppo_grad_t<uint16_t>(d, c, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
+                                     newval, losses, st);
+}
+
+// Clip the summed gradient and apply Muon to every matrix (fp32 master weights), stepvec to biases.
+int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, float* mom, float* G,
+                hipStream_t st) {
+  const int H = d.H, D = d.D, L = d.L, A = d.A;
+  const long P = mingru_param_count(d);
+  PH_TRY(gclip_f32(G, P, m.gscale, m.max_grad_norm, st));
+  const long szE = (long)H * D, szL = 3L * H * H;
+  const long offBEnc = szE, offW = szE + H, offDec = offW + (long)L * szL, offBDec = offDec + (long)A * H,
+             offVal = offBDec + A, offBVal = offVal + H;
+  auto mat = [&](long off, int rows, int cols) {
+    return muon_fast(params + off, G + off, mom + off, rows, cols, 1.f, m.lr, m.wd, m.mu, m.eps,
+                     m.coeffs, m.nsteps, m.math, st);
+  };
+  auto vec = [&](long off, long n) {
+    return stepvec_f32(params + off, G + off, mom + off, n, 1.f, m.lr, m.wd, m.mu, st);
+  };
+  PH_TRY(mat(0, H, D));
+  PH_TRY(vec(offBEnc, H));
+  for (int l = 0; l < L; l++) PH_TRY(mat(offW + l * szL, 3 * H, H));
+  PH_TRY(mat(offDec, A, H));
+  PH_TRY(vec(offBDec, A));
+  PH_TRY(mat(offVal, 1, H));
+  PH_TRY(vec(offBVal, 1));
+  return PH_OK;
+}
+
+int mingru_step(const ph_mingru_dims& d, const ph_ppo_coefs& c, const ph_muon_coefs& m,
+                float* params, float* mom, const float* obs, const int* act, const float* oldlp,
+                const float* oldval, const float* rew, const float* done, const float* logrho,
+                const float* boot, float* G, double* losses, hipStream_t st) {
+  const long TB = (long)d.T * d.B;
+  Bufs b;
+  PH_TRY(get_bufs(d, b, st));
+  // V-trace (bootstrapped variant, time-major) on the behaviour values; targets = adv + V
+  PH_TRY(vtrace_f32(rew, oldval, done, logrho, boot, d.B, d.T, 1, 1, logrho != nullptr, 1, c.gamma,
+                    c.lam, c.rho_clip, c.c_clip, b.adv, b.tgt, st));
+  // minibatch advantage normalisation
+  PH_TRY(moments_normalize(PH_F32, b.adv, TB, b.advn, b.stats, st));
+  PH_TRY(mingru_ppo_grad(d, c, params, obs, act, b.advn, b.tgt, oldlp, oldval, done, G, b.newlp,
+                         b.newval, losses, st));
+  PH_TRY(mingru_muon(d, m, params, mom, G, st));
+  return PH_OK;
+}
+
+}  // namespace ph
+
+using namespace ph;
+
+extern "C" long ph_mingru_param_count(const ph_mingru_dims* d) { return d ? mingru_param_count(*d) : -1; }
+
+extern "C" int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c, const float* params,
+                                  const float* obs, const int* act, const float* adv, const float* ret,
+                                  const float* oldlp, const float* oldval, const float* done, float* G,
+                                  float* newlp, float* newval, double* losses, void* stream) {
+  PH_REQUIRE(d && c, "ph_mingru_ppo_grad: null config");
+  return mingru_ppo_grad(*d, *c, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval,
+                         losses, as_stream(stream));
+}
+
+extern "C" int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params,
+                              float* mom, float* G, void* stream) {
+  PH_REQUIRE(d && m, "ph_mingru_muon: null config");
+  return mingru_muon(*d, *m, params, mom, G, as_stream(stream));
+}
+
+extern "C" int ph_mingru_step(const ph_mingru_dims* d, const ph_ppo_coefs* c, const ph_muon_coefs* m,
+                              float* params, float* mom, const float* obs, const int* act,
+                              const float* oldlp, const float* oldval, const float* rew,
+                              const float* done, const float* logrho, const float* boot, float* G,
+                              double* losses, void* stream) {
+  PH_REQUIRE(d && c && m, "ph_mingru_step: null config");
+  return mingru_step(*d, *c, *m, params, mom, obs, act, oldlp, oldval, rew, done, logrho, boot, G,
+                     losses, as_stream(stream));
+}

@@ -1,0 +1,408 @@
+// Muon optimizer step: Nesterov momentum -> Newton-Schulz orthogonalisation -> decoupled weight
+// decay (ascent form), plus the bias step and the global grad-norm clip.
+//
+// Two tiers:
+//  * exact (f64): naive matmuls that sum over the shared index in ascending order, the two-level
+//    Frobenius fold (rows in parallel, then rows summed in order by one lane) and contraction
+//    disabled, so every value matches the reference CPU step (pufferblas.c:1369-1406) bit for bit.
+//  * fast: the quintic iterate on MFMA GEMMs (bf16 or fp32 math, fp32 state), wide form
+//    X <- aX + (bA + cA^2)X with A = XX^T; A and A^2 are symmetric, so A^2 = A A^T is computed by
+//    the same NT kernel as XX^T, and the b/c/a combinations are fused into the GEMM epilogues.
+//    Tall matrices are transposed to wide on the way in and back on the way out.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ph {
+namespace {
+
+// ---- exact tier ---------------------------------------------------------------------------------
+__global__ void k_nesterov_f64(const double* __restrict__ G, const double* __restrict__ M,
+                               double* __restrict__ nM, double* __restrict__ U, long n, double gscale,
+                               double mu) {
+#pragma clang fp contract(off)
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double gi = G[i] * gscale;
+  const double m = mu * M[i] + gi;
+  nM[i] = m;
+  U[i] = gi + mu * m;
+}
+
+// per-row sum of squares, ascending column order
+__global__ void k_rowsq_f64(const double* __restrict__ U, double* __restrict__ rs, int rows, int cols) {
+#pragma clang fp contract(off)
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const double* u = U + (long)r * cols;
+  double s = 0.0;
+  for (int j = 0; j < cols; j++) {
+    const double v = u[j];
+    s = s + v * v;
+  }
+  rs[r] = s;
+}
+
+// rows summed in order by one lane; inv = 1/(sqrt(s)+eps)
+__global__ void k_frob_inv_f64(const double* __restrict__ rs, int rows, double eps, double* __restrict__ inv) {
+#pragma clang fp contract(off)
+  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+  double s = 0.0;
+  for (int r = 0; r < rows; r++) s = s + rs[r];
+  inv[0] = 1.0 / (sqrt(s) + eps);
+}
+
+__global__ void k_scale_f64(const double* __restrict__ U, const double* __restrict__ inv,
+                            double* __restrict__ X, long n) {
+#pragma clang fp contract(off)
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) X[i] = inv[0] * U[i];
+}
+
+__global__ void k_transpose_f64(const double* __restrict__ X, double* __restrict__ Xt, int rows, int cols) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * cols) return;
+  int i = (int)(idx / cols), j = (int)(idx % cols);
+  Xt[(long)j * rows + i] = X[idx];
+}
+
+// C[m x n] = A[m x k] B[k x n], one lane per output, ascending l, no contraction
+__global__ void k_matmul_f64(const double* __restrict__ A, const double* __restrict__ B,
+                             double* __restrict__ C, int m, int k, int n) {
+#pragma clang fp contract(off)
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)m * n) return;
+  int i = (int)(idx / n), j = (int)(idx % n);
+  double t = 0.0;
+  for (int l = 0; l < k; l++) t = t + A[(long)i * k + l] * B[(long)l * n + j];
+  C[idx] = t;
+}
+
+__global__ void k_lincomb3_f64(double* __restrict__ X, double a, const double* __restrict__ P, double b,
+                               const double* __restrict__ Q, double c, long n) {
+#pragma clang fp contract(off)
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) X[i] = a * X[i] + b * P[i] + c * Q[i];
+}
+
+__global__ void k_finalize_f64(const double* __restrict__ W, const double* __restrict__ X,
+                               double* __restrict__ nW, double c1, double c2, long n) {
+#pragma clang fp contract(off)
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) nW[i] = c1 * W[i] + c2 * X[i];
+}
+
+__global__ void k_stepvec_f64(const double* __restrict__ b, const double* __restrict__ g,
+                              const double* __restrict__ m, double* __restrict__ nb,
+                              double* __restrict__ nm, long n, double gscale, double lr, double wd,
+                              double mu) {
+#pragma clang fp contract(off)
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double gi = g[i] * gscale;
+  const double newm = mu * m[i] + gi;
+  const double upd = gi + mu * newm;
+  nb[i] = b[i] * (1.0 - lr * wd) + lr * upd;
+  nm[i] = newm;
+}
+
+// ---- fast tier helpers --------------------------------------------------------------------------
+// sum of squares of an fp32 matrix into part[blockIdx.x] (fixed chunks), then a one-block fold
+__global__ void __launch_bounds__(256) k_sumsq_part(const float* __restrict__ x, long n, long chunk,
+                                                    float* __restrict__ part) {
+  __shared__ float sh[256];
+  const long lo = (long)blockIdx.x * chunk, hi = lo + chunk < n ? lo + chunk : n;
+  float s = 0.f;
+  for (long i = lo + threadIdx.x; i < hi; i += 256) s += x[i] * x[i];
+  sh[threadIdx.x] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if ((int)threadIdx.x < st) sh[threadIdx.x] += sh[threadIdx.x + st];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
+}
+
+__global__ void k_norm_inv(const float* __restrict__ part, int G, float eps, float* __restrict__ inv) {
+  __shared__ float sh[256];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < G; i += 256) s += part[i];
+  sh[threadIdx.x] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if ((int)threadIdx.x < st) sh[threadIdx.x] += sh[threadIdx.x + st];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) inv[0] = 1.f / (sqrtf(sh[0]) + eps);
+}
+
+// Load the normalised iterate in wide form: Xf (fp32, m x w), Xb (bf16, m x w), Xt (bf16, w x m).
+// src is rows x cols; tall (rows > cols) sources are transposed.
+__global__ void k_ns_load(const float* __restrict__ src, int rows, int cols, const float* __restrict__ inv,
+                          float* __restrict__ Xf, uint16_t* __restrict__ Xb, uint16_t* __restrict__ Xt) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * cols) return;
+  const int i = (int)(idx / cols), j = (int)(idx % cols);
+  const bool tall = rows > cols;
+  const int m = tall ? cols : rows, w = tall ? rows : cols;
+  const int wi = tall ? j : i, wj = tall ? i : j;  // wide coordinates
+  const float v = inv[0] * src[idx];
+  Xf[(long)wi * w + wj] = v;
+  const uint16_t b = bf16_rne(v);
+  Xb[(long)wi * w + wj] = b;
+  Xt[(long)wj * m + wi] = b;
+}
+
+__global__ void k_ns_load_f32(const float* __restrict__ src, int rows, int cols,
+                              const float* __restrict__ inv, float* __restrict__ Xf) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * cols) return;
+  const int i = (int)(idx / cols), j = (int)(idx % cols);
+  const bool tall = rows > cols;
+  const int w = tall ? rows : cols;
+  const int wi = tall ? j : i, wj = tall ? i : j;
+  Xf[(long)wi * w + wj] = inv[0] * src[idx];
+}
+
+__global__ void k_ns_store(const float* __restrict__ Xf, int rows, int cols, float* __restrict__ dst) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * cols) return;
+  const int i = (int)(idx / cols), j = (int)(idx % cols);
+  const bool tall = rows > cols;
+  const int w = tall ? rows : cols;
+  const int wi = tall ? j : i, wj = tall ? i : j;
+  dst[idx] = Xf[(long)wi * w + wj];
+}
+
+// Nesterov on fp32 state: nM = mu*M + g*gscale; U = g*gscale + mu*nM
+__global__ void k_nesterov_f32(const float* __restrict__ G, float* __restrict__ M, float* __restrict__ U,
+                               long n, float gscale, float mu) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gi = G[i] * gscale;
+  const float m = mu * M[i] + gi;
+  M[i] = m;
+  U[i] = gi + mu * m;
+}
+
+__global__ void k_finalize_f32(float* __restrict__ W, const float* __restrict__ X, long n, float c1, float c2) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) W[i] = c1 * W[i] + c2 * X[i];
+}
+
+__global__ void k_stepvec_f32(float* __restrict__ b, const float* __restrict__ g, float* __restrict__ m,
+                              long n, float gscale, float lr, float wd, float mu) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gi = g[i] * gscale;
+  const float newm = mu * m[i] + gi;
+  const float upd = gi + mu * newm;
+  b[i] = b[i] * (1.f - lr * wd) + lr * upd;
+  m[i] = newm;
+}
+
+// Global grad-norm clip over a flat fp32 gradient: sumsq in fixed-chunk partials, then scale.
+__global__ void k_gclip_scale(float* __restrict__ g, long n, const float* __restrict__ part, int G,
+                              float sc, float maxNorm) {
+  __shared__ float tot;
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int i = 0; i < G; i++) s += part[i];
+    tot = s;
+  }
+  __syncthreads();
+  const float gn = sqrtf(tot) * fabsf(sc);
+  const float cc = ((maxNorm > 0.f && gn > maxNorm) ? maxNorm / gn : 1.f) * sc;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    g[i] = g[i] * cc;
+}
+
+constexpr unsigned kB = 256;
+
+}  // namespace
+
+// ---- exact tier host driver: one matrix, device f64 buffers ------------------------------------
+int muon_mat_exact(int rows, int cols, const double* W, const double* G, const double* M, double* nW,
+                   double* nM, double gscale, double lr, double wd, double mu, double eps,
+                   const double* coeffs, int nsteps, hipStream_t st) {
+  const long n = (long)rows * cols;
+  if (n == 0) return PH_OK;
+  const int mn = rows < cols ? rows : cols;
+  double* ws = (double*)scratch(kSlotMuonExact, (size_t)(6 * n + (long)mn * mn + rows + 8) * 8);
+  if (!ws) return PH_ERR_NOMEM;
+  double *U = ws, *X = U + n, *Xt = X + n, *P = Xt + n, *Q = P + n, *A = Q + n, *rs = A + (long)mn * mn,
+         *inv = rs + rows;
+  const unsigned gN = ceil_div(n, kB);
+  k_nesterov_f64<<<gN, kB, 0, st>>>(G, M, nM, U, n, gscale, mu);
+  k_rowsq_f64<<<ceil_div(rows, kB), kB, 0, st>>>(U, rs, rows, cols);
+  k_frob_inv_f64<<<1, 1, 0, st>>>(rs, rows, eps, inv);
+  k_scale_f64<<<gN, kB, 0, st>>>(U, inv, X, n);
+  for (int it = 0; it < nsteps; it++) {
+    const double a = coeffs[3 * it], b = coeffs[3 * it + 1], c = coeffs[3 * it + 2];
+    k_transpose_f64<<<gN, kB, 0, st>>>(X, Xt, rows, cols);
+    if (rows <= cols) {
+      k_matmul_f64<<<ceil_div((long)rows * rows, kB), kB, 0, st>>>(X, Xt, A, rows, cols, rows);
+      k_matmul_f64<<<gN, kB, 0, st>>>(A, X, P, rows, rows, cols);
+      k_matmul_f64<<<gN, kB, 0, st>>>(A, P, Q, rows, rows, cols);
+    } else {
+      k_matmul_f64<<<ceil_div((long)cols * cols, kB), kB, 0, st>>>(Xt, X, A, cols, rows, cols);
+      k_matmul_f64<<<gN, kB, 0, st>>>(X, A, P, rows, cols, cols);
+      k_matmul_f64<<<gN, kB, 0, st>>>(P, A, Q, rows, cols, cols);
+    }
+    k_lincomb3_f64<<<gN, kB, 0, st>>>(X, a, P, b, Q, c, n);
+  }
+  const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
+  k_finalize_f64<<<gN, kB, 0, st>>>(W, X, nW, 1.0 - lr * wd, lr * scale, n);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int stepvec_exact(long n, const double* b, const double* g, const double* m, double* nb, double* nm,
+                  double gscale, double lr, double wd, double mu, hipStream_t st) {
+  if (n == 0) return PH_OK;
+  k_stepvec_f64<<<ceil_div(n, kB), kB, 0, st>>>(b, g, m, nb, nm, n, gscale, lr, wd, mu);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+// ---- fast tier: in-place NS of one fp32 matrix --------------------------------------------------
+// Per step, all operands read straight from fp32 buffers:
+//   A  = X X^T                 (bf16 MFMA; math == PH_MATH_F32: fp32 MFMA)
+//   B  = b A + c A A^T         (split-bf16 MFMA, epilogue b*A + c*acc)
+//   X' = a X + B X             (split-bf16 MFMA, epilogue a*X + acc, into the other X buffer)
+// The split products keep the quintic within 1e-2 of the f64 iterate, which plain bf16 operands for
+// A^2 and BX do not (about 2% at 512 x 1024 with the constant coefficients).
+int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
+                       int math, int slot_base, hipStream_t st) {
+  const long n = (long)rows * cols;
+  if (n == 0) return PH_OK;
+  const int m = rows < cols ? rows : cols, w = rows < cols ? cols : rows;
+  const long mm = (long)m * m;
+  const long chunk = 4096;
+  const int G = (int)((n + chunk - 1) / chunk);
+  if (G > 4000) {
+    set_error("newton_schulz: matrix too large (%ld elements)", n);
+    return PH_ERR_UNSUPPORTED;
+  }
+  const size_t bytes = (size_t)(2 * n + 2 * mm) * 4 + 4096 * 4 + 256;
+  float* ws = (float*)scratch(slot_base, bytes);
+  if (!ws) return PH_ERR_NOMEM;
+  float* Xs[2] = {ws, ws + n};
+  float* Af = ws + 2 * n;
+  float* Bf = Af + mm;
+  float* part = Bf + mm;
+  float* inv = part + 4000;
+  k_sumsq_part<<<G, 256, 0, st>>>(X, n, chunk, part);
+  k_norm_inv<<<1, 256, 0, st>>>(part, G, eps, inv);
+  k_ns_load_f32<<<ceil_div(n, kB), kB, 0, st>>>(X, rows, cols, inv, Xs[0]);
+  PH_LAUNCH_CHECK();
+  const int m1 = math == PH_MATH_F32 ? PH_MATH_F32 : PH_MATH_BF16;
+  const int m23 = math == PH_MATH_F32 ? PH_MATH_F32 : PH_MATH_BF16X3;
+  for (int it = 0; it < nsteps; it++) {
+    const float a = coeffs[3 * it], b = coeffs[3 * it + 1], c = coeffs[3 * it + 2];
+    float* Xi = Xs[it & 1];
+    float* Xo = Xs[(it + 1) & 1];
+    PhGemmDesc d{};
+    d.trans_a = 0; d.trans_b = 1; d.M = m; d.N = m; d.K = w;
+    d.a_dtype = PH_F32; d.A = Xi; d.lda = w; d.b_dtype = PH_F32; d.B = Xi; d.ldb = w;
+    d.c_dtype = PH_F32; d.C = Af; d.ldc = m; d.math = m1; d.epi = PH_EPI_NONE; d.alpha = 1.f;
+    PH_TRY(gemm(d, st));
+    d = PhGemmDesc{};
+    d.trans_a = 0; d.trans_b = 1; d.M = m; d.N = m; d.K = m;
+    d.a_dtype = PH_F32; d.A = Af; d.lda = m; d.b_dtype = PH_F32; d.B = Af; d.ldb = m;
+    d.c_dtype = PH_F32; d.C = Bf; d.ldc = m; d.math = m23;
+    d.epi = PH_EPI_AXPBY; d.alpha = c; d.beta = b; d.aux = Af; d.ldaux = m;
+    PH_TRY(gemm(d, st));
+    d = PhGemmDesc{};
+    d.trans_a = 0; d.trans_b = 0; d.M = m; d.N = w; d.K = m;
+    d.a_dtype = PH_F32; d.A = Bf; d.lda = m; d.b_dtype = PH_F32; d.B = Xi; d.ldb = w;
+    d.c_dtype = PH_F32; d.C = Xo; d.ldc = w; d.math = m23;
+    d.epi = PH_EPI_AXPBY; d.alpha = 1.f; d.beta = a; d.aux = Xi; d.ldaux = w;
+    PH_TRY(gemm(d, st));
+  }
+  k_ns_store<<<ceil_div(n, kB), kB, 0, st>>>(Xs[nsteps & 1], rows, cols, X);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
+              float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
+              hipStream_t st) {
+  const long n = (long)rows * cols;
+  if (n == 0) return PH_OK;
+  float* U = (float*)scratch(kSlotMuonFastU, (size_t)n * 4);
+  if (!U) return PH_ERR_NOMEM;
+  k_nesterov_f32<<<ceil_div(n, kB), kB, 0, st>>>(G, M, U, n, gscale, mu);
+  PH_LAUNCH_CHECK();
+  PH_TRY(newton_schulz_fast(U, rows, cols, coeffs, nsteps, eps, math, kSlotNs, st));
+  const float scale = sqrtf(fmaxf(1.f, (float)rows / (float)cols));
+  k_finalize_f32<<<ceil_div(n, kB), kB, 0, st>>>(W, U, n, 1.f - lr * wd, lr * scale);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
+                hipStream_t st) {
+  if (n == 0) return PH_OK;
+  k_stepvec_f32<<<ceil_div(n, kB), kB, 0, st>>>(b, g, m, n, gscale, lr, wd, mu);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st) {
+  if (n == 0) return PH_OK;
+  const long chunk = 8192;
+  const int G = (int)((n + chunk - 1) / chunk);
+  float* part = (float*)scratch(kSlotGclip, (size_t)G * 4);
+  if (!part) return PH_ERR_NOMEM;
+  k_sumsq_part<<<G, 256, 0, st>>>(g, n, chunk, part);
+  unsigned grid = ceil_div(n, 256);
+  if (grid > 2048) grid = 2048;
+  k_gclip_scale<<<grid, 256, 0, st>>>(g, n, part, G, sc, maxNorm);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+}  // namespace ph
+
+using namespace ph;
+
+extern "C" int ph_muon_mat_f64(int rows, int cols, const double* W, const double* G, const double* M,
+                               double* nW, double* nM, double gscale, double lr, double wd, double mu,
+                               double eps, const double* coeffs, int nsteps, void* stream) {
+  PH_REQUIRE(rows >= 0 && cols >= 0 && nsteps >= 0 && nsteps <= 64, "ph_muon_mat_f64: bad shape");
+  PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_muon_mat_f64: coefficient table missing");
+  return muon_mat_exact(rows, cols, W, G, M, nW, nM, gscale, lr, wd, mu, eps, coeffs, nsteps,
+                        as_stream(stream));
+}
+
+extern "C" int ph_stepvec_f64(size_t n, const double* b, const double* g, const double* m, double* nb,
+                              double* nm, double gscale, double lr, double wd, double mu, void* stream) {
+  return stepvec_exact((long)n, b, g, m, nb, nm, gscale, lr, wd, mu, as_stream(stream));
+}
+
+extern "C" int ph_newton_schulz(float* X, int rows, int cols, const float* coeffs, int nsteps,
+                                float eps, int math, void* stream) {
+  PH_REQUIRE(rows >= 0 && cols >= 0 && nsteps >= 0 && nsteps <= 64, "ph_newton_schulz: bad shape");
+  PH_REQUIRE(math == PH_MATH_BF16 || math == PH_MATH_F32 || math == PH_MATH_BF16X3,
+             "ph_newton_schulz: unknown math");
+  PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_newton_schulz: coefficient table missing");
+  return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, as_stream(stream));
+}
+
+extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale,
+                           float lr, float wd, float mu, float eps, const float* coeffs, int nsteps,
+                           int math, void* stream) {
+  PH_REQUIRE(rows >= 0 && cols >= 0 && nsteps >= 0 && nsteps <= 64, "ph_muon_mat: bad shape");
+  PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_muon_mat: coefficient table missing");
+  return muon_fast(W, G, M, rows, cols, gscale, lr, wd, mu, eps, coeffs, nsteps, math,
+                   as_stream(stream));
+}
+
+extern "C" int ph_stepvec(float* b, const float* g, float* m, size_t n, float gscale, float lr,
+                          float wd, float mu, void* stream) {
+  return stepvec_f32(b, g, m, (long)n, gscale, lr, wd, mu, as_stream(stream));
+}
+
+extern "C" int ph_gclip(float* g, size_t n, float sc, float maxNorm, void* stream) {
+  return gclip_f32(g, (long)n, sc, maxNorm, as_stream(stream));
+}

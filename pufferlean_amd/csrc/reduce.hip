@@ -113,7 +113,32 @@ __global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict_
   if (i < n) y[i] = bf16_rne(x[i]);
 }
 
+// 32x32 tiles through LDS (+1 column of padding against bank conflicts)
+__global__ void k_transpose_u16(const uint16_t* __restrict__ X, uint16_t* __restrict__ Xt, int rows,
+                                int cols) {
+  __shared__ uint16_t t[32][33];
+  const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows per pass
+  for (int r = ty; r < 32; r += 8) {
+    const int i = by + r, j = bx + tx;
+    if (i < rows && j < cols) t[r][tx] = X[(long)i * cols + j];
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int j = bx + r, i = by + tx;
+    if (i < rows && j < cols) Xt[(long)j * rows + i] = t[tx][r];
+  }
+}
+
 }  // namespace
+
+int transpose_bf16(const uint16_t* X, uint16_t* Xt, int rows, int cols, hipStream_t st) {
+  if (rows == 0 || cols == 0) return PH_OK;
+  dim3 grid(ceil_div(cols, 32), ceil_div(rows, 32));
+  k_transpose_u16<<<grid, 256, 0, st>>>(X, Xt, rows, cols);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
 
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st) {
   if (n == 0) return PH_OK;

@@ -10,6 +10,7 @@
 // kernel is bit-identical to the reference CPU scans (puffercuda.cu:120-132, 200-211) and the f32
 // kernel is bit-identical to an f32 evaluation of the same expressions.
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace ph {
 namespace {
@@ -120,6 +121,15 @@ int launch_vtrace(const R* rew, const R* val, const R* term, const R* rho, const
 }
 
 }  // namespace
+
+int vtrace_f32(const float* rew, const float* val, const float* term, const float* rho,
+               const float* boot, size_t B, size_t T, int variant, int time_major, int rho_is_log,
+               int clamp, double gamma, double lam, double rhoClip, double cClip, float* adv,
+               float* tgt, hipStream_t st) {
+  return launch_vtrace<float>(rew, val, term, rho, boot, B, T, variant, time_major, rho_is_log, clamp,
+                              gamma, lam, rhoClip, cClip, adv, tgt, st);
+}
+
 }  // namespace ph
 
 using namespace ph;

@@ -9,6 +9,7 @@ import ctypes as C
 import torch
 
 from . import _lib as L
+from . import _lib as _L
 
 _DT = {torch.float32: L.PH_F32, torch.float64: L.PH_F64, torch.bfloat16: L.PH_BF16,
        torch.int32: L.PH_I32}
@@ -110,3 +111,121 @@ def gemm(a, b, *, trans_a=False, trans_b=False, out=None, out_dtype=torch.float3
            _p(bias), _p(aux), aux.stride(0) if aux is not None else 0, alpha, beta, _p(out2),
            out2.stride(0) if out2 is not None else 0, int(out2_trans), splits, _stream())
     return out
+
+
+REF_COEFFS = [(4.0848, -6.8946, 2.9270), (3.9505, -6.3029, 2.6377), (3.7418, -5.5913, 2.3037),
+              (2.8769, -3.1427, 1.2046), (2.8366, -3.0525, 1.2012)]
+CONST_COEFFS = [(3.4445, -4.7750, 2.0315)] * 5
+
+
+def _coeffs(coeffs, dtype):
+    import numpy as np
+    c = np.ascontiguousarray(np.asarray(coeffs, dtype=dtype).reshape(-1, 3))
+    return c, c.ctypes.data_as(C.c_void_p), c.shape[0]
+
+
+def muon_mat_f64(W, G, M, *, gscale=1.0, lr=0.1, wd=0.0, mu=0.95, eps=1e-7, coeffs=REF_COEFFS,
+                 out_w=None, out_m=None):
+    """Exact-tier Muon matrix step on f64 device tensors; returns (newW, newM)."""
+    _dev(W, G, M)
+    rows, cols = W.shape
+    nW = out_w if out_w is not None else torch.empty_like(W)
+    nM = out_m if out_m is not None else torch.empty_like(M)
+    c, cp, ns = _coeffs(coeffs, "float64")
+    L.call("ph_muon_mat_f64", rows, cols, _p(W), _p(G), _p(M), _p(nW), _p(nM), gscale, lr, wd, mu,
+           eps, cp, ns, _stream())
+    return nW, nM
+
+
+def stepvec_f64(b, g, m, *, gscale=1.0, lr=0.1, wd=0.0, mu=0.95):
+    _dev(b, g, m)
+    nb, nm = torch.empty_like(b), torch.empty_like(m)
+    L.call("ph_stepvec_f64", b.numel(), _p(b), _p(g), _p(m), _p(nb), _p(nm), gscale, lr, wd, mu,
+           _stream())
+    return nb, nm
+
+
+def newton_schulz(X, *, coeffs=CONST_COEFFS, eps=1e-7, math="bf16"):
+    """In-place fast-tier NS of an fp32 matrix; returns X."""
+    _dev(X)
+    if X.dtype != torch.float32 or not X.is_contiguous():
+        raise TypeError("newton_schulz needs a contiguous fp32 matrix")
+    c, cp, ns = _coeffs(coeffs, "float32")
+    m = L.PH_MATH_BF16 if math == "bf16" else L.PH_MATH_F32
+    L.call("ph_newton_schulz", _p(X), X.shape[0], X.shape[1], cp, ns, eps, m, _stream())
+    return X
+
+
+def muon_mat(W, G, M, *, gscale=1.0, lr=0.015, wd=0.0, mu=0.95, eps=1e-7, coeffs=CONST_COEFFS,
+             math="bf16"):
+    """In-place fast-tier Muon matrix step on fp32 W and momentum M."""
+    _dev(W, G, M)
+    c, cp, ns = _coeffs(coeffs, "float32")
+    m = L.PH_MATH_BF16 if math == "bf16" else L.PH_MATH_F32
+    L.call("ph_muon_mat", _p(W), _p(G), _p(M), W.shape[0], W.shape[1], gscale, lr, wd, mu, eps, cp,
+           ns, m, _stream())
+    return W, M
+
+
+def stepvec(b, g, m, *, gscale=1.0, lr=0.015, wd=0.0, mu=0.95):
+    _dev(b, g, m)
+    L.call("ph_stepvec", _p(b), _p(g), _p(m), b.numel(), gscale, lr, wd, mu, _stream())
+    return b, m
+
+
+def gclip(g, *, scale=1.0, max_norm=0.0):
+    _dev(g)
+    L.call("ph_gclip", _p(g), g.numel(), scale, max_norm, _stream())
+    return g
+
+
+# ---- MinGRU policy PPO+Muon step ----------------------------------------------------------------
+
+class MinGRUConfig:
+    """Dimensions and coefficients of the MinGRU PPO+Muon minibatch step (time-major columns)."""
+
+    def __init__(self, B, T, D, H, L, A, *, gamma=0.99, lam=0.95, rho_clip=1.0, c_clip=1.0,
+                 clip_eps=0.2, vf_coef=0.5, ent_coef=0.01, vf_clip=0.0, lr=0.015, wd=0.0, mu=0.95,
+                 eps=1e-7, max_grad_norm=0.0, gscale=1.0, coeffs=CONST_COEFFS, math="bf16",
+                 precision="bf16"):
+        import numpy as np
+        self.dims = _L.MinGRUDims(B, T, D, H, L, A, {"bf16": 0, "f32": 1}[precision])
+        self.ppo = _L.PPOCoefs(gamma, lam, rho_clip, c_clip, clip_eps, vf_coef, ent_coef, vf_clip)
+        self._coeffs = np.ascontiguousarray(np.asarray(coeffs, dtype=np.float32).reshape(-1, 3))
+        m = {"bf16": _L.PH_MATH_BF16, "f32": _L.PH_MATH_F32}[math]
+        self.muon = _L.MuonCoefs(lr, wd, mu, eps, max_grad_norm, gscale, self._coeffs.shape[0], m,
+                                self._coeffs.ctypes.data_as(C.c_void_p))
+
+    @property
+    def P(self):
+        return int(_L.lib().ph_mingru_param_count(C.byref(self.dims)))
+
+
+def mingru_ppo_grad(cfg, params, obs, act, adv, ret, oldlp, oldval, done, G=None, newlp=None,
+                    newval=None, losses=None):
+    _dev(params, obs, act, adv, ret, oldlp, oldval, done)
+    TB = cfg.dims.T * cfg.dims.B
+    G = G if G is not None else torch.zeros(cfg.P, device=params.device)
+    newlp = newlp if newlp is not None else torch.empty(TB, device=params.device)
+    newval = newval if newval is not None else torch.empty(TB, device=params.device)
+    L.call("ph_mingru_ppo_grad", C.byref(cfg.dims), C.byref(cfg.ppo), _p(params), _p(obs), _p(act),
+           _p(adv), _p(ret), _p(oldlp), _p(oldval), _p(done), _p(G), _p(newlp), _p(newval),
+           _p(losses), _stream())
+    return G, newlp, newval
+
+
+def mingru_muon(cfg, params, mom, G):
+    _dev(params, mom, G)
+    L.call("ph_mingru_muon", C.byref(cfg.dims), C.byref(cfg.muon), _p(params), _p(mom), _p(G),
+           _stream())
+    return params, mom
+
+
+def mingru_step(cfg, params, mom, obs, act, oldlp, oldval, rew, done, logrho, boot, G=None,
+                losses=None):
+    _dev(params, mom, obs, act, oldlp, oldval, rew, done, logrho, boot)
+    G = G if G is not None else torch.zeros(cfg.P, device=params.device)
+    L.call("ph_mingru_step", C.byref(cfg.dims), C.byref(cfg.ppo), C.byref(cfg.muon), _p(params),
+           _p(mom), _p(obs), _p(act), _p(oldlp), _p(oldval), _p(rew), _p(done), _p(logrho),
+           _p(boot), _p(G), _p(losses), _stream())
+    return params, mom, G

@@ -1,0 +1,106 @@
+"""Muon / Newton-Schulz on the GPU vs the CPU oracle.
+
+Exact tier: bit-exact with the reference-order f64 oracle (the reference's verify-muon-gpu shapes).
+Fast tier: bf16 MFMA within 1e-2 relative Frobenius of the f64 oracle (and of the fp32-MFMA tier);
+fp32 MFMA within 1e-4 of the f64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from pufferlean_amd import device as D
+from pufferlean_amd import rng
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("shape", [(16, 24), (24, 16), (20, 20), (128, 128), (6, 128)])
+def test_exact_tier_bit_exact(gpu, shape):
+    # verify-muon-gpu draw order: per element w U[-.5,.5), g U[-.3,.3), m U[-.2,.2) (Exe/Puffer.lean:1134-1138)
+    rows, cols = shape
+    n = rows * cols
+    w = rng.uniform01(rng.words(0x3E7A + rows * 7 + cols, 3 * n)).reshape(n, 3)
+    W = -0.5 + (0.5 - -0.5) * w[:, 0]
+    G = -0.3 + (0.3 - -0.3) * w[:, 1]
+    M = -0.2 + (0.2 - -0.2) * w[:, 2]
+    lr, wd, mu, eps = 0.1, 0.01, 0.95, 1e-7
+    nW = np.zeros(n); nM = np.zeros(n)
+    c = O.coeffs_array(O.REF_COEFFS)
+    O.lib().orc_muon_mat(rows, cols, O.P(W), O.P(G), O.P(M), O.P(nW), O.P(nM), 1.0, lr, wd, mu, eps,
+                         O.P(c), 5, 0)
+    t = lambda x: torch.from_numpy(x.reshape(rows, cols)).cuda()
+    gW, gM = D.muon_mat_f64(t(W), t(G), t(M), lr=lr, wd=wd, mu=mu, eps=eps)
+    assert np.array_equal(gM.cpu().numpy().ravel(), nM)
+    got = gW.cpu().numpy().ravel()
+    assert np.array_equal(got, nW), f"max|d| {np.abs(got - nW).max()}"
+
+
+def test_stepvec_bit_exact(gpu):
+    n = 300
+    b, g, m = rng.normal(1, n), rng.normal(2, n), rng.normal(3, n)
+    nb = np.zeros(n); nm = np.zeros(n)
+    O.lib().orc_stepvec(n, O.P(b), O.P(g), O.P(m), O.P(nb), O.P(nm), 0.25, 0.1, 0.01, 0.95)
+    t = lambda x: torch.from_numpy(x).cuda()
+    gb, gm = D.stepvec_f64(t(b), t(g), t(m), gscale=0.25, lr=0.1, wd=0.01, mu=0.95)
+    assert np.array_equal(gb.cpu().numpy(), nb) and np.array_equal(gm.cpu().numpy(), nm)
+
+
+CONFIG3 = [(512, 512)] * 4 + [(512, 1024), (1024, 512)]
+
+
+@pytest.mark.parametrize("shape", CONFIG3[3:] + [(128, 128), (96, 200), (200, 96)])
+@pytest.mark.parametrize("coeffs", ["const", "ref"])
+def test_fast_ns_vs_oracle(gpu, shape, coeffs):
+    rows, cols = shape
+    X0 = rng.normal(0x300 + rows + cols, rows * cols, 0.0, 0.02).reshape(rows, cols).astype(np.float32)
+    cf = O.BASELINE_COEFFS if coeffs == "const" else O.REF_COEFFS
+    ref = O.newton_schulz(X0.astype(np.float64), cf, 1e-7, form=1)
+    xb = torch.from_numpy(X0).cuda()
+    D.newton_schulz(xb, coeffs=cf, math="bf16")
+    xf = torch.from_numpy(X0).cuda()
+    D.newton_schulz(xf, coeffs=cf, math="f32")
+    gb, gf = xb.cpu().numpy(), xf.cpu().numpy()
+    assert rel(gf, ref) < 1e-4
+    assert rel(gb, ref) < 1e-2
+    assert rel(gb, gf.astype(np.float64)) < 1e-2
+
+
+def test_fast_ns_orthogonalises(gpu):
+    # size-independent property at the full config-3 size: singular values pushed into the
+    # quintic's fixed band (the constant-coefficient schedule leaves them in about [0.68, 1.2])
+    X0 = rng.normal(0x301, 512 * 1024, 0.0, 0.02).reshape(512, 1024).astype(np.float32)
+    x = torch.from_numpy(X0).cuda()
+    D.newton_schulz(x, coeffs=O.BASELINE_COEFFS, math="bf16")
+    s = np.linalg.svd(x.cpu().numpy().astype(np.float64), compute_uv=False)
+    assert s.min() > 0.5 and s.max() < 1.3
+
+
+def test_fast_muon_step_vs_oracle(gpu):
+    rows, cols = 128, 128
+    W = rng.normal(0x310, rows * cols, 0, 0.1).reshape(rows, cols).astype(np.float32)
+    G = rng.normal(0x311, rows * cols).reshape(rows, cols).astype(np.float32)
+    M = rng.normal(0x312, rows * cols, 0, 0.1).reshape(rows, cols).astype(np.float32)
+    nW = np.zeros(rows * cols); nM = np.zeros(rows * cols)
+    c = O.coeffs_array(O.BASELINE_COEFFS)
+    O.lib().orc_muon_mat(rows, cols, O.P(O.f64(W)), O.P(O.f64(G)), O.P(O.f64(M)), O.P(nW), O.P(nM),
+                         1 / 64, 0.015, 0.0, 0.95, 1e-7, O.P(c), 5, 1)
+    gW, gM = torch.from_numpy(W).cuda(), torch.from_numpy(M).cuda()
+    D.muon_mat(gW, torch.from_numpy(G).cuda(), gM, gscale=1 / 64, lr=0.015, wd=0.0, mu=0.95,
+               coeffs=O.BASELINE_COEFFS, math="bf16")
+    assert rel(gM.cpu().numpy().ravel(), nM) < 1e-6
+    dW = gW.cpu().numpy().ravel() - W.ravel()
+    assert rel(dW, nW - W.ravel().astype(np.float64)) < 1e-2
+
+
+def test_gclip(gpu):
+    g = rng.normal(0x320, 100000).astype(np.float32)
+    ref = g.astype(np.float64).copy()
+    O.lib().orc_gclip(O.P(ref), ref.size, 0.5, 10.0)
+    t = torch.from_numpy(g).cuda()
+    D.gclip(t, scale=0.5, max_norm=10.0)
+    assert rel(t.cpu().numpy(), ref) < 1e-6
