@@ -1,21 +1,26 @@
 """Benchmark of the pufferlean training-step hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu-baseline] [--eager]
 
-Prints ONE JSON line. Workloads (synthetic, seeded, inputs resident in HBM before timing):
-  gemm    policy GEMMs M=16384 (256 segments x 64 steps), K=N=512: forward X.W^T, dgrad dY.W,
-          wgrad dY^T.X, bf16 MFMA with fp32 accumulate (fp32 storage in, fp32 out)
-  vtrace  V-trace reverse scan, fp32 time-major, 4096 segments x horizon 64, replicated 64x in
-          one launch so the working set (403 MB) exceeds the 256 MB Infinity Cache
-A "step" is one pass of the workload's hot path over one batch. Timed with HIP events on the
-stream the kernels run on.
+Prints ONE JSON line. The headline workload (value) is the full PPO+Muon minibatch step of a
+2-layer MinGRU policy at hidden 512: obs 128 -> encoder 512 -> 2 MinGRU layers of 512 -> 16-way
+categorical head + value head, 4096 segments x horizon 64 (262,144 rows), V-trace -> advantage
+normalisation -> forward -> clipped PPO loss (clip 0.2, vf 0.5, ent 0.01) -> backward -> grad-norm
+clip -> Muon (5 constant-coefficient Newton-Schulz steps) on every matrix, bias steps on biases.
+fp32 master weights, bf16 activations and bf16 MFMA GEMMs. A "step" is one such minibatch update,
+captured once into a HIP graph and replayed (--eager: launched directly).
+
+Components, each on its own synthetic seeded inputs already resident in HBM:
+  gemm    policy GEMMs M=16384, K=N=512 in the three forms (forward X.W^T, dgrad dY.W, wgrad dY^T.X)
+  ns      Newton-Schulz batch: 4 x (512x512) + 2 x (512x1024), 5 steps, constant coefficients
+  vtrace  V-trace, fp32 time-major, 4096 segments x 64, replicated 64x in one launch (403 MB)
+Kernel times are HIP-event times on the stream the kernels run on.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -27,8 +32,11 @@ BF16_PEAK_TFLOPS = 2516.6
 F32_PEAK_TFLOPS = 157.3
 METRIC = "PPO update samples/sec @ hidden 512 (1 GPU); GEMM/NS MFMA util %; V-trace GB/s"
 
+# the headline workload
+B5, T5, D5, H5, L5, A5 = 4096, 64, 128, 512, 2, 16
 
-def _events():
+
+def _ev():
     import torch
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -39,7 +47,7 @@ def time_loop(fn, steps, warmup):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    s, e = _events()
+    s, e = _ev()
     s.record()
     for _ in range(steps):
         fn()
@@ -48,7 +56,103 @@ def time_loop(fn, steps, warmup):
     return s.elapsed_time(e) / steps
 
 
+def _t(x, dtype=None):
+    import numpy as np
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, dtype or np.float32)).cuda()
+
+
 # ------------------------------------------------------------------------------------------------
+def mingru_inputs(B, T, D, H, L, A, seed_base=5):
+    """Seeded synthetic minibatch of the headline workload (time-major columns)."""
+    import numpy as np
+    from pufferlean_amd import rng
+    s = lambda k: rng.seed_for(seed_base, k)
+    n = B * T
+    parts = [rng.normal(s(0), H * D) / np.sqrt(D), np.zeros(H)]
+    for l in range(L):
+        parts.append(rng.normal(s(1 + l), 3 * H * H) / np.sqrt(H))
+    parts += [rng.normal(s(8), A * H) / np.sqrt(H), np.zeros(A), rng.normal(s(9), H) / np.sqrt(H),
+              np.zeros(1)]
+    params = np.concatenate(parts)
+    cols = dict(
+        obs=rng.normal(s(10), n * D),
+        act=rng.randint(s(11), n, A).astype(np.int32),
+        rew=rng.normal(s(12), n),
+        done=rng.bernoulli(s(13), n, 0.01),
+        logrho=rng.normal(s(14), n, 0.0, 0.1),
+        val=rng.normal(s(15), n),
+        boot=rng.normal(s(16), B),
+        # behaviour log-probs of the (near-uniform) initial policy, perturbed
+        old=np.log(1.0 / A) + rng.normal(s(17), n, 0.0, 0.05),
+    )
+    return params, cols
+
+
+def bench_ppo_step(steps, warmup, eager=False):
+    import numpy as np
+    import torch
+    from pufferlean_amd import device as D
+
+    cfg = D.MinGRUConfig(B5, T5, D5, H5, L5, A5, lr=0.015, mu=0.95, max_grad_norm=0.5,
+                         gscale=1.0 / (B5 * T5), vf_clip=0.0)
+    params, cols = mingru_inputs(B5, T5, D5, H5, L5, A5)
+    p = _t(params)
+    mom = torch.zeros_like(p)
+    g = torch.zeros_like(p)
+    obs = _t(cols["obs"]).view(T5, B5, D5)
+    act = _t(cols["act"], np.int32).view(T5, B5)
+    old, val, rew, done, logrho = (_t(cols[k]).view(T5, B5) for k in ("old", "val", "rew", "done", "logrho"))
+    boot = _t(cols["boot"])
+    losses = torch.zeros(7, device="cuda", dtype=torch.float64)
+
+    def step():
+        D.mingru_step(cfg, p, mom, obs, act, old, val, rew, done, logrho, boot, G=g, losses=losses)
+
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    graph = None
+    if not eager:
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        run = graph.replay
+    else:
+        run = step
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = _ev()
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    finite = bool(torch.isfinite(p).all().item())
+    rows = B5 * T5
+    out = {"ms": round(ms, 4), "samples_per_s": round(rows / (ms * 1e-3), 1), "rows": rows,
+           "params": cfg.P, "graph": graph is not None, "finite": finite,
+           "losses": [round(float(x), 5) for x in losses.cpu().tolist()]}
+    # dominant kernel: the layer-forward GEMM (x_l W_l^T, 262144 x 1536 x 512, bf16 in/out)
+    x = torch.randn(rows, H5, device="cuda").bfloat16()
+    w = (torch.randn(3 * H5, H5, device="cuda") / 22.6).bfloat16()
+    y = torch.empty(rows, 3 * H5, device="cuda", dtype=torch.bfloat16)
+    gms = time_loop(lambda: D.gemm(x, w, trans_b=True, out=y), 10, 3)
+    flops = 2.0 * rows * 3 * H5 * H5
+    tf = flops / (gms * 1e-3) / 1e12
+    out["dominant_kernel"] = {"name": "k_gemm_bf16 (layer forward 262144x1536x512)", "us": round(gms * 1e3, 1),
+                              "tflops": round(tf, 1), "flops": flops,
+                              "hbm_bytes": 2.0 * (rows * H5 + rows * 3 * H5 + 3 * H5 * H5)}
+    return out
+
+
 def bench_gemm(steps, warmup):
     import numpy as np
     import torch
@@ -56,31 +160,52 @@ def bench_gemm(steps, warmup):
     from pufferlean_amd import rng
 
     M, K, N = 16384, 512, 512
-    X = torch.from_numpy(rng.normal(rng.seed_for(2, 0), M * K).astype(np.float32)).cuda().view(M, K)
-    W = torch.from_numpy((rng.normal(rng.seed_for(2, 1), N * K) / np.sqrt(512)).astype(np.float32)).cuda().view(N, K)
-    dY = torch.from_numpy(rng.normal(rng.seed_for(2, 2), M * N).astype(np.float32)).cuda().view(M, N)
+    X = _t(rng.normal(rng.seed_for(2, 0), M * K)).view(M, K)
+    W = _t(rng.normal(rng.seed_for(2, 1), N * K) / np.sqrt(512)).view(N, K)
+    dY = _t(rng.normal(rng.seed_for(2, 2), M * N)).view(M, N)
     Xb, Wb, dYb = X.bfloat16(), W.bfloat16(), dY.bfloat16()
     Y = torch.empty(M, N, device="cuda")
     Yb = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
     dX = torch.empty(M, K, device="cuda")
+    dXb = torch.empty(M, K, device="cuda", dtype=torch.bfloat16)
     dW = torch.empty(N, K, device="cuda")
     flops = 2.0 * M * N * K
-    out = {}
     forms = {
-        "nn_fwd_f32io": lambda: D.gemm(X, W, trans_b=True, out=Y),
-        "nt_dgrad_f32io": lambda: D.gemm(dY, W, out=dX),
-        "tn_wgrad_f32io": lambda: D.gemm(dY, X, trans_a=True, out=dW),
-        "nn_fwd_bf16io": lambda: D.gemm(Xb, Wb, trans_b=True, out=Yb),
-        "nt_dgrad_bf16in": lambda: D.gemm(dYb, Wb, out=dX),
-        "tn_wgrad_bf16in": lambda: D.gemm(dYb, Xb, trans_a=True, out=dW),
-        "nn_fwd_f32math": lambda: D.gemm(X, W, trans_b=True, out=Y, math="f32"),
+        "fwd_bf16": (lambda: D.gemm(Xb, Wb, trans_b=True, out=Yb), BF16_PEAK_TFLOPS),
+        "dgrad_bf16": (lambda: D.gemm(dYb, Wb, out=dXb), BF16_PEAK_TFLOPS),
+        "wgrad_bf16": (lambda: D.gemm(dYb, Xb, trans_a=True, out=dW), BF16_PEAK_TFLOPS),
+        "fwd_f32io_bf16math": (lambda: D.gemm(X, W, trans_b=True, out=Y), BF16_PEAK_TFLOPS),
+        "dgrad_f32io_bf16math": (lambda: D.gemm(dY, W, out=dX), BF16_PEAK_TFLOPS),
+        "wgrad_f32io_bf16math": (lambda: D.gemm(dY, X, trans_a=True, out=dW), BF16_PEAK_TFLOPS),
+        "fwd_f32math": (lambda: D.gemm(X, W, trans_b=True, out=Y, math="f32"), F32_PEAK_TFLOPS),
     }
-    for name, fn in forms.items():
+    out = {}
+    for name, (fn, peak) in forms.items():
         ms = time_loop(fn, steps, warmup)
-        peak = F32_PEAK_TFLOPS if name.endswith("f32math") else BF16_PEAK_TFLOPS
         tf = flops / (ms * 1e-3) / 1e12
         out[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / peak, 4)}
     return out
+
+
+def bench_ns(steps, warmup):
+    import numpy as np
+    import torch
+    from pufferlean_amd import device as D
+    from pufferlean_amd import rng
+
+    shapes = [(512, 512)] * 4 + [(512, 1024)] * 2
+    mats = [_t(rng.normal(rng.seed_for(3, i), r * c, 0.0, 0.02)).view(r, c) for i, (r, c) in enumerate(shapes)]
+    work = [m.clone() for m in mats]
+
+    def run():
+        for w in work:
+            D.newton_schulz(w, coeffs=D.CONST_COEFFS, math="bf16")
+
+    ms = time_loop(run, max(steps // 5, 3), warmup)
+    flops = sum(5 * (4 * min(r, c) ** 2 * max(r, c) + 2 * min(r, c) ** 3) for r, c in shapes)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            "flops": flops, "matrices": len(shapes)}
 
 
 def bench_vtrace(steps, warmup):
@@ -91,15 +216,11 @@ def bench_vtrace(steps, warmup):
 
     B, T, R = 4096, 64, 64
     n = B * T
-    cols = []
-    for i in range(4):
-        base = [rng.normal(rng.seed_for(4, 1), n), rng.normal(rng.seed_for(4, 2), n),
-                rng.bernoulli(rng.seed_for(4, 3), n, 0.01),
-                rng.normal(rng.seed_for(4, 4), n, 0.0, 0.1)][i]
-        t = torch.from_numpy(base.astype(np.float32)).cuda().view(T, B)
-        cols.append(t.repeat(1, R).contiguous())
+    base = [rng.normal(rng.seed_for(4, 1), n), rng.normal(rng.seed_for(4, 2), n),
+            rng.bernoulli(rng.seed_for(4, 3), n, 0.01), rng.normal(rng.seed_for(4, 4), n, 0.0, 0.1)]
+    cols = [_t(x).view(T, B).repeat(1, R).contiguous() for x in base]
     val, rew, done, logr = cols
-    boot = torch.from_numpy(rng.normal(rng.seed_for(4, 5), B).astype(np.float32)).cuda().repeat(R).contiguous()
+    boot = _t(rng.normal(rng.seed_for(4, 5), B)).repeat(R).contiguous()
     adv = torch.empty_like(val)
     tgt = torch.empty_like(val)
     fn = lambda: D.vtrace(rew, val, done, logr, boot, variant=1, time_major=True, rho_is_log=True,
@@ -107,77 +228,98 @@ def bench_vtrace(steps, warmup):
     ms = time_loop(fn, steps, warmup)
     bytes_ = 24.0 * n * R + 4.0 * B * R
     gbs = bytes_ / (ms * 1e-3) / 1e9
-    # single (non-replicated) call latency
     v1, r1, d1, l1 = (c[:, :B].contiguous() for c in cols)
     b1 = boot[:B].contiguous()
-    ms1 = time_loop(lambda: D.vtrace(r1, v1, d1, l1, b1, variant=1, time_major=True,
-                                     rho_is_log=True), steps, warmup)
+    a1, t1 = torch.empty_like(v1), torch.empty_like(v1)
+    ms1 = time_loop(lambda: D.vtrace(r1, v1, d1, l1, b1, variant=1, time_major=True, rho_is_log=True,
+                                     out_adv=a1, out_tgt=t1), steps, warmup)
     return {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "bytes": bytes_, "single_call_us": round(ms1 * 1e3, 2)}
 
 
 # ------------------------------------------------------------------------------------------------
-def cpu_baseline_gemm():
-    """The oracle's OpenMP f64 GEMM (forward form) on a 2048-row sample of the 16384x512x512 forward."""
+def cpu_baseline_ppo(budget_s=15.0):
+    """The oracle's single-sequence MinGRU PPO gradient (f64, one thread, the reference CPU path's
+    algorithm) over sampled segments of the headline workload; samples/s = rows / second."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
-    from pufferlean_amd import rng
-    cores = os.cpu_count() or 1
-    cores = min(cores, 16)
-    rows, K, N = 2048, 512, 512
-    X = rng.normal(1, rows * K).reshape(rows, K)
-    W = rng.normal(2, N * K).reshape(N, K)
+    params, cols = mingru_inputs(B5, T5, D5, H5, L5, A5)
+    P = params.size
+    obs = cols["obs"].reshape(T5, B5, D5)
+    seg_cols = {k: cols[k].reshape(T5, B5) for k in ("act", "rew", "val", "old", "done")}
     t0 = time.perf_counter()
-    reps = 0
-    while True:
-        O.gemm(0, 1, X, W, rows, N, K, threads=cores)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    return {"value": round(2.0 * rows * N * K / dt / 1e9, 2), "unit": "GFLOP/s (f64)", "cores": cores,
-            "kind": "port", "sample": f"forward GEMM {rows}x{K}x{N} (of 16384 rows), {reps} reps"}
+    done_segs = 0
+    out = np.zeros(P + 2 * T5)
+    while time.perf_counter() - t0 < budget_s and done_segs < B5:
+        b = done_segs
+        f = lambda k: O.f64(seg_cols[k][:, b])
+        O.lib().orc_mingru_ppo_grad_seq(O.P(params), O.P(O.f64(obs[:, b, :])), O.P(f("act")),
+                                        O.P(f("rew")), O.P(f("val")), O.P(f("old")), O.P(f("done")),
+                                        O.P(f("val")), T5, H5, D5, L5, A5, 0.5, 0.01, 0.2, 0.0, O.P(out))
+        done_segs += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(done_segs * T5 / dt, 1), "unit": "samples/s", "cores": 1, "kind": "port",
+            "sample": f"{done_segs} of 4096 segments x 64 steps: forward+backward PPO gradient "
+                      f"(f64, single thread) in {dt:.1f} s; Muon (<2% of the CPU step) not included"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path would shard segments/rows across GPUs; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the step would shard segments across GPUs with one gradient all-reduce per minibatch)",
+              file=sys.stderr)
         return 2
     import torch
     from pufferlean_amd import _lib
     _lib.lib()
-    assert torch.cuda.is_available(), "bench needs a GPU"
-    res = {}
-    if args.workload in ("all", "gemm"):
-        res["gemm"] = bench_gemm(args.steps, args.warmup)
-    if args.workload in ("all", "vtrace"):
-        res["vtrace"] = bench_vtrace(args.steps, args.warmup)
-    g = res.get("gemm", {})
-    head = g.get("nn_fwd_bf16io")
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    comps = {}
+    head = None
+    if args.only in ("all", "ppo"):
+        head = bench_ppo_step(args.steps, args.warmup, eager=args.eager)
+        print(f"# ppo step {head['ms']} ms", file=sys.stderr, flush=True)
+    if args.only in ("all", "gemm"):
+        comps["gemm"] = bench_gemm(args.steps, args.warmup)
+        print("# gemm done", file=sys.stderr, flush=True)
+    if args.only in ("all", "ns"):
+        comps["ns"] = bench_ns(args.steps, args.warmup)
+        print("# ns done", file=sys.stderr, flush=True)
+    if args.only in ("all", "vtrace"):
+        comps["vtrace"] = bench_vtrace(args.steps, args.warmup)
+        print("# vtrace done", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
-        "value": head["tflops"] if head else None,
-        "unit": "TFLOP/s (policy GEMM forward, bf16 MFMA)",
+        "value": head["samples_per_s"] if head else None,
+        "unit": "samples/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(head["us"] / 1e3, 4) if head else None,
+        "ms_per_step": head["ms"] if head else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded splitmix64)",
-        "config": {"workload": "policy GEMM 16384x512x512 (configs: gemm, vtrace)"},
-        "roofline": ({"bound": "mfma", "achieved": head["tflops"], "peak": BF16_PEAK_TFLOPS,
-                      "unit": "TFLOP/s", "frac": head["frac"], "traffic": None} if head else None),
-        "components": res,
+        "data": "synthetic (seeded splitmix64; random-init weights)",
+        "config": {"workload": "MinGRU PPO+Muon minibatch step: obs 128 -> enc 512 -> 2x MinGRU 512 -> "
+                               "16-way + value; 4096 segments x 64 steps",
+                   "segments": B5, "horizon": T5, "hidden": H5, "layers": L5, "actions": A5,
+                   "obs": D5},
     }
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_gemm()
+    if head:
+        dk = head["dominant_kernel"]
+        line["roofline"] = {"bound": "mfma", "achieved": dk["tflops"], "peak": BF16_PEAK_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(dk["tflops"] / BF16_PEAK_TFLOPS, 4),
+                            "traffic": None, "kernel": dk["name"], "kernel_us": dk["us"]}
+        line["step"] = {k: v for k, v in head.items() if k != "dominant_kernel"}
+    line["components"] = comps
+    if not args.no_cpu_baseline and head:
+        line["cpu_baseline"] = cpu_baseline_ppo()
     print(json.dumps(line))
     return 0
 
