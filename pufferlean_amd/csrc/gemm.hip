@@ -60,14 +60,25 @@ __device__ inline float to_f32(float v) { return v; }
 template <typename T> struct Raw8;
 template <> struct Raw8<uint16_t> { uint4 v; };
 template <> struct Raw8<float> { float4 a, b; };
-__device__ inline Raw8<uint16_t> load_raw8(const uint16_t* p) { return {*reinterpret_cast<const uint4*>(p)}; }
-__device__ inline Raw8<float> load_raw8(const float* p) {
-  return {reinterpret_cast<const float4*>(p)[0], reinterpret_cast<const float4*>(p)[1]};
+// Operand pointers are used in the global address space explicitly, so a select between a source
+// address and the zero page below still compiles to global (not flat) loads.
+#define PH_GLOBAL __attribute__((address_space(1)))
+template <typename T> using gptr = const PH_GLOBAL T*;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline Raw8<uint16_t> load_raw8(gptr<uint16_t> p) {
+  const u32x4_t v = *reinterpret_cast<gptr<u32x4_t>>(p);
+  return {make_uint4(v.x, v.y, v.z, v.w)};
 }
-__device__ inline Raw8<uint16_t> zero_raw8(const uint16_t*) { return {make_uint4(0, 0, 0, 0)}; }
-__device__ inline Raw8<float> zero_raw8(const float*) {
-  return {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+__device__ inline Raw8<float> load_raw8(gptr<float> p) {
+  const f32x4_t a = reinterpret_cast<gptr<f32x4_t>>(p)[0], b = reinterpret_cast<gptr<f32x4_t>>(p)[1];
+  return {make_float4(a.x, a.y, a.z, a.w), make_float4(b.x, b.y, b.z, b.w)};
 }
+// Out-of-range chunks (rows past M, k past the split's end) are loaded from this zero page instead
+// of being masked after the load, so no work touches a prefetched register before its LDS store.
+__device__ const float4 kZeroPage[2] = {};
+template <typename T>
+__device__ __forceinline__ gptr<T> zero_page() { return (gptr<T>)(&kZeroPage[0]); }
 __device__ inline uint4 to_bf16x8(const Raw8<uint16_t>& r) { return r.v; }
 __device__ inline uint4 to_bf16x8(const Raw8<float>& r) {
   uint4 o;
@@ -96,6 +107,58 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Position (row r, k) of a thread's chunk c inside an R x BK operand tile (8 consecutive elements
+// along the source's contiguous dimension per chunk, CH chunks per thread, NT threads).
+//  - k-contiguous source: chunks walk a row's k first, so each chunk is one 16-byte LDS row piece.
+//  - m/n-contiguous source, CH >= 2: the thread owns CH consecutive k rows of one 8-wide column
+//    group and transposes them in registers into 8 LDS row pieces of CH elements. Consecutive
+//    threads take consecutive k groups: with the padded pitch this puts the 8/4-byte LDS writes of a
+//    wavefront on distinct banks, and a wavefront's loads cover whole 64-byte row segments.
+//  - m/n-contiguous source, CH == 1: consecutive threads walk the column groups of a k row and
+//    write their 8 elements one at a time.
+template <bool TRANS, int R, int BK, int CH, int NT>
+__device__ __forceinline__ void chunk_rk(int tid, int c, int& r, int& k) {
+  if constexpr (!TRANS) {
+    const int id = tid + c * NT;
+    r = id / (BK / 8);
+    k = (id % (BK / 8)) * 8;
+  } else if constexpr (CH >= 2) {
+    constexpr int KG = BK / CH;
+    static_assert((R / 8) * KG == NT, "transposed chunk mapping");
+    r = (tid / KG) * 8;
+    k = (tid % KG) * CH + c;
+  } else {
+    const int id = tid + c * NT;
+    k = id / (R / 8);
+    r = (id % (R / 8)) * 8;
+  }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int j) {
+  return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
+}
+
+// v[c] holds the 8 bf16 of source k row (k + c) at columns r..r+7. Writes LDS rows r..r+7, each
+// the CH elements k..k+CH-1 (one 8-byte or 4-byte store per row).
+template <int CH, int LDK>
+__device__ __forceinline__ void put_trans(uint16_t* dst, int r, int k, const uint4 (&v)[CH]) {
+  static_assert(CH == 2 || CH == 4, "transposed store width");
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    const int j = q >> 1;
+    uint32_t w[CH / 2];
+#pragma unroll
+    for (int p = 0; p < CH / 2; p++) {
+      const uint32_t lo = word_of(v[2 * p], j), hi = word_of(v[2 * p + 1], j);
+      // column r+q of rows k+2p (low half) and k+2p+1 (high half)
+      w[p] = (q & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+    uint16_t* p = &dst[(r + q) * LDK + k];
+    if constexpr (CH == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(p) = w[0];
+  }
 }
 
 // Thread-block tile id -> (tile_m, tile_n). With remap, the blocks that land on one XCD (blocks are
@@ -198,6 +261,30 @@ __device__ __forceinline__ void stage_acc(float* sC, const floatx16 (&acc)[SM][S
 #pragma unroll
       for (int r = 0; r < 16; r++)
         sC[(wm0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3)) * LDC + wn0 + j * 32 + lr] = acc[i][j][r];
+}
+
+// Sub-tiles i of a wave whose 32 rows (relative row wr0 + 32 i) fall inside [0, rows) of the
+// current staging pass; the others belong to another pass.
+template <int SM, int SN, int LDC>
+__device__ __forceinline__ void stage_acc_rows(float* sC, const floatx16 (&acc)[SM][SN], int wr0, int wn0,
+                                               int lane, int rows) {
+  const int hrow = (lane >> 5) * 4, lr = lane & 31;
+#pragma unroll
+  for (int i = 0; i < SM; i++) {
+    const int r0 = wr0 + i * 32;
+    if (r0 < 0 || r0 >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        sC[(r0 + 8 * (r >> 2) + hrow + (r & 3)) * LDC + wn0 + j * 32 + lr] = acc[i][j][r];
+  }
+}
+
+constexpr int epilogue_rows(int bm, int row_bytes, int budget) {
+  int r = bm;
+  while (r > 32 && (r * row_bytes > budget || bm % r != 0)) r -= 32;
+  return r;
 }
 
 __device__ __forceinline__ float4 load4_f32(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -331,7 +418,11 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
 
   constexpr int LDC = BN + 4;  // fp32 C staging pitch
   constexpr int PIPE_BYTES = 2 * NSPLIT * (BM + BN) * LDK * 2;
-  constexpr int C_BYTES = BM * LDC * 4;
+  // The C tile is staged through the pipeline's LDS in passes of EPR rows (all BM rows at once
+  // when they fit, else the largest multiple of 32 rows dividing BM that fits).
+  constexpr int EPR = epilogue_rows(BM, LDC * 4, PIPE_BYTES);
+  static_assert(EPR >= 32 && BM % EPR == 0, "epilogue staging rows");
+  constexpr int C_BYTES = EPR * LDC * 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
   uint16_t (*sA)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
   uint16_t (*sB)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
@@ -353,42 +444,50 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   const int kend = min(g.K, kbeg + g.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
-  const TIA* A = reinterpret_cast<const TIA*>(g.A);
-  const TIB* B = reinterpret_cast<const TIB*>(g.B);
+  const gptr<TIA> A = (gptr<TIA>)g.A;
+  const gptr<TIB> B = (gptr<TIB>)g.B;
 
   Raw8<TIA> ra[2][CA];
   Raw8<TIB> rb[2][CB];
-  uint32_t va[2], vb[2];  // per-chunk validity bits of each register set
 
   // Global -> register set for the k-tile starting at k0. Every load is issued unconditionally (an
-  // out-of-range chunk reads a clamped in-range address and is zeroed when written to LDS), so no
-  // branch separates the loads and the compiler can wait for exactly the set it needs.
-  auto gload = [&](Raw8<TIA> (&xa)[CA], Raw8<TIB> (&xb)[CB], uint32_t& ma, uint32_t& mb, int k0) {
-    ma = 0u;
-    mb = 0u;
+  // out-of-range chunk reads the zero page), so no branch separates the loads and the compiler can
+  // wait for exactly the set it needs.
+  // Per-chunk source offsets split into a per-thread part fixed for the whole k loop and the
+  // uniform k0-dependent part (k0 or k0*ld, a scalar), so a k step adds one scalar per chunk.
+  long offA[CA], offB[CB];
+  int kA[CA], kB[CB];
+  uint32_t rowA = 0u, rowB = 0u;  // bit c: chunk c's row is inside the matrix
+#pragma unroll
+  for (int c = 0; c < CA; c++) {
+    int r, k;
+    chunk_rk<TA, BM, BK, CA, NT>(tid, c, r, k);
+    const int gm = m0 + r;
+    offA[c] = !TA ? (long)gm * g.lda + k : (long)k * g.lda + gm;
+    kA[c] = k;
+    rowA |= (gm < g.M ? 1u : 0u) << c;
+  }
+#pragma unroll
+  for (int c = 0; c < CB; c++) {
+    int r, k;
+    chunk_rk<!TB, BN, BK, CB, NT>(tid, c, r, k);
+    const int gn = n0 + r;
+    offB[c] = TB ? (long)gn * g.ldb + k : (long)k * g.ldb + gn;
+    kB[c] = k;
+    rowB |= (gn < g.N ? 1u : 0u) << c;
+  }
+  auto gload = [&](Raw8<TIA> (&xa)[CA], Raw8<TIB> (&xb)[CB], int k0) {
+    const long da = !TA ? (long)k0 : (long)k0 * g.lda;
+    const long db = TB ? (long)k0 : (long)k0 * g.ldb;
 #pragma unroll
     for (int c = 0; c < CA; c++) {
-      const int id = tid + c * NT;
-      int r, k;
-      if (!TA) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
-      else { k = id / (BM / 8); r = (id % (BM / 8)) * 8; }
-      const int gm = m0 + r, gk = k0 + k;
-      const bool ok = gm < g.M && gk < kend;
-      const long off = ok ? (!TA ? (long)gm * g.lda + gk : (long)gk * g.lda + gm) : 0;
-      xa[c] = load_raw8(A + off);
-      ma |= (ok ? 1u : 0u) << c;
+      const bool ok = ((rowA >> c) & 1u) && k0 + kA[c] < kend;
+      xa[c] = load_raw8(ok ? A + (offA[c] + da) : zero_page<TIA>());
     }
 #pragma unroll
     for (int c = 0; c < CB; c++) {
-      const int id = tid + c * NT;
-      int r, k;
-      if (TB) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
-      else { k = id / (BN / 8); r = (id % (BN / 8)) * 8; }
-      const int gn = n0 + r, gk = k0 + k;
-      const bool ok = gn < g.N && gk < kend;
-      const long off = ok ? (TB ? (long)gn * g.ldb + gk : (long)gk * g.ldb + gn) : 0;
-      xb[c] = load_raw8(B + off);
-      mb |= (ok ? 1u : 0u) << c;
+      const bool ok = ((rowB >> c) & 1u) && k0 + kB[c] < kend;
+      xb[c] = load_raw8(ok ? B + (offB[c] + db) : zero_page<TIB>());
     }
   };
   // Register set -> LDS buffer `s` (transposing m/n-contiguous chunks).
@@ -404,30 +503,36 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
       }
     }
   };
-  auto sstore = [&](const Raw8<TIA> (&xa)[CA], const Raw8<TIB> (&xb)[CB], uint32_t ma, uint32_t mb,
-                    int s) {
+  // One operand's register set -> LDS (hi part, and the lo part of the split for X3).
+  auto sstore_op = [&](auto trans_c, auto rows_c, const auto& x, uint16_t* dst, uint16_t* dstl) {
+    constexpr bool TR = decltype(trans_c)::value;
+    constexpr int R = decltype(rows_c)::value;
+    constexpr int CH = sizeof(x) / sizeof(x[0]);
+    if constexpr (TR && CH >= 2) {
+      uint4 v[CH], l[CH];
 #pragma unroll
-    for (int c = 0; c < CA; c++) {
-      const int id = tid + c * NT;
-      const bool ok = (ma >> c) & 1u;
+      for (int c = 0; c < CH; c++) {
+        v[c] = to_bf16x8(x[c]);
+        if constexpr (X3) l[c] = lo_bf16x8(x[c], v[c]);
+      }
       int r, k;
-      if (!TA) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
-      else { k = id / (BM / 8); r = (id % (BM / 8)) * 8; }
-      uint4 v = ok ? to_bf16x8(xa[c]) : make_uint4(0, 0, 0, 0);
-      put(sA[s], r, k, v, TA);
-      if constexpr (X3) put(sAl[s], r, k, ok ? lo_bf16x8(xa[c], v) : make_uint4(0, 0, 0, 0), TA);
-    }
+      chunk_rk<TR, R, BK, CH, NT>(tid, 0, r, k);
+      put_trans<CH, LDK>(dst, r, k, v);
+      if constexpr (X3) put_trans<CH, LDK>(dstl, r, k, l);
+    } else {
 #pragma unroll
-    for (int c = 0; c < CB; c++) {
-      const int id = tid + c * NT;
-      const bool ok = (mb >> c) & 1u;
-      int r, k;
-      if (TB) { r = id / (BK / 8); k = (id % (BK / 8)) * 8; }
-      else { k = id / (BN / 8); r = (id % (BN / 8)) * 8; }
-      uint4 v = ok ? to_bf16x8(xb[c]) : make_uint4(0, 0, 0, 0);
-      put(sB[s], r, k, v, !TB);
-      if constexpr (X3) put(sBl[s], r, k, ok ? lo_bf16x8(xb[c], v) : make_uint4(0, 0, 0, 0), !TB);
+      for (int c = 0; c < CH; c++) {
+        int r, k;
+        chunk_rk<TR, R, BK, CH, NT>(tid, c, r, k);
+        const uint4 v = to_bf16x8(x[c]);
+        put(dst, r, k, v, TR);
+        if constexpr (X3) put(dstl, r, k, lo_bf16x8(x[c], v), TR);
+      }
     }
+  };
+  auto sstore = [&](const Raw8<TIA> (&xa)[CA], const Raw8<TIB> (&xb)[CB], int s) {
+    sstore_op(std::integral_constant<bool, TA>{}, std::integral_constant<int, BM>{}, xa, sA[s], sAl[s]);
+    sstore_op(std::integral_constant<bool, !TB>{}, std::integral_constant<int, BN>{}, xb, sB[s], sBl[s]);
   };
 
   floatx16 acc[SM][SN];
@@ -507,30 +612,50 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
     }
   };
 
+  // The k loop runs over an even number of tiles with no conditional work inside: a tile at or past
+  // kend is loaded from a clamped address and written to LDS as zeros (so an odd tile count gets one
+  // zero tile), and the prefetch of the two tiles past the end is issued the same way. Every load
+  // is therefore issued on every path, which lets the compiler wait for exactly the register set a
+  // store needs and keep the accumulators in place across iterations.
+  const int nk2 = (nk + 1) & ~1;
   // Prologue: tile 0 -> LDS buffer 0, tile 1 -> register set 1 (in flight).
-  if (nk > 0) {
-    gload(ra[0], rb[0], va[0], vb[0], kbeg);
-    if (nk > 1) gload(ra[1], rb[1], va[1], vb[1], kbeg + BK);
-    sstore(ra[0], rb[0], va[0], vb[0], 0);
+  if (nk2 > 0) {
+    gload(ra[0], rb[0], kbeg);
+    gload(ra[1], rb[1], kbeg + BK);
+    sstore(ra[0], rb[0], 0);
     lds_barrier();
   }
   // Step for tile kt held in LDS buffer P; register set P^1 holds tile kt+1; set P receives kt+2.
+  // The phases are fenced against the instruction scheduler: the prefetch is issued first and the
+  // LDS store of the older set comes after the MFMAs, so each set has a full step to arrive.
   auto step = [&](int kt, auto Pc) {
     constexpr int P = decltype(Pc)::value;
-    if (kt + 2 < nk) gload(ra[P], rb[P], va[P], vb[P], kbeg + (kt + 2) * BK);
+    gload(ra[P], rb[P], kbeg + (kt + 2) * BK);
+    __builtin_amdgcn_sched_barrier(0);
     compute(P);
-    if (kt + 1 < nk) sstore(ra[P ^ 1], rb[P ^ 1], va[P ^ 1], vb[P ^ 1], P ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    sstore(ra[P ^ 1], rb[P ^ 1], P ^ 1);
     lds_barrier();
   };
-  for (int kt = 0; kt < nk; kt += 2) {
+  for (int kt = 0; kt < nk2; kt += 2) {
     step(kt, std::integral_constant<int, 0>{});
-    if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
   }
 
   // the last loop iteration ended with a barrier: the pipeline buffers are free for the C tile
-  stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
-  lds_barrier();
-  flush_tile<TC, BM, BN, NT, LDC>(g, sC, m0, n0);
+  if constexpr (EPR == BM) {
+    stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
+    lds_barrier();
+    flush_tile<TC, BM, BN, NT, LDC>(g, sC, m0, n0);
+  } else {
+#pragma unroll 1
+    for (int p = 0; p < BM / EPR; p++) {
+      if (p > 0) lds_barrier();  // the previous pass's flush has read the staging area
+      stage_acc_rows<SM, SN, LDC>(sC, acc, wm0 - p * EPR, wn0, lane, EPR);
+      lds_barrier();
+      flush_tile<TC, EPR, BN, NT, LDC>(g, sC, m0 + p * EPR, n0);
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -709,6 +834,14 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
   else launch_bf16<BM, BN, BK, true, true, TIA, TIB>(g, grid, st);
 }
 
+// Larger tiles for bf16 operands: 256x128 (four 128x64 wavefronts) for big outputs, 256x256 (four
+// 128x128 wavefronts, one block per CU) for split-K over long reductions. Per MFMA they move 3/4
+// and 1/2 of the 128x128 tile's LDS bytes.
+void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStream_t st) {
+  if (bn == 256) dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  else dispatch_bf16_t<256, 128, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+}
+
 // fp32 operands are kept raw (8 floats per chunk) in the two prefetch register sets, so they use
 // half the k-tile of bf16 operands to stay within the register file.
 template <int BM, int BN>
@@ -809,16 +942,25 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
                        ((uintptr_t)d.B % 16) == 0;
   if (!aligned) return gemm_scalar(g, d, st);
 
-  // Tile choice: 128x128 when that gives >= 128 tiles. Otherwise, for long reductions (the wgrad
-  // forms, K = rows of the minibatch) 128x128 with split-K up to ~512 blocks, >= 2048 of k each;
-  // for short ones 64x64 tiles when those reach 128, else split-K with >= 256 of k each.
+  // Tile choice (measured on the policy shapes). bf16 x bf16 with >= 512 tiles of 256x128: the
+  // 256x128 kernel. Otherwise 128x128 when that gives >= 128 tiles. Otherwise, for long reductions
+  // (the wgrad forms, K = rows of the minibatch) split-K over 256x256 (bf16) or 128x128 tiles up to
+  // the resident block count (one 256x256 or two 128x128 blocks on each of the 256 CUs, so all
+  // splits run in one round), >= 2048 of k per split; for short reductions 64x64 tiles when those
+  // reach 128, else split-K with >= 256 of k each.
   int splits = d.splits > 0 ? d.splits : 1;
+  const long tiles256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
+  const long tiles256x128 = (long)((d.M + 255) / 256) * ((d.N + 127) / 128);
   const long tiles128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
-  bool small = false;
-  if (d.splits <= 0 && tiles128 < 128) {
+  const bool big_ok = d.math == PH_MATH_BF16 && d.a_dtype == PH_BF16 && d.b_dtype == PH_BF16;
+  bool small = false, big = big_ok && tiles256x128 >= 512;
+  int big_bn = 128;
+  if (!big && d.splits <= 0 && tiles128 < 128) {
     if (d.K >= 4096) {
-      const long want = (512 + tiles128 - 1) / (tiles128 > 0 ? tiles128 : 1);
+      big = big_ok;
+      big_bn = 256;
+      const long want = big ? 256 / tiles256 : 512 / tiles128;
       const long maxs = d.K / 2048;
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
@@ -838,13 +980,15 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   if (splits < 1) splits = 1;
   g.kps = kps > 0 ? kps : BK;
   if (splits > 1) {
-    g.ws = (float*)scratch(kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
+    g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
   }
-  const int bm = small ? 64 : 128, bn = small ? 64 : 128;
+  const int bm = big ? 256 : (small ? 64 : 128), bn = big ? big_bn : bm;
   const unsigned tiles = (unsigned)(((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn));
   dim3 grid(tiles, 1, splits);
-  if (d.math == PH_MATH_BF16) {
+  if (big) {
+    dispatch_big(g, bn, d.trans_a, d.trans_b, grid, st);
+  } else if (d.math == PH_MATH_BF16) {
     if (small) dispatch_bf16<64, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
     else dispatch_bf16<128, 128>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
   } else if (d.math == PH_MATH_BF16X3) {

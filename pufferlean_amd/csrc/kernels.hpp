@@ -13,17 +13,28 @@ enum : int {
   kSlotPpoPart = 4,
   kSlotPpoCounter = 5,
   kSlotGemmWs = 6,
-  kSlotGemmCounter = 7,
-  kSlotNs = 8,        // 8..15 Newton-Schulz
+  kSlotNs = 8,        // Newton-Schulz buffers of the stand-alone entry points
   kSlotMuonExact = 16,
   kSlotMuonFastU = 17,
   kSlotGclip = 18,
-  kSlotMgColsum = 19,
   kSlotMgBufs = 20,
-  kSlotMgZero = 21,
-  kSlotLean = 32,     // 32..95 host-buffer entry points
-  kSlotMlp = 96,      // 96..127 resident MLP step
+  kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
+  kSlotHost = 48,     // 48..127: host-buffer entry points
 };
+constexpr int kLanes = 8;
+
+// Per-lane scratch for one Muon matrix update running on its own stream.
+struct LaneSlots {
+  int u, ns, gemm_ws;
+};
+inline LaneSlots lane_slots(int lane) {
+  return {kSlotLane + 3 * lane, kSlotLane + 3 * lane + 1, kSlotLane + 3 * lane + 2};
+}
+// Library-owned side stream `lane` of the current device (created on first use, default priority)
+// and fork/join events.
+hipStream_t lane_stream(int lane);
+int fork_lanes(hipStream_t main, int n);  // lanes 0..n-1 wait for work queued so far on main
+int join_lanes(hipStream_t main, int n);  // main waits for everything queued on lanes 0..n-1
 
 // Zero a 256-byte arrival-counter block once per pointer (fill kernel, no memset node).
 int ensure_zeroed_counter(unsigned* counter, hipStream_t st);
@@ -47,7 +58,8 @@ struct PhGemmDesc {
   void* C2;
   long ldc2;
   int c2_trans;
-  int splits;  // <= 0: chosen by shape
+  int splits;   // <= 0: chosen by shape
+  int ws_slot;  // scratch slot of the split-K partials (0: the shared default slot)
 };
 int gemm(const PhGemmDesc& d, hipStream_t st);
 
@@ -68,10 +80,10 @@ int muon_mat_exact(int rows, int cols, const double* W, const double* G, const d
 int stepvec_exact(long n, const double* b, const double* g, const double* m, double* nb, double* nm,
                   double gscale, double lr, double wd, double mu, hipStream_t st);
 int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
-                       int math, int slot_base, hipStream_t st);
+                       int math, int ns_slot, int ws_slot, hipStream_t st);
 int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
               float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
-              hipStream_t st);
+              const LaneSlots& slots, hipStream_t st);
 int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
                 hipStream_t st);
 int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);
@@ -79,6 +91,8 @@ int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st);
 int colsum_f32(const float* X, size_t N, int J, size_t ld, float* out, float scale, int accumulate,
                hipStream_t st);
+int colsum_bf16(const uint16_t* X, long N, int J, long ld, float* out, float scale, int accumulate,
+                hipStream_t st);
 int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st);
 
 long mingru_param_count(const ph_mingru_dims& d);

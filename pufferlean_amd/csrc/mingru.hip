@@ -21,70 +21,150 @@ namespace {
 constexpr int HP = 32;  // padded head rows
 constexpr unsigned kB = 256;
 
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
+// Logistic function on the hardware exp2 / reciprocal instructions (a few ulp; the scans are
+// VALU-bound with IEEE exp and division). exp(-x) overflowing to +inf gives exactly 0.
+__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float gact(float x) { return x >= 0.f ? x + 0.5f : sigm(x); }
 __device__ __forceinline__ float ld(const uint16_t* p) { return bf16_to_f32(*p); }
 __device__ __forceinline__ float ld(const float* p) { return *p; }
 __device__ __forceinline__ void st(uint16_t* p, float v) { *p = bf16_rne(v); }
 __device__ __forceinline__ void st(float* p, float v) { *p = v; }
 
-// Forward scan of one layer. Thread = (b, j); o = (1-z)*prev + z*g(hid), h = hg*o + (1-hg)*hin.
+// 4 consecutive hidden units per thread: raw vector of 4 elements as loaded (8 bytes bf16,
+// 16 bytes fp32), unpacked to fp32 only where the recurrence uses it.
+template <typename TS> struct Raw4;
+template <> struct Raw4<uint16_t> { uint2 v; };
+template <> struct Raw4<float> { float4 v; };
+__device__ __forceinline__ Raw4<uint16_t> ld4(const uint16_t* p) { return {*reinterpret_cast<const uint2*>(p)}; }
+__device__ __forceinline__ Raw4<float> ld4(const float* p) { return {*reinterpret_cast<const float4*>(p)}; }
+__device__ __forceinline__ float el(const Raw4<uint16_t>& r, int q) {
+  const uint32_t w = q < 2 ? r.v.x : r.v.y;
+  return bf16_to_f32((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+__device__ __forceinline__ float el(const Raw4<float>& r, int q) {
+  return q == 0 ? r.v.x : (q == 1 ? r.v.y : (q == 2 ? r.v.z : r.v.w));
+}
+__device__ __forceinline__ void st4(uint16_t* p, const float (&v)[4]) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3]));
+}
+__device__ __forceinline__ void st4(float* p, const float (&v)[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+constexpr int kScanCh = 4;  // timesteps loaded ahead of the recurrence
+
+// Forward scan of one layer. Thread = (b, 4 consecutive j); o = (1-z)*prev + z*g(hid),
+// h = hg*o + (1-hg)*hin, state reset after a terminal step. The loads of kScanCh steps are issued
+// before their arithmetic; per element the math is the sequential recurrence.
 template <typename TS>
 __global__ void __launch_bounds__(256) k_scan_fwd(const TS* __restrict__ cmb, const TS* __restrict__ hin,
                                                   TS* __restrict__ hout, TS* __restrict__ oS,
                                                   const float* __restrict__ done, int B, int H, int T) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)B * H) return;
-  const int b = (int)(idx / H), j = (int)(idx % H);
+  const int HV = H / 4;
+  if (idx >= (long)B * HV) return;
+  const int b = (int)(idx / HV), j = (int)(idx % HV) * 4;
   const long BH = (long)B * H, B3H = (long)B * 3 * H;
-  float state = 0.f;
-  const TS* y = cmb + (long)b * 3 * H + j;
-  for (int t = 0; t < T; t++) {
-    const long s = (long)t * BH + idx;
-    const TS* yt = y + (long)t * B3H;
-    const float hid = ld(yt), gate = ld(yt + H), proj = ld(yt + 2 * H);
-    const float z = sigm(gate), g = gact(hid), hg = sigm(proj);
-    const float o = (1.f - z) * state + z * g;
-    const float hi = ld(hin + s);
-    st(hout + s, hg * o + (1.f - hg) * hi);
-    st(oS + s, o);
-    state = o;
-    if (done[(long)t * B + b] != 0.f) state = 0.f;
+  const long xo = (long)b * H + j, yo = (long)b * 3 * H + j;
+  float state[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < T; t0 += kScanCh) {
+    Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh];
+    float rd[kScanCh];
+#pragma unroll
+    for (int c = 0; c < kScanCh; c++) {
+      const int t = t0 + c < T ? t0 + c : T - 1;  // clamped: a step past T is loaded, not used
+      const TS* yt = cmb + (long)t * B3H + yo;
+      rh[c] = ld4(yt);
+      rg[c] = ld4(yt + H);
+      rp[c] = ld4(yt + 2 * H);
+      rx[c] = ld4(hin + (long)t * BH + xo);
+      rd[c] = done[(long)t * B + b];
+    }
+#pragma unroll
+    for (int c = 0; c < kScanCh; c++) {
+      if (t0 + c >= T) break;
+      float hv[4], ov[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float z = sigm(el(rg[c], q)), g = gact(el(rh[c], q)), hg = sigm(el(rp[c], q));
+        const float o = (1.f - z) * state[q] + z * g;
+        hv[q] = hg * o + (1.f - hg) * el(rx[c], q);
+        ov[q] = o;
+        state[q] = rd[c] != 0.f ? 0.f : o;
+      }
+      const long so = (long)(t0 + c) * BH + xo;
+      st4(hout + so, hv);
+      st4(oS + so, ov);
+    }
   }
 }
 
-// Backward scan of one layer (adjoint of k_scan_fwd). dhn: gradient w.r.t. this layer's output;
-// writes dy = d(hid,gate,proj) pre-activation gradients and dhx = dhn*(1-hg) (the direct part of
-// the gradient w.r.t. the layer input; the GEMM dy.W adds the rest).
+// Backward scan of one layer (adjoint of k_scan_fwd), t descending. dhn: gradient w.r.t. this
+// layer's output; writes dy = d(hid,gate,proj) pre-activation gradients and dhx = dhn*(1-hg) (the
+// direct part of the gradient w.r.t. the layer input; the GEMM dy.W adds the rest). o_{t-1} is
+// loaded once and carried as o_t of the next (earlier) step.
 template <typename TS>
 __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, const TS* __restrict__ oS,
                                                   const TS* __restrict__ hin, const TS* __restrict__ dhn,
                                                   TS* __restrict__ dy, TS* __restrict__ dhx,
                                                   const float* __restrict__ done, int B, int H, int T) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)B * H || T <= 0) return;
-  const int b = (int)(idx / H), j = (int)(idx % H);
+  const int HV = H / 4;
+  if (idx >= (long)B * HV || T <= 0) return;
+  const int b = (int)(idx / HV), j = (int)(idx % HV) * 4;
   const long BH = (long)B * H, B3H = (long)B * 3 * H;
-  float dOn = 0.f;
-  for (int t = T - 1; t >= 0; t--) {
-    const long s = (long)t * BH + idx;
-    const long yo = (long)t * B3H + (long)b * 3 * H + j;
-    const float hid = ld(cmb + yo), gate = ld(cmb + yo + H), proj = ld(cmb + yo + 2 * H);
-    const float o = ld(oS + s), hi = ld(hin + s), dh = ld(dhn + s);
-    const bool keep_prev = t > 0 && done[(long)(t - 1) * B + b] == 0.f;
-    const float prev = keep_prev ? ld(oS + s - BH) : 0.f;
-    const float z = sigm(gate), hg = sigm(proj), g = gact(hid);
-    const float dhg = dh * (o - hi);
-    const float dox = dh * hg + dOn;
-    st(dhx + s, dh * (1.f - hg));
-    const float dz = dox * (g - prev);
-    const float dprev = dox * (1.f - z);
-    const float dg = dox * z;
-    const float sg = hid >= 0.f ? 1.f : sigm(hid) * (1.f - sigm(hid));
-    st(dy + yo, dg * sg);
-    st(dy + yo + H, dz * z * (1.f - z));
-    st(dy + yo + 2 * H, dhg * hg * (1.f - hg));
-    dOn = keep_prev ? dprev : 0.f;
+  const long xo = (long)b * H + j, yo = (long)b * 3 * H + j;
+  float dOn[4] = {0.f, 0.f, 0.f, 0.f};
+  Raw4<TS> ocur = ld4(oS + (long)(T - 1) * BH + xo);
+  for (int t0 = T - 1; t0 >= 0; t0 -= kScanCh) {
+    Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh], rdh[kScanCh], rpo[kScanCh];
+    float rkeep[kScanCh];
+#pragma unroll
+    for (int c = 0; c < kScanCh; c++) {
+      const int t = t0 - c >= 0 ? t0 - c : 0;  // clamped: a step before 0 is loaded, not used
+      const int tp = t > 0 ? t - 1 : 0;
+      const TS* yt = cmb + (long)t * B3H + yo;
+      rh[c] = ld4(yt);
+      rg[c] = ld4(yt + H);
+      rp[c] = ld4(yt + 2 * H);
+      rx[c] = ld4(hin + (long)t * BH + xo);
+      rdh[c] = ld4(dhn + (long)t * BH + xo);
+      rpo[c] = ld4(oS + (long)tp * BH + xo);
+      rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < kScanCh; c++) {
+      const int t = t0 - c;
+      if (t < 0) break;
+      const bool keep_prev = rkeep[c] != 0.f;
+      float vdhx[4], vdg[4], vdz[4], vdp[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float hid = el(rh[c], q), gate = el(rg[c], q), proj = el(rp[c], q);
+        const float o = el(ocur, q), hi = el(rx[c], q), dh = el(rdh[c], q);
+        const float prev = keep_prev ? el(rpo[c], q) : 0.f;
+        const float z = sigm(gate), hg = sigm(proj), sh = sigm(hid);
+        const float g = hid >= 0.f ? hid + 0.5f : sh;
+        const float dhg = dh * (o - hi);
+        const float dox = dh * hg + dOn[q];
+        vdhx[q] = dh * (1.f - hg);
+        const float dz = dox * (g - prev);
+        const float dprev = dox * (1.f - z);
+        const float dg = dox * z;
+        const float sg = hid >= 0.f ? 1.f : sh * (1.f - sh);
+        vdg[q] = dg * sg;
+        vdz[q] = dz * z * (1.f - z);
+        vdp[q] = dhg * hg * (1.f - hg);
+        dOn[q] = keep_prev ? dprev : 0.f;
+      }
+      const long so = (long)t * BH + xo;
+      const long yw = (long)t * B3H + yo;
+      st4(dhx + so, vdhx);
+      st4(dy + yw, vdg);
+      st4(dy + yw + H, vdz);
+      st4(dy + yw + 2 * H, vdp);
+      ocur = rpo[c];
+    }
   }
 }
 
@@ -145,47 +225,14 @@ __global__ void k_norm_adv(const float* __restrict__ adv, const float* __restric
   if (i < n) advn[i] = (adv[i] - stats[0]) / stats[1];
 }
 
-__global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y, long n) {
-  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = bf16_rne(x[i]);
-}
-
-// Column sums of a bf16 [N][J] matrix in fixed row chunks (partials [G][J] fp32)
-__global__ void __launch_bounds__(256) k_colsum_bf16_part(const uint16_t* __restrict__ X, long N, int J,
-                                                          long rows_per, float* __restrict__ part) {
-  __shared__ float sh[4][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int r0 = threadIdx.x >> 6;
-  const long lo = (long)blockIdx.y * rows_per;
-  const long hi = lo + rows_per < N ? lo + rows_per : N;
-  float acc = 0.f;
-  if (c < J)
-    for (long r = lo + r0; r < hi; r += 4) acc += bf16_to_f32(X[r * J + c]);
-  sh[r0][threadIdx.x & 63] = acc;
-  __syncthreads();
-  if (threadIdx.x < 64 && c < J)
-    part[(long)blockIdx.y * J + c] = ((sh[0][threadIdx.x] + sh[1][threadIdx.x]) + sh[2][threadIdx.x]) + sh[3][threadIdx.x];
-}
-
-__global__ void k_colsum_fin(const float* __restrict__ part, int G, int J, float* __restrict__ out) {
-  int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= J) return;
-  float s = 0.f;
-  for (int g = 0; g < G; g++) s += part[(long)g * J + c];
-  out[c] = s;
-}
-
-int colsum_bf16(const uint16_t* X, long N, int J, float* out, hipStream_t st) {
-  long rows_per = 1024;
-  long G = (N + rows_per - 1) / rows_per;
-  if (G > 512) { G = 512; rows_per = (N + G - 1) / G; }
-  if (G < 1) G = 1;
-  float* part = (float*)scratch(kSlotMgColsum, (size_t)G * J * 4);
-  if (!part) return PH_ERR_NOMEM;
-  k_colsum_bf16_part<<<dim3(ceil_div(J, 64), (unsigned)G), 256, 0, st>>>(X, N, J, rows_per, part);
-  k_colsum_fin<<<ceil_div(J, 256), 256, 0, st>>>(part, (int)G, J, out);
-  PH_LAUNCH_CHECK();
-  return PH_OK;
+// fp32 -> bf16 (RNE), 8 elements per thread (n is a multiple of 8: the observation width is)
+__global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y, long n8) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+  reinterpret_cast<uint4*>(y)[i] =
+      make_uint4(bf16x2_rne(a.x, a.y), bf16x2_rne(a.z, a.w), bf16x2_rne(b.x, b.y), bf16x2_rne(b.z, b.w));
 }
 
 // Activation and weight-copy buffers hold bf16 (precision 0) or fp32 (precision 1) elements; they
@@ -299,7 +346,8 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const floa
                                           (TS*)b.wht, b.bh);
   const void* obsg = obs;
   if (BF) {
-    k_f32_to_bf16_k<<<ceil_div(TB * D, kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D);
+    PH_REQUIRE(((uintptr_t)obs % 16) == 0, "mingru: observations must be 16-byte aligned");
+    k_f32_to_bf16_k<<<ceil_div(TB * D / 8, kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D / 8);
     obsg = b.obsb;
   }
   PH_LAUNCH_CHECK();
@@ -316,8 +364,8 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const floa
     TS* cmb = cmbs + (long)l * TB * 3 * H;
     PhGemmDesc g = gd(0, 1, (int)TB, 3 * H, H, DT, xl, H, DT, wl + l * szL, H, DT, cmb, 3 * H, MATH);
     PH_TRY(gemm(g, st));
-    k_scan_fwd<TS><<<ceil_div((long)d.B * H, kB), kB, 0, st>>>(cmb, xl, xl + TB * H, os + (long)l * TB * H,
-                                                             done, d.B, H, d.T);
+    k_scan_fwd<TS><<<ceil_div((long)d.B * H / 4, kB), kB, 0, st>>>(cmb, xl, xl + TB * H,
+                                                                 os + (long)l * TB * H, done, d.B, H, d.T);
     PH_LAUNCH_CHECK();
   }
   TS* xL = x + (long)L * TB * H;
@@ -346,8 +394,8 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const floa
   for (int l = L - 1; l >= 0; l--) {
     TS* xl = x + (long)l * TB * H;
     TS* cmb = cmbs + (long)l * TB * 3 * H;
-    k_scan_bwd<TS><<<ceil_div((long)d.B * H, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn, dy,
-                                                             dhx, done, d.B, H, d.T);
+    k_scan_bwd<TS><<<ceil_div((long)d.B * H / 4, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn,
+                                                                 dy, dhx, done, d.B, H, d.T);
     PH_LAUNCH_CHECK();
     // gW_l = dy^T x_l  -> G
     PhGemmDesc g = gd(1, 0, 3 * H, H, (int)TB, DT, dy, 3 * H, DT, xl, H, PH_F32,
@@ -360,7 +408,7 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const floa
     TS* t = dhn; dhn = dhx; dhx = t;
   }
   // encoder backward: gbEnc = colsum(dh), gWEnc = dh^T obs
-  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, G + offBEnc, st));
+  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
   else PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
   {
     PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, D, PH_F32, G, D, MATH);
@@ -383,6 +431,7 @@ int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float*
   PH_REQUIRE(d.A + 1 <= HP, "mingru: at most %d actions", HP - 1);
   PH_REQUIRE(d.H % 8 == 0 && d.D % 8 == 0, "mingru: hidden and obs sizes must be multiples of 8");
   PH_REQUIRE(d.precision == 0 || d.precision == 1, "mingru: precision must be 0 (bf16) or 1 (fp32)");
+  PH_REQUIRE(d.L <= kLanes - 3, "mingru: at most %d layers", kLanes - 3);
   PH_REQUIRE((long)d.T * d.B <= INT32_MAX, "mingru: T*B exceeds int32");
   if (d.precision == 1)
     return mingru_ppo_grad_t<float>(d, c, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
@@ -392,6 +441,8 @@ int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float*
 }
 
 // Clip the summed gradient and apply Muon to every matrix (fp32 master weights), stepvec to biases.
+// The matrix updates are independent: each runs on its own library stream lane (own scratch),
+// forked from and joined back into `st`; the bias updates run on `st` meanwhile.
 int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, float* mom, float* G,
                 hipStream_t st) {
   const int H = d.H, D = d.D, L = d.L, A = d.A;
@@ -400,20 +451,26 @@ int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, 
   const long szE = (long)H * D, szL = 3L * H * H;
   const long offBEnc = szE, offW = szE + H, offDec = offW + (long)L * szL, offBDec = offDec + (long)A * H,
              offVal = offBDec + A, offBVal = offVal + H;
-  auto mat = [&](long off, int rows, int cols) {
-    return muon_fast(params + off, G + off, mom + off, rows, cols, 1.f, m.lr, m.wd, m.mu, m.eps,
-                     m.coeffs, m.nsteps, m.math, st);
-  };
+  struct Mat { long off; int rows, cols; };
+  Mat mats[kLanes];
+  int nm = 0;
+  mats[nm++] = {0, H, D};
+  for (int l = 0; l < L; l++) mats[nm++] = {offW + l * szL, 3 * H, H};
+  mats[nm++] = {offDec, A, H};
+  mats[nm++] = {offVal, 1, H};
+  PH_REQUIRE(nm <= kLanes, "mingru: at most %d weight matrices (layers <= %d)", kLanes, kLanes - 3);
+  PH_TRY(fork_lanes(st, nm));
+  for (int i = 0; i < nm; i++)
+    PH_TRY(muon_fast(params + mats[i].off, G + mats[i].off, mom + mats[i].off, mats[i].rows,
+                     mats[i].cols, 1.f, m.lr, m.wd, m.mu, m.eps, m.coeffs, m.nsteps, m.math,
+                     lane_slots(i), lane_stream(i)));
   auto vec = [&](long off, long n) {
     return stepvec_f32(params + off, G + off, mom + off, n, 1.f, m.lr, m.wd, m.mu, st);
   };
-  PH_TRY(mat(0, H, D));
   PH_TRY(vec(offBEnc, H));
-  for (int l = 0; l < L; l++) PH_TRY(mat(offW + l * szL, 3 * H, H));
-  PH_TRY(mat(offDec, A, H));
   PH_TRY(vec(offBDec, A));
-  PH_TRY(mat(offVal, 1, H));
   PH_TRY(vec(offBVal, 1));
+  PH_TRY(join_lanes(st, nm));
   return PH_OK;
 }
 

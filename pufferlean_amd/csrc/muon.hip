@@ -272,7 +272,7 @@ int stepvec_exact(long n, const double* b, const double* g, const double* m, dou
 // The split products keep the quintic within 1e-2 of the f64 iterate, which plain bf16 operands for
 // A^2 and BX do not (about 2% at 512 x 1024 with the constant coefficients).
 int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
-                       int math, int slot_base, hipStream_t st) {
+                       int math, int ns_slot, int ws_slot, hipStream_t st) {
   const long n = (long)rows * cols;
   if (n == 0) return PH_OK;
   const int m = rows < cols ? rows : cols, w = rows < cols ? cols : rows;
@@ -284,7 +284,7 @@ int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int ns
     return PH_ERR_UNSUPPORTED;
   }
   const size_t bytes = (size_t)(2 * n + 2 * mm) * 4 + 4096 * 4 + 256;
-  float* ws = (float*)scratch(slot_base, bytes);
+  float* ws = (float*)scratch(ns_slot, bytes);
   if (!ws) return PH_ERR_NOMEM;
   float* Xs[2] = {ws, ws + n};
   float* Af = ws + 2 * n;
@@ -305,18 +305,21 @@ int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int ns
     d.trans_a = 0; d.trans_b = 1; d.M = m; d.N = m; d.K = w;
     d.a_dtype = PH_F32; d.A = Xi; d.lda = w; d.b_dtype = PH_F32; d.B = Xi; d.ldb = w;
     d.c_dtype = PH_F32; d.C = Af; d.ldc = m; d.math = m1; d.epi = PH_EPI_NONE; d.alpha = 1.f;
+    d.ws_slot = ws_slot;
     PH_TRY(gemm(d, st));
     d = PhGemmDesc{};
     d.trans_a = 0; d.trans_b = 1; d.M = m; d.N = m; d.K = m;
     d.a_dtype = PH_F32; d.A = Af; d.lda = m; d.b_dtype = PH_F32; d.B = Af; d.ldb = m;
     d.c_dtype = PH_F32; d.C = Bf; d.ldc = m; d.math = m23;
     d.epi = PH_EPI_AXPBY; d.alpha = c; d.beta = b; d.aux = Af; d.ldaux = m;
+    d.ws_slot = ws_slot;
     PH_TRY(gemm(d, st));
     d = PhGemmDesc{};
     d.trans_a = 0; d.trans_b = 0; d.M = m; d.N = w; d.K = m;
     d.a_dtype = PH_F32; d.A = Bf; d.lda = m; d.b_dtype = PH_F32; d.B = Xi; d.ldb = w;
     d.c_dtype = PH_F32; d.C = Xo; d.ldc = w; d.math = m23;
     d.epi = PH_EPI_AXPBY; d.alpha = 1.f; d.beta = a; d.aux = Xi; d.ldaux = w;
+    d.ws_slot = ws_slot;
     PH_TRY(gemm(d, st));
   }
   k_ns_store<<<ceil_div(n, kB), kB, 0, st>>>(Xs[nsteps & 1], rows, cols, X);
@@ -326,14 +329,14 @@ int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int ns
 
 int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
               float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
-              hipStream_t st) {
+              const LaneSlots& slots, hipStream_t st) {
   const long n = (long)rows * cols;
   if (n == 0) return PH_OK;
-  float* U = (float*)scratch(kSlotMuonFastU, (size_t)n * 4);
+  float* U = (float*)scratch(slots.u, (size_t)n * 4);
   if (!U) return PH_ERR_NOMEM;
   k_nesterov_f32<<<ceil_div(n, kB), kB, 0, st>>>(G, M, U, n, gscale, mu);
   PH_LAUNCH_CHECK();
-  PH_TRY(newton_schulz_fast(U, rows, cols, coeffs, nsteps, eps, math, kSlotNs, st));
+  PH_TRY(newton_schulz_fast(U, rows, cols, coeffs, nsteps, eps, math, slots.ns, slots.gemm_ws, st));
   const float scale = sqrtf(fmaxf(1.f, (float)rows / (float)cols));
   k_finalize_f32<<<ceil_div(n, kB), kB, 0, st>>>(W, U, n, 1.f - lr * wd, lr * scale);
   PH_LAUNCH_CHECK();
@@ -386,7 +389,7 @@ extern "C" int ph_newton_schulz(float* X, int rows, int cols, const float* coeff
   PH_REQUIRE(math == PH_MATH_BF16 || math == PH_MATH_F32 || math == PH_MATH_BF16X3,
              "ph_newton_schulz: unknown math");
   PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_newton_schulz: coefficient table missing");
-  return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, as_stream(stream));
+  return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, 0, as_stream(stream));
 }
 
 extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale,
@@ -395,7 +398,7 @@ extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int col
   PH_REQUIRE(rows >= 0 && cols >= 0 && nsteps >= 0 && nsteps <= 64, "ph_muon_mat: bad shape");
   PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_muon_mat: coefficient table missing");
   return muon_fast(W, G, M, rows, cols, gscale, lr, wd, mu, eps, coeffs, nsteps, math,
-                   as_stream(stream));
+                   LaneSlots{kSlotMuonFastU, kSlotNs, 0}, as_stream(stream));
 }
 
 extern "C" int ph_stepvec(float* b, const float* g, float* m, size_t n, float gscale, float lr,

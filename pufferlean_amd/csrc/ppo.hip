@@ -98,14 +98,13 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
         if (cc > du) vl = cc;
       }
       lsum[1] = 0.5 * vl;
-      double ent = 0.0;
+      // entropy from the fp32 probabilities of the gradient path (one fp64 exp per row above is
+      // for the ratio terms; 16 more per row made this kernel fp64-bound)
+      float ent = 0.f;
 #pragma unroll
       for (int k = 0; k < AMAX; k++)
-        if (k < A) {
-          const double lp = (double)x[k] - (double)lse;
-          ent -= exp(lp) * lp;
-        }
-      lsum[2] = ent;
+        if (k < A) ent -= pk[k] * (x[k] - lse);
+      lsum[2] = (double)ent;
       lsum[3] = -lr;
       lsum[4] = (r - 1.0) - lr;
       lsum[5] = (r < dlo || r > dhi) ? 1.0 : 0.0;
@@ -133,13 +132,22 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
   __syncthreads();
   if (!last) return;
   __threadfence();
-  if (threadIdx.x < 6) {
+  // Fold the block partials in a fixed order: thread t adds blocks t, t+256, ... in sequence, then
+  // the same tree as above combines the 256 thread sums.
+#pragma unroll
+  for (int q = 0; q < 6; q++) {
     double s = 0.0;
-    for (unsigned b = 0; b < gridDim.x; b++)
-      s += __hip_atomic_load(&part[(size_t)b * 6 + threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh[threadIdx.x][0] = s;
+    for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x)
+      s += __hip_atomic_load(&part[(size_t)b * 6 + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh[q][threadIdx.x] = s;
   }
   __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s)
+#pragma unroll
+      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
+    __syncthreads();
+  }
   if (threadIdx.x == 0) {
     const double dn = (double)(N > 0 ? N : 1);
     const double pg = sh[0][0] / dn, vl = sh[1][0] / dn, en = sh[2][0] / dn;

@@ -72,34 +72,99 @@ __global__ void k_normalize(const R* __restrict__ x, R* __restrict__ y, size_t n
   if (i < n) y[i] = (x[i] - stats[0]) / stats[1];
 }
 
-// Column sums of a row-major [N x J] matrix: grid (ceil(J/64), G) tiles; each block sums a chunk of
-// rows for 64 columns (coalesced row reads), partials [G][J]; k_colsum_finish adds them in order.
-__global__ void __launch_bounds__(256) k_colsum_part(const float* __restrict__ X, size_t N, int J,
-                                                     size_t ld, size_t rows_per, float* __restrict__ part) {
-  __shared__ float sh[4][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int r0 = threadIdx.x >> 6;  // 4 row lanes
-  const size_t lo = (size_t)blockIdx.y * rows_per;
-  const size_t hi = lo + rows_per < N ? lo + rows_per : N;
-  float acc = 0.f;
-  if (c < J)
-    for (size_t r = lo + r0; r < hi; r += 4) acc += X[r * ld + c];
-  sh[r0][threadIdx.x & 63] = acc;
+// Column sums of a row-major [N x J] matrix (fp32 or bf16 elements), deterministic.
+// Pass 1: grid (column blocks, G row chunks). A block is CT column threads x (256/CT) row lanes;
+// each thread owns V consecutive columns (one 16-byte fp32 / 8-byte bf16 load per row when V = 4)
+// and walks its lane's rows of the chunk; the row lanes are then added in lane order into
+// partials [G][J]. CT is sized to the matrix width so narrow matrices keep all lanes busy.
+// Pass 2: 64 columns per block, 4 lanes per column each adding every 4th partial in order, then
+// ((l0 + l1) + l2) + l3.
+__device__ inline float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ inline float4 load4(const uint16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(bf16_to_f32((uint16_t)(u.x & 0xffffu)), bf16_to_f32((uint16_t)(u.x >> 16)),
+                     bf16_to_f32((uint16_t)(u.y & 0xffffu)), bf16_to_f32((uint16_t)(u.y >> 16)));
+}
+__device__ inline float load1(const float* p) { return *p; }
+__device__ inline float load1(const uint16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T, int V>
+__global__ void __launch_bounds__(256) k_colsum_part(const T* __restrict__ X, long N, int J, long ld,
+                                                     long rows_per, int ct, float* __restrict__ part) {
+  __shared__ float4 sh[256];
+  const int cg = threadIdx.x % ct, rl = threadIdx.x / ct, nrl = 256 / ct;
+  const int c = (blockIdx.x * ct + cg) * V;
+  const long lo = (long)blockIdx.y * rows_per;
+  const long hi = lo + rows_per < N ? lo + rows_per : N;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < J && rl < nrl) {
+    if constexpr (V == 4) {
+#pragma unroll 4
+      for (long r = lo + rl; r < hi; r += nrl) {
+        const float4 v = load4(X + r * ld + c);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+    } else {
+#pragma unroll 4
+      for (long r = lo + rl; r < hi; r += nrl) acc.x += load1(X + r * ld + c);
+    }
+  }
+  sh[threadIdx.x] = acc;
   __syncthreads();
-  if (threadIdx.x < 64 && c < J) {
-    float s = ((sh[0][threadIdx.x] + sh[1][threadIdx.x]) + sh[2][threadIdx.x]) + sh[3][threadIdx.x];
-    part[(size_t)blockIdx.y * J + c] = s;
+  if (rl == 0 && c < J) {
+    float4 s4 = sh[cg];
+    for (int q = 1; q < nrl; q++) {
+      const float4 v = sh[q * ct + cg];
+      s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w;
+    }
+    float* o = part + (long)blockIdx.y * J + c;
+    o[0] = s4.x;
+    if constexpr (V == 4) { o[1] = s4.y; o[2] = s4.z; o[3] = s4.w; }
   }
 }
 
-__global__ void k_colsum_finish(const float* __restrict__ part, int G, int J, float* __restrict__ out,
-                                float scale, int accumulate) {
-  int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= J) return;
+__global__ void __launch_bounds__(256) k_colsum_finish(const float* __restrict__ part, int G, int J,
+                                                       float* __restrict__ out, float scale,
+                                                       int accumulate) {
+  __shared__ float sh[4][64];
+  const int lc = threadIdx.x & 63, ln = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lc;
   float s = 0.f;
-  for (int g = 0; g < G; g++) s += part[(size_t)g * J + c];
-  s *= scale;
-  out[c] = accumulate ? out[c] + s : s;
+  if (c < J)
+    for (int g = ln; g < G; g += 4) s += part[(long)g * J + c];
+  sh[ln][lc] = s;
+  __syncthreads();
+  if (ln == 0 && c < J) {
+    const float t = (((sh[0][lc] + sh[1][lc]) + sh[2][lc]) + sh[3][lc]) * scale;
+    out[c] = accumulate ? out[c] + t : t;
+  }
+}
+
+template <typename T>
+int colsum_t(const T* X, long N, int J, long ld, float* out, float scale, int accumulate,
+             hipStream_t st) {
+  if (J <= 0) return PH_OK;
+  const bool vec = J % 4 == 0 && ld % 4 == 0 && ((uintptr_t)X % (4 * sizeof(T))) == 0;
+  const int V = vec ? 4 : 1;
+  const int groups = (J + V - 1) / V;           // column threads needed
+  int ct = 64;
+  while (ct > 1 && ct / 2 >= groups) ct /= 2;   // narrow matrices: more row lanes per block
+  const unsigned gx = (unsigned)((groups + ct - 1) / ct);
+  long rows_per = 2048;
+  long G = (N + rows_per - 1) / rows_per;
+  if (G > 1024 / (long)gx) {
+    G = 1024 / (long)gx > 0 ? 1024 / (long)gx : 1;
+    rows_per = (N + G - 1) / G;
+  }
+  if (G < 1) G = 1;
+  float* part = (float*)scratch(kSlotColsumPart, (size_t)G * J * 4);
+  if (!part) return PH_ERR_NOMEM;
+  dim3 grid(gx, (unsigned)G);
+  if (vec) k_colsum_part<T, 4><<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, ct, part);
+  else k_colsum_part<T, 1><<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, ct, part);
+  k_colsum_finish<<<ceil_div(J, 64), 256, 0, st>>>(part, (int)G, J, out, scale, accumulate);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
 }
 
 template <typename S, typename D>
@@ -169,21 +234,12 @@ int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, 
 
 int colsum_f32(const float* X, size_t N, int J, size_t ld, float* out, float scale, int accumulate,
                hipStream_t st) {
-  if (J <= 0) return PH_OK;
-  size_t rows_per = 1024;
-  size_t G = (N + rows_per - 1) / rows_per;
-  if (G == 0) G = 1;
-  if (G > 512) {  // cap partial count; rows_per grows instead
-    G = 512;
-    rows_per = (N + G - 1) / G;
-  }
-  float* part = (float*)scratch(kSlotColsumPart, G * (size_t)J * 4);
-  if (!part) return PH_ERR_NOMEM;
-  dim3 grid(ceil_div(J, 64), (unsigned)G);
-  k_colsum_part<<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, part);
-  k_colsum_finish<<<ceil_div(J, 256), 256, 0, st>>>(part, (int)G, J, out, scale, accumulate);
-  PH_LAUNCH_CHECK();
-  return PH_OK;
+  return colsum_t<float>(X, (long)N, J, (long)ld, out, scale, accumulate, st);
+}
+
+int colsum_bf16(const uint16_t* X, long N, int J, long ld, float* out, float scale, int accumulate,
+                hipStream_t st) {
+  return colsum_t<uint16_t>(X, N, J, ld, out, scale, accumulate, st);
 }
 
 int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st) {

@@ -74,6 +74,85 @@ int ensure_zeroed_counter(unsigned* counter, hipStream_t st) {
   return PH_OK;
 }
 
+namespace {
+struct LaneTable {
+  hipStream_t s[kLanes] = {};
+  hipEvent_t fork = nullptr;
+  hipEvent_t join[kLanes] = {};
+};
+LaneTable g_lanes[kMaxDev];
+
+LaneTable* lane_table() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  return &g_lanes[dev];
+}
+
+hipEvent_t make_event(hipEvent_t& e) {
+  if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    e = nullptr;
+  }
+  return e;
+}
+}  // namespace
+
+hipStream_t lane_stream(int lane) {
+  if (lane < 0 || lane >= kLanes) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  LaneTable* t = lane_table();
+  if (!t) return nullptr;
+  if (!t->s[lane] && hipStreamCreateWithFlags(&t->s[lane], hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    t->s[lane] = nullptr;
+  }
+  return t->s[lane];
+}
+
+int fork_lanes(hipStream_t main, int n) {
+  PH_REQUIRE(n >= 0 && n <= kLanes, "fork_lanes: %d lanes", n);
+  hipEvent_t ev = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    LaneTable* t = lane_table();
+    if (t) ev = make_event(t->fork);
+  }
+  if (!ev) {
+    set_error("fork_lanes: event creation failed");
+    return PH_ERR_HIP;
+  }
+  PH_CHECK_HIP(hipEventRecord(ev, main));
+  for (int i = 0; i < n; i++) {
+    hipStream_t s = lane_stream(i);
+    if (!s) {
+      set_error("fork_lanes: stream creation failed");
+      return PH_ERR_HIP;
+    }
+    PH_CHECK_HIP(hipStreamWaitEvent(s, ev, 0));
+  }
+  return PH_OK;
+}
+
+int join_lanes(hipStream_t main, int n) {
+  PH_REQUIRE(n >= 0 && n <= kLanes, "join_lanes: %d lanes", n);
+  for (int i = 0; i < n; i++) {
+    hipEvent_t ev = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      LaneTable* t = lane_table();
+      if (t) ev = make_event(t->join[i]);
+    }
+    hipStream_t s = lane_stream(i);
+    if (!ev || !s) {
+      set_error("join_lanes: event or stream creation failed");
+      return PH_ERR_HIP;
+    }
+    PH_CHECK_HIP(hipEventRecord(ev, s));
+    PH_CHECK_HIP(hipStreamWaitEvent(main, ev, 0));
+  }
+  return PH_OK;
+}
+
 }  // namespace ph
 
 extern "C" const char* ph_last_error(void) { return ph::g_err; }

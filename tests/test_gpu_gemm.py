@@ -121,3 +121,57 @@ def test_gemm_small_dims_scalar_path(gpu, M, N, K):
         ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
         c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), math="f32").cpu().numpy()
         assert rel(c, oracle(a, b, ta, tb, M, N, K)) < 1e-5
+
+
+def _bf(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda().to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("ta,tb", FORMS)
+def test_gemm_big_tiles_ragged(gpu, ta, tb):
+    """bf16 x bf16 with >= 512 tiles of 256x128 takes the 256x128 kernel (four 128x64 wavefronts,
+    C staged in 64-row passes). Ragged M and N (not multiples of the tile) and a K tail (K % 32 = 8)."""
+    M, N, K = 4136, 4104, 264
+    a, b = operands(M, N, K, ta, tb, 300 + 2 * ta + tb)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = (ar.T if ta else ar).astype(np.float64) @ (br.T if tb else br).astype(np.float64)
+    c = D.gemm(_bf(a), _bf(b), trans_a=bool(ta), trans_b=bool(tb)).cpu().numpy()
+    assert rel(c, ref) < 1e-5
+    cb = D.gemm(_bf(a), _bf(b), trans_a=bool(ta), trans_b=bool(tb), out_dtype=torch.bfloat16)
+    assert rel(cb.float().cpu().numpy(), ref) < 4e-3
+
+
+def test_gemm_big_tiles_epilogues(gpu):
+    M, N, K = 4160, 4096, 128
+    a, b = operands(M, N, K, 0, 1, 310)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = ar.astype(np.float64) @ br.T.astype(np.float64)
+    ga, gb = _bf(a), _bf(b)
+    bias = torch.from_numpy(rng.normal(311, N).astype(np.float32)).cuda()
+    bn = bias.cpu().numpy()
+    c = D.gemm(ga, gb, trans_b=True, epilogue=L.PH_EPI_BIAS, bias=bias).cpu().numpy()
+    assert rel(c, ref + bn) < 1e-5
+    aux = torch.from_numpy(rng.normal(312, M * N).reshape(M, N).astype(np.float32)).cuda()
+    auxn = aux.cpu().numpy()
+    c = D.gemm(ga, gb, trans_b=True, epilogue=L.PH_EPI_RELU_MASK, aux=aux).cpu().numpy()
+    np.testing.assert_array_equal(c == 0, (auxn <= 0) | (ref == 0))
+    assert rel(c, np.where(auxn > 0, ref, 0)) < 1e-5
+    c2 = torch.empty((N, M), device="cuda", dtype=torch.bfloat16)
+    c = D.gemm(ga, gb, trans_b=True, epilogue=L.PH_EPI_AXPBY, aux=aux, alpha=-0.5, beta=2.0,
+               out2=c2, out2_trans=True).cpu().numpy()
+    assert rel(c, -0.5 * ref + 2.0 * auxn) < 1e-5
+    assert rel(c2.float().cpu().numpy(), c.T) < 4e-3
+
+
+@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 1)])
+def test_gemm_big_tiles_split_k(gpu, ta, tb):
+    """Few output tiles and a long reduction: split-K over 256x256 tiles (four 128x128 wavefronts,
+    C staged in 64-row passes), deterministic fold."""
+    M, N, K = 300, 520, 8232
+    a, b = operands(M, N, K, ta, tb, 320 + ta)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = (ar.T if ta else ar).astype(np.float64) @ (br.T if tb else br).astype(np.float64)
+    c = D.gemm(_bf(a), _bf(b), trans_a=bool(ta), trans_b=bool(tb)).cpu().numpy()
+    assert rel(c, ref) < 1e-5
+    c2 = D.gemm(_bf(a), _bf(b), trans_a=bool(ta), trans_b=bool(tb)).cpu().numpy()
+    assert np.array_equal(c, c2)

@@ -1,0 +1,69 @@
+"""The MinGRU PPO+Muon step captured in a HIP graph (as the benchmark runs it) replays exactly.
+
+The step forks its per-matrix Muon updates onto library stream lanes and joins them back, and its
+reductions reset their own arrival counters; a captured step must therefore reproduce the eager
+step bit for bit on every replay. Eager torch work and device synchronisations sit between the
+replays.
+"""
+import numpy as np
+import pytest
+import torch
+
+from pufferlean_amd import device as D
+from pufferlean_amd import rng
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dt=np.float32):
+    return torch.from_numpy(np.ascontiguousarray(x, dt)).cuda()
+
+
+@pytest.mark.parametrize("precision", ["bf16", "f32"])
+def test_graph_replays_match_eager(gpu, precision):
+    B, T, Dm, H, L, A = 64, 16, 8, 32, 2, 5
+    cfg = D.MinGRUConfig(B, T, Dm, H, L, A, lr=0.015, mu=0.95, max_grad_norm=0.5,
+                         gscale=1.0 / (B * T), precision=precision, math=precision)
+    n = B * T
+    p0 = rng.normal(0x900, cfg.P) * 0.1
+    obs = _t(rng.normal(0x901, n * Dm)).view(T, B, Dm)
+    act = _t(rng.randint(0x902, n, A), np.int32).view(T, B)
+    old = _t(np.log(1.0 / A) + rng.normal(0x903, n, 0.0, 0.05)).view(T, B)
+    val = _t(rng.normal(0x904, n)).view(T, B)
+    rew = _t(rng.normal(0x905, n)).view(T, B)
+    done = _t(rng.bernoulli(0x906, n, 0.05)).view(T, B)
+    logrho = _t(rng.normal(0x907, n, 0.0, 0.1)).view(T, B)
+    boot = _t(rng.normal(0x908, B))
+
+    def run_eager(p, m, g, k):
+        outs = []
+        for _ in range(k):
+            D.mingru_step(cfg, p, m, obs, act, old, val, rew, done, logrho, boot, G=g)
+            torch.cuda.synchronize()
+            outs.append((p.clone(), m.clone()))
+        return outs
+
+    # eager reference chain of 3 steps
+    ref = run_eager(_t(p0), torch.zeros(cfg.P, device="cuda"), torch.zeros(cfg.P, device="cuda"), 3)
+
+    # warm up (library buffers, lane streams) on throw-away copies, then capture one step
+    run_eager(_t(p0), torch.zeros(cfg.P, device="cuda"), torch.zeros(cfg.P, device="cuda"), 1)
+    p = _t(p0)
+    m = torch.zeros(cfg.P, device="cuda")
+    g = torch.zeros(cfg.P, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            D.mingru_step(cfg, p, m, obs, act, old, val, rew, done, logrho, boot, G=g)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    # capture records work without running it: the parameters are still the initial ones
+    assert torch.equal(p, _t(p0))
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = (torch.ones(1000, device="cuda") * 2).sum().item()  # eager work between replays
+        assert torch.equal(p, ref[k][0]), f"replay {k}: parameters differ from the eager step"
+        assert torch.equal(m, ref[k][1]), f"replay {k}: momentum differs from the eager step"
