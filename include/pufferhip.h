@@ -180,6 +180,112 @@ int ph_mingru_step(const ph_mingru_dims* d, const ph_ppo_coefs* c, const ph_muon
                    const float* oldval, const float* rew, const float* done, const float* logrho,
                    const float* boot, float* G, double* losses, void* stream);
 
+/* ============================================================================================== */
+/* Host-buffer entry points (layer 2). Each replaces the reference GPU symbol named beside it, with
+ * the same argument order and meaning; FloatArray inputs become host `const double*`, the returned
+ * FloatArray a caller-allocated `double*` of the stated length. All synchronise before returning.
+ * Where the reference falls back to its CPU path or returns zeros, these return an error status.
+ * Policy handles are device addresses of a [params(P); mom(P)] f64 buffer, as in the reference. */
+
+/* lean_cuda_vtrace (puffercuda.cu:94-136): vec-form V-trace over segment-major [B][T] f64 arrays;
+ * imp is the importance ratio, rewards clamped to [-1,1]. adv: B*T. */
+int ph_cuda_vtrace(const double* rew, const double* val, const double* term, const double* imp,
+                   size_t B, size_t T, double gamma, double lam, double rhoClip, double cClip,
+                   double* adv);
+/* lean_cuda_vtrace_mingru (puffercuda.cu:168-216): bootstrapped form with bootv[B]. adv: B*T. */
+int ph_cuda_vtrace_mingru(const double* rew, const double* val, const double* term, const double* imp,
+                          const double* bootv, size_t B, size_t T, double gamma, double lam,
+                          double rhoClip, double cClip, double* adv);
+/* lean_cuda_adv_normalize (puffercuda.cu:836-855): (adv - mean) / (pop-std + 1e-8). out: n. */
+int ph_cuda_adv_normalize(const double* adv, size_t n, double* out);
+/* lean_cuda_mlp_ppo_grad (puffercuda.cu:748-820): summed PPO gradient of the one-hidden-layer MLP
+ * (flattenMLP params W1[H*D] | b1[H] | W2[O*H] | b2[O], O = A+1). bf16: bf16-MFMA GEMMs on fp32
+ * operands, else fp32 MFMA. g: P = H*D + H + O*H + O. */
+int ph_cuda_mlp_ppo_grad(const double* params, const double* obs, const double* acts,
+                         const double* advs, const double* rets, const double* oldlps, size_t N,
+                         size_t H, size_t D, size_t A, double vfCoef, double entCoef, double clipEps,
+                         uint8_t bf16, double* g);
+/* lean_cuda_train_step (puffercuda.cu:988-1090): pm = [params; mom] (2P); adv-normalise, gradient,
+ * mean over N, Muon (the reference's 5-triple schedule; bf16: fp32-MFMA Newton-Schulz with f64
+ * state, else the exact f64 tier) on W1, W2, stepvec on b1, b2. out: [newParams; newMom] (2P). */
+int ph_cuda_train_step(const double* pm, const double* obs, const double* acts, const double* advRaw,
+                       const double* rets, const double* oldlps, size_t N, size_t H, size_t D,
+                       size_t A, double lr, double wd, double mu, double eps, double vfCoef,
+                       double entCoef, double clipEps, uint8_t bf16, double* out);
+/* lean_cuda_train_update (puffercuda.cu:1094-1172): epochs x numMB minibatches (perm: epochs*NT row
+ * indices as doubles), exact f64 Muon. out: [params; mom] (2P). */
+int ph_cuda_train_update(const double* pm, const double* obs, const double* acts, const double* adv,
+                         const double* ret, const double* olp, const double* perm, size_t NT,
+                         size_t D, size_t H, size_t A, size_t epochs, size_t numMB, double lr,
+                         double wd, double mu, double eps, double vfCoef, double entCoef,
+                         double clipEps, uint8_t bf16, double* out);
+/* lean_cuda_train_update_resident (puffercuda.cu:1187-1290): as above on a policy handle, in place,
+ * with the value-loss clip (when vfClip > 0 and ovN >= NT) and the global grad-norm clip
+ * (maxGradNorm > 0); bf16 also selects the fp32-MFMA Newton-Schulz. Fills the dashboard-loss channel
+ * on the last minibatch when enabled. out1: params[0]. */
+int ph_cuda_train_update_resident(size_t policyH, const double* obs, const double* acts,
+                                  const double* adv, const double* ret, const double* olp,
+                                  const double* ov, size_t ovN, const double* perm, size_t NT, size_t D,
+                                  size_t H, size_t A, size_t epochs, size_t numMB, double lr, double wd,
+                                  double mu, double eps, double vfCoef, double entCoef, double clipEps,
+                                  double vfClip, double maxGradNorm, uint8_t bf16, double* out1);
+/* lean_cuda_muon_stepmat (puffercuda.cu:557-631): exact f64 Muon of one matrix. out: [newW; newMom]. */
+int ph_cuda_muon_stepmat(const double* W, const double* G, const double* M, size_t rows, size_t cols,
+                         double lr, double wd, double mu, double eps, double* out);
+/* lean_cuda_muon_step_mlp_resident (puffercuda.cu:5985-6011): gRaw (P) scaled by gscale, exact f64
+ * Muon on the handle in place. newParams: P. */
+int ph_cuda_muon_step_mlp_resident(size_t policyH, const double* gRaw, size_t H, size_t D, size_t O,
+                                   double gscale, double lr, double wd, double mu, double eps,
+                                   double* newParams);
+/* lean_cuda_policy_load / _download / _free (puffercuda.cu:6100-6116). */
+int ph_cuda_policy_load(const double* pm, size_t P, size_t* handle);
+int ph_cuda_policy_download(size_t handle, size_t P, double* pm);
+int ph_cuda_policy_free(size_t handle);
+/* lean_cuda_mg_loss_enable / lean_cuda_mg_read_losses (puffercuda.cu:336-352): the 7 dashboard
+ * losses (policy, value, entropy, total, old_kl, kl, clipfrac) of the last surfaced minibatch. */
+int ph_cuda_mg_loss_enable(uint8_t on);
+int ph_cuda_mg_read_losses(double* out7);
+extern int g_mgLossOn;      /* link-time contract of pufferblas.c:38-39 */
+extern double g_mgLoss[7];
+/* pufferblas.c:46-50 link-time contract: always 0 here (the GPU LSTM BPTT is not in this library),
+ * which makes pufferblas.c take its CPU path. */
+int cuda_lstm_ppo_grad_batch(const double* pp, const double* obsB, const double* actA,
+                             const double* advA, const double* retA, const double* oldA,
+                             const double* termA, const double* h0s, const double* c0s, size_t B,
+                             size_t T, size_t H, size_t D, size_t A, double vfCoef, double entCoef,
+                             double clipEps, double* gOut, double* outHostOrNull, int tier);
+/* lean_ffi_dense_forward_cublas (pufferblas.c:111-147): Y = relu(X W^T + b), f64 (each dot product
+ * an ascending fold, the order of lean_ffi_dense_forward_ref). Y: N*H. */
+int ph_ffi_dense_forward_gpu(const double* X, const double* W, const double* b, size_t N, size_t D,
+                             size_t H, double* Y);
+/* lean_ffi_dense_forward_cublaslt_bf16 (pufferblas.c:190-249): bf16 (RNE) operands, fp32 MFMA
+ * accumulate, bias and ReLU in f64. Y: N*H. */
+int ph_ffi_dense_forward_bf16(const double* X, const double* W, const double* b, size_t N, size_t D,
+                              size_t H, double* Y);
+/* lean_ffi_mlp_forward_batch_cublaslt_bf16 (pufferblas.c:373-416): flattenMLP forward, bf16 MFMA on
+ * fp32 operands, fused bias+ReLU / bias. Y: N*O. */
+int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, size_t D, size_t H,
+                                  size_t O, double* Y);
+/* lean_ffi_bench_cublaslt_bf16_resident (pufferblas.c:256-292): device-resident bf16 dense-layer
+ * GFLOP/s over reps launches; -1 without a device. */
+double ph_ffi_bench_bf16_resident(size_t N, size_t D, size_t H, size_t reps);
+/* lean_ffi_cuda_available (pufferblas.c:1348-1352). */
+uint8_t ph_ffi_cuda_available(void);
+/* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206), host mode: params (flattenMG, P), obs (nobs >=
+ * T*B*D, time-major), scal = [act|adv|ret|old|term|ov] (nscal >= 6*T*B), K = 1, no segment indices
+ * (nseg = 0) or priorities (nprio = 0). out: [g (P); new_logp (T*B); new_value (T*B)]. Precision:
+ * bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
+int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
+                            size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L, size_t A,
+                            size_t K, double vfCoef, double entCoef, double clipEps, double vfClip,
+                            size_t nseg, size_t nprio, double* out);
+/* lean_cuda_mingru_muon_resident (puffercuda.cu:5727), host-gradient mode: gClip (nG >= P) is the
+ * clipped gradient; Muon on every flattenMG matrix of the handle (fp32-MFMA Newton-Schulz on f64
+ * state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the biases, in place. wOut: P. */
+int ph_cuda_mingru_muon_resident(size_t policyH, const double* gClip, size_t nG, size_t H, size_t D,
+                                 size_t L, size_t A, double lr, double wd, double mu, double eps,
+                                 double maxGradNorm, double gscale, double* wOut);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,8 +62,35 @@ SIGNATURES: dict[str, list] = {
     "ph_mingru_ppo_grad": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_mingru_muon": [vp, vp, vp, vp, vp, vp],
     "ph_mingru_step": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    # host-buffer layer (reference Lean @[extern] GPU symbols)
+    "ph_cuda_vtrace": [dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_vtrace_mingru": [dptr, dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_adv_normalize": [dptr, sz, dptr],
+    "ph_cuda_mlp_ppo_grad": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, u8, dptr],
+    "ph_cuda_train_step": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl,
+                           dbl, u8, dptr],
+    "ph_cuda_train_update": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, sz, sz, dbl, dbl, dbl,
+                             dbl, dbl, dbl, dbl, u8, dptr],
+    "ph_cuda_train_update_resident": [sz, dptr, dptr, dptr, dptr, dptr, dptr, sz, dptr, sz, sz, sz, sz, sz,
+                                      sz, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, u8, dptr],
+    "ph_cuda_muon_stepmat": [dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_muon_step_mlp_resident": [sz, dptr, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_policy_load": [dptr, sz, szptr],
+    "ph_cuda_policy_download": [sz, sz, dptr],
+    "ph_cuda_policy_free": [sz],
+    "ph_cuda_mg_loss_enable": [u8],
+    "ph_cuda_mg_read_losses": [dptr],
+    "ph_ffi_dense_forward_gpu": [dptr, dptr, dptr, sz, sz, sz, dptr],
+    "ph_ffi_dense_forward_bf16": [dptr, dptr, dptr, sz, sz, sz, dptr],
+    "ph_ffi_mlp_forward_batch_bf16": [dptr, dptr, sz, sz, sz, sz, dptr],
+    "ph_ffi_bench_bf16_resident": [sz, sz, sz, sz],
+    "ph_ffi_cuda_available": [],
+    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, sz,
+                                sz, dptr],
+    "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }
-_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long}
+_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long,
+             "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_cuda_available": C.c_uint8}
 
 _lib = None
 _lock = threading.Lock()

@@ -1,0 +1,853 @@
+// Host-buffer entry points: one per GPU symbol the reference's Lean side binds with @[extern]
+// (Puffer/Float/CUDA.lean, Puffer/Float/BLAS.lean; C bodies in ffi/puffercuda.cu, ffi/pufferblas.c).
+//
+// Each takes the reference symbol's arguments with every Lean FloatArray turned into a host
+// `const double*` (input) or a caller-allocated `double*` (output of the documented size), uploads,
+// runs the device kernels of this library on the default stream, downloads and synchronises, as the
+// reference entries do. Differences from the reference, by design:
+//   - no CPU fallback and no zero-filled result: a failure returns a ph_status and sets
+//     ph_last_error(), and the outputs are unspecified;
+//   - device buffers are library-owned scratch reused across calls (the reference's ts_buf / bg / rb2
+//     caches play the same role).
+#include <cmath>
+#include <cstdlib>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+// The shared dashboard-loss channel (policy, value, entropy, total, old_kl, kl, clipfrac): defined
+// here with external linkage because the reference's pufferblas.c declares it extern
+// (pufferblas.c:38-39; defined at puffercuda.cu:261-262).
+extern "C" {
+int g_mgLossOn = 0;
+double g_mgLoss[7] = {0, 0, 0, 0, 0, 0, 0};
+}
+
+namespace ph {
+namespace {
+
+constexpr unsigned kT = 256;
+
+// The reference's Newton-Schulz coefficient schedule, one triple per step (pufferblas.c:1362-1364,
+// puffercuda.cu:520-525).
+const double kRefCoeffs[15] = {4.0848, -6.8946, 2.9270, 3.9505, -6.3029, 2.6377, 3.7418, -5.5913,
+                               2.3037, 2.8769, -3.1427, 1.2046, 2.8366, -3.0525, 1.2012};
+const float kRefCoeffsF[15] = {4.0848f, -6.8946f, 2.9270f, 3.9505f, -6.3029f, 2.6377f, 3.7418f, -5.5913f,
+                               2.3037f, 2.8769f, -3.1427f, 1.2046f, 2.8366f, -3.0525f, 1.2012f};
+
+enum : int {
+  kHsVtrace = kSlotHost,
+  kHsMlp = kSlotHost + 1,     // MLP minibatch working set
+  kHsState = kSlotHost + 2,   // f64 parameter / momentum / gradient state of the non-resident steps
+  kHsCols = kSlotHost + 3,    // whole-update columns + permutation
+  kHsMuonU = kSlotHost + 4,   // f32 Newton-Schulz input of the mixed-precision Muon
+  kHsMg = kSlotHost + 5,      // MinGRU host-mode staging
+  kHsDense = kSlotHost + 6,
+  kHsLoss = kSlotHost + 7,
+  kHsClip = kSlotHost + 8,
+  kHsGrad = kSlotHost + 9,    // uploaded f64 gradient of the resident Muon entries
+  kHsMgOut = kSlotHost + 10,  // MinGRU host-mode result staging
+};
+
+// Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
+// again to assign.
+struct Carve {
+  uint8_t* base = nullptr;
+  size_t off = 0;
+  template <typename T>
+  T* take(size_t n) {
+    const size_t o = off;
+    off += (n * sizeof(T) + 255) & ~(size_t)255;
+    return base ? reinterpret_cast<T*>(base + o) : nullptr;
+  }
+};
+template <typename F>
+int carve(int slot, F&& layout) {
+  Carve c0;
+  layout(c0);
+  void* p = scratch(slot, c0.off);
+  if (!p) return PH_ERR_NOMEM;
+  Carve c1;
+  c1.base = (uint8_t*)p;
+  layout(c1);
+  return PH_OK;
+}
+
+int up(void* d, const void* h, size_t bytes) {
+  if (bytes) PH_CHECK_HIP(hipMemcpy(d, h, bytes, hipMemcpyHostToDevice));
+  return PH_OK;
+}
+int down(void* h, const void* d, size_t bytes) {
+  if (bytes) PH_CHECK_HIP(hipMemcpy(h, d, bytes, hipMemcpyDeviceToHost));
+  return PH_OK;
+}
+int finish() {
+  PH_CHECK_HIP(hipDeviceSynchronize());
+  return PH_OK;
+}
+
+// ---- element kernels ---------------------------------------------------------------------------
+__global__ void k_f64_f32(const double* __restrict__ x, float* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (float)x[i];
+}
+__global__ void k_f32_f64(const float* __restrict__ x, double* __restrict__ y, long n, double scale) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (double)x[i] * scale;
+}
+__global__ void k_f64_i32(const double* __restrict__ x, int* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (int)x[i];
+}
+// dst row k = src row idx[k] (the permutation holds row indices as doubles, read as (int)).
+__global__ void k_gather_rows(const float* __restrict__ src, const double* __restrict__ idx,
+                              float* __restrict__ dst, long n, int cols) {
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * cols) return;
+  const long k = t / cols;
+  const int j = (int)(t % cols);
+  dst[t] = src[(long)(int)idx[k] * cols + j];
+}
+// Minibatch columns: actions as int, the rest as the f32 the loss kernel computes in.
+__global__ void k_gather_cols(const double* __restrict__ idx, long n, const double* __restrict__ act,
+                              const double* __restrict__ adv, const double* __restrict__ ret,
+                              const double* __restrict__ old, const double* __restrict__ ov,
+                              int* __restrict__ gact, double* __restrict__ gadv, float* __restrict__ gret,
+                              float* __restrict__ gold, float* __restrict__ gov) {
+  const long k = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n) return;
+  const long r = idx ? (long)(int)idx[k] : k;
+  gact[k] = (int)act[r];
+  gadv[k] = adv[r];
+  gret[k] = (float)ret[r];
+  gold[k] = (float)old[r];
+  if (ov) gov[k] = (float)ov[r];
+}
+__global__ void k_bias_relu_f64(double* __restrict__ Y, const double* __restrict__ b, long N, int H,
+                                int relu) {
+#pragma clang fp contract(off)
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N * H) return;
+  const double v = Y[i] + b[i % H];
+  Y[i] = relu ? (v > 0.0 ? v : 0.0) : v;
+}
+// Y[N x H] = relu(X W^T + b) in f64, each dot product an ascending fold over d (the reference's
+// left-folded scalar order, pufferblas.c:65-80).
+__global__ void k_dense_f64(const double* __restrict__ X, const double* __restrict__ W,
+                            const double* __restrict__ b, double* __restrict__ Y, long N, int D, int H) {
+#pragma clang fp contract(off)
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * H) return;
+  const long i = t / H;
+  const int j = (int)(t % H);
+  const double* xr = X + i * D;
+  const double* wr = W + (long)j * D;
+  double acc = 0.0;
+  for (int d = 0; d < D; d++) acc += xr[d] * wr[d];
+  const double v = acc + b[j];
+  Y[t] = v > 0.0 ? v : 0.0;
+}
+__global__ void k_f64_bf16(const double* __restrict__ x, uint16_t* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = bf16_rne((float)x[i]);
+}
+
+// Mixed-precision Muon pieces: f64 momentum and weights, f32 orthogonalisation input.
+__global__ void k_nesterov_mixed(const double* __restrict__ G, double* __restrict__ M,
+                                 float* __restrict__ U, long n, double gscale, double mu) {
+#pragma clang fp contract(off)
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double gi = G[i] * gscale;
+  const double m = mu * M[i] + gi;
+  M[i] = m;
+  U[i] = (float)(gi + mu * m);
+}
+__global__ void k_finalize_mixed(double* __restrict__ W, const float* __restrict__ X, long n, double c1,
+                                 double c2) {
+#pragma clang fp contract(off)
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) W[i] = c1 * W[i] + c2 * (double)X[i];
+}
+
+// Gradient-norm clip on an f64 vector (PufferLib clip_grad_norm_ over all parameters; the
+// reference's k_gclip_norm/k_gclip_scale, puffercuda.cu:5122-5131): s = sum (g*sc)^2 in fixed
+// chunks, folded in chunk order; cc = (maxNorm > 0 and sqrt(s) > maxNorm ? maxNorm/sqrt(s) : 1)*sc.
+__global__ void __launch_bounds__(256) k_sq_part_f64(const double* __restrict__ g, long n, long chunk,
+                                                     double sc, double* __restrict__ part) {
+  __shared__ double sh[256];
+  const long lo = (long)blockIdx.x * chunk;
+  const long hi = lo + chunk < n ? lo + chunk : n;
+  double s = 0.0;
+  for (long i = lo + threadIdx.x; i < hi; i += 256) {
+    const double x = g[i] * sc;
+    s += x * x;
+  }
+  sh[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
+}
+__global__ void k_clip_scale_f64(double* __restrict__ g, long n, const double* __restrict__ part, int G,
+                                 double maxNorm, double sc) {
+  __shared__ double cc;
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int q = 0; q < G; q++) s += part[q];
+    const double gn = sqrt(s);
+    cc = ((maxNorm > 0.0 && gn > maxNorm) ? maxNorm / gn : 1.0) * sc;
+  }
+  __syncthreads();
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    g[i] = g[i] * cc;
+}
+__global__ void k_scale_f64v(double* __restrict__ g, long n, double sc) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) g[i] = sc * g[i];
+}
+
+int to_f32(const double* d, float* f, long n, hipStream_t st) {
+  if (n <= 0) return PH_OK;
+  k_f64_f32<<<ceil_div(n, kT), kT, 0, st>>>(d, f, n);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+// ---- one-hidden-layer MLP policy (flattenMLP: W1[H*D] | b1[H] | W2[O*H] | b2[O], O = A + 1) --------
+struct MlpShape {
+  long N;
+  int H, D, A, O;
+  long P, oW1, ob1, oW2, ob2;
+};
+MlpShape mlp_shape(size_t N, size_t H, size_t D, size_t A) {
+  MlpShape s;
+  s.N = (long)N; s.H = (int)H; s.D = (int)D; s.A = (int)A; s.O = (int)A + 1;
+  s.oW1 = 0; s.ob1 = (long)H * D; s.oW2 = s.ob1 + (long)H; s.ob2 = s.oW2 + (long)s.O * H;
+  s.P = s.ob2 + s.O;
+  return s;
+}
+
+struct MlpWork {
+  float *X, *Wf, *H1, *Out, *dOut, *dZ, *gf, *ret, *old, *ov;
+  int* act;
+  double *adv, *advn, *stats, *losses;
+};
+int mlp_work(const MlpShape& s, long Nmax, MlpWork& w) {
+  return carve(kHsMlp, [&](Carve& c) {
+    w.X = c.take<float>((size_t)Nmax * s.D);
+    w.Wf = c.take<float>(s.P);
+    w.H1 = c.take<float>((size_t)Nmax * s.H);
+    w.Out = c.take<float>((size_t)Nmax * s.O);
+    w.dOut = c.take<float>((size_t)Nmax * s.O);
+    w.dZ = c.take<float>((size_t)Nmax * s.H);
+    w.gf = c.take<float>(s.P);
+    w.ret = c.take<float>(Nmax);
+    w.old = c.take<float>(Nmax);
+    w.ov = c.take<float>(Nmax);
+    w.act = c.take<int>(Nmax);
+    w.adv = c.take<double>(Nmax);
+    w.advn = c.take<double>(Nmax);
+    w.stats = c.take<double>(8);
+    w.losses = c.take<double>(8);
+  });
+}
+
+PhGemmDesc f32desc(int ta, int tb, long M, long N, long K, const float* A, long lda, const float* B, long ldb,
+                   float* C, long ldc, int math) {
+  PhGemmDesc d{};
+  d.trans_a = ta; d.trans_b = tb; d.M = (int)M; d.N = (int)N; d.K = (int)K;
+  d.a_dtype = PH_F32; d.A = A; d.lda = lda; d.b_dtype = PH_F32; d.B = B; d.ldb = ldb;
+  d.c_dtype = PH_F32; d.C = C; d.ldc = ldc; d.math = math; d.alpha = 1.f;
+  return d;
+}
+
+// Summed PPO gradient of one minibatch into w.gf (f32, flattenMLP layout). Inputs in w: X [N][D],
+// Wf [P], act, adv (f64, already normalised if the caller wants), ret, old, ov (or use_ov = 0).
+// Follows lean_cuda_mlp_ppo_grad (puffercuda.cu:748-820): H1 = relu(X W1^T + b1); Out = H1 W2^T + b2;
+// dOut by the fused PPO loss (no max shift, as k_ppo_dout); gb2 = colsum dOut; gW2 = dOut^T H1;
+// dZ = (dOut W2) masked by H1 > 0; gb1 = colsum dZ; gW1 = dZ^T X. `bf`: bf16 MFMA on the fp32
+// operands (the reference's FAST_16BF), else fp32 MFMA.
+int mlp_grad_dev(const MlpShape& s, long N, const MlpWork& w, int bf, double vf, double ent, double clip,
+                 double vfClip, bool use_ov, double* losses, hipStream_t st) {
+  const int math = bf ? PH_MATH_BF16 : PH_MATH_F32;
+  const float* W1 = w.Wf + s.oW1;
+  const float* b1 = w.Wf + s.ob1;
+  const float* W2 = w.Wf + s.oW2;
+  const float* b2 = w.Wf + s.ob2;
+  // advantages as the f32 the loss computes in, staged in dZ's first N floats (dZ is written only
+  // by the dgrad GEMM, after the loss kernel has read them)
+  float* advf = w.dZ;
+  PH_TRY(to_f32(w.advn, advf, N, st));
+  PhGemmDesc g = f32desc(0, 1, N, s.H, s.D, w.X, s.D, W1, s.D, w.H1, s.H, math);
+  g.epi = PH_EPI_BIAS_RELU; g.bias = b1;
+  PH_TRY(gemm(g, st));
+  g = f32desc(0, 1, N, s.O, s.H, w.H1, s.H, W2, s.H, w.Out, s.O, math);
+  g.epi = PH_EPI_BIAS; g.bias = b2;
+  PH_TRY(gemm(g, st));
+  PH_TRY(ppo_grad(w.Out, s.O, w.Out + s.A, s.O, w.act, advf, w.ret, w.old, use_ov ? w.ov : nullptr, N,
+                  s.A, (float)vf, (float)ent, (float)clip, (float)vfClip, 0, w.dOut, s.O, w.dOut + s.A,
+                  s.O, nullptr, nullptr, losses, st));
+  PH_TRY(colsum_f32(w.dOut, N, s.O, s.O, w.gf + s.ob2, 1.f, 0, st));
+  PH_TRY(gemm(f32desc(1, 0, s.O, s.H, N, w.dOut, s.O, w.H1, s.H, w.gf + s.oW2, s.H, math), st));
+  g = f32desc(0, 0, N, s.H, s.O, w.dOut, s.O, W2, s.H, w.dZ, s.H, math);
+  g.epi = PH_EPI_RELU_MASK; g.aux = w.H1; g.ldaux = s.H;
+  PH_TRY(gemm(g, st));
+  PH_TRY(colsum_f32(w.dZ, N, s.H, s.H, w.gf + s.ob1, 1.f, 0, st));
+  PH_TRY(gemm(f32desc(1, 0, s.H, s.D, N, w.dZ, s.H, w.X, s.D, w.gf + s.oW1, s.D, math), st));
+  return PH_OK;
+}
+
+// Muon on an f64 [rows x cols] matrix in place: exact tier (f64 Newton-Schulz, the reference's op
+// order) or mixed tier (f64 momentum and weights, f32-MFMA Newton-Schulz, as muon_mat_dev_bf,
+// puffercuda.cu:942-966).
+int muon_f64(int rows, int cols, double* W, const double* G, double* M, double gscale, double lr,
+             double wd, double mu, double eps, bool mixed, hipStream_t st) {
+  const long n = (long)rows * cols;
+  if (n == 0) return PH_OK;
+  if (!mixed)
+    return muon_mat_exact(rows, cols, W, G, M, W, M, gscale, lr, wd, mu, eps, kRefCoeffs, 5, st);
+  float* U = (float*)scratch(kHsMuonU, (size_t)n * 4);
+  if (!U) return PH_ERR_NOMEM;
+  k_nesterov_mixed<<<ceil_div(n, kT), kT, 0, st>>>(G, M, U, n, gscale, mu);
+  PH_LAUNCH_CHECK();
+  PH_TRY(newton_schulz_fast(U, rows, cols, kRefCoeffsF, 5, (float)eps, PH_MATH_F32, kSlotNs, 0, st));
+  const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
+  k_finalize_mixed<<<ceil_div(n, kT), kT, 0, st>>>(W, U, n, 1.0 - lr * wd, lr * scale);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+int stepvec_f64(long n, double* b, const double* g, double* m, double gscale, double lr, double wd,
+                double mu, hipStream_t st) {
+  return stepvec_exact(n, b, g, m, b, m, gscale, lr, wd, mu, st);
+}
+// Whole-MLP Muon over [params | mom] in place (W1, W2 orthogonalised; b1, b2 by stepvec).
+int mlp_muon(const MlpShape& s, double* par, double* mom, const double* G, double gscale, double lr,
+             double wd, double mu, double eps, bool mixed, hipStream_t st) {
+  PH_TRY(muon_f64(s.H, s.D, par + s.oW1, G + s.oW1, mom + s.oW1, gscale, lr, wd, mu, eps, mixed, st));
+  PH_TRY(stepvec_f64(s.H, par + s.ob1, G + s.ob1, mom + s.ob1, gscale, lr, wd, mu, st));
+  PH_TRY(muon_f64(s.O, s.H, par + s.oW2, G + s.oW2, mom + s.oW2, gscale, lr, wd, mu, eps, mixed, st));
+  PH_TRY(stepvec_f64(s.O, par + s.ob2, G + s.ob2, mom + s.ob2, gscale, lr, wd, mu, st));
+  return PH_OK;
+}
+
+int gclip_f64(double* g, long n, double sc, double maxNorm, hipStream_t st) {
+  if (n == 0) return PH_OK;
+  const long chunk = 16384;
+  const int G = (int)((n + chunk - 1) / chunk);
+  double* part = (double*)scratch(kHsClip, (size_t)G * 8);
+  if (!part) return PH_ERR_NOMEM;
+  k_sq_part_f64<<<G, 256, 0, st>>>(g, n, chunk, sc, part);
+  unsigned grid = ceil_div(n, 256);
+  if (grid > 2048) grid = 2048;
+  k_clip_scale_f64<<<grid, 256, 0, st>>>(g, n, part, G, maxNorm, sc);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
+// Minibatch-sized f64 state of a non-resident step: params | mom | G.
+struct State {
+  double *par, *mom, *G;
+};
+int state_bufs(long P, State& t) {
+  return carve(kHsState, [&](Carve& c) {
+    t.par = c.take<double>(2 * P);
+    t.mom = t.par ? t.par + P : nullptr;
+    t.G = c.take<double>(P);
+  });
+}
+
+// One minibatch of the PPO+Muon update on device-resident state: gather (idx may be null: rows 0..N-1
+// of the columns), normalise the advantages, gradient, mean (and optional clip), Muon in place.
+struct Cols {
+  float* obs;  // [NT][D]
+  const double *act, *adv, *ret, *old, *ov;
+};
+int mlp_minibatch(const MlpShape& s, const Cols& cols, const double* idx, long Nmb, MlpWork& w,
+                  double* par, double* mom, double* G, int bf, bool mixed, double lr, double wd, double mu,
+                  double eps, double vf, double ent, double clip, double vfClip, double maxGradNorm,
+                  bool want_losses, hipStream_t st) {
+  const bool use_ov = cols.ov != nullptr && vfClip > 0.0;
+  if (idx) {
+    k_gather_rows<<<ceil_div(Nmb * s.D, kT), kT, 0, st>>>(cols.obs, idx, w.X, Nmb, s.D);
+  } else {
+    PH_CHECK_HIP(hipMemcpyAsync(w.X, cols.obs, (size_t)Nmb * s.D * 4, hipMemcpyDeviceToDevice, st));
+  }
+  k_gather_cols<<<ceil_div(Nmb, kT), kT, 0, st>>>(idx, Nmb, cols.act, cols.adv, cols.ret, cols.old,
+                                                 use_ov ? cols.ov : nullptr, w.act, w.adv, w.ret, w.old,
+                                                 w.ov);
+  PH_LAUNCH_CHECK();
+  PH_TRY(moments_normalize(PH_F64, w.adv, Nmb, w.advn, w.stats, st));
+  PH_TRY(to_f32(par, w.Wf, s.P, st));
+  PH_TRY(mlp_grad_dev(s, Nmb, w, bf, vf, ent, clip, vfClip, use_ov, want_losses ? w.losses : nullptr, st));
+  k_f32_f64<<<ceil_div(s.P, kT), kT, 0, st>>>(w.gf, G, s.P, 1.0);
+  PH_LAUNCH_CHECK();
+  double gscale = 1.0 / (double)Nmb;
+  if (maxGradNorm > 0.0) {
+    PH_TRY(gclip_f64(G, s.P, gscale, maxGradNorm, st));
+    gscale = 1.0;
+  }
+  PH_TRY(mlp_muon(s, par, mom, G, gscale, lr, wd, mu, eps, mixed, st));
+  if (want_losses) PH_TRY(down(g_mgLoss, w.losses, 7 * 8));
+  return PH_OK;
+}
+
+bool env_is(const char* name, const char* val) {
+  const char* e = getenv(name);
+  return e && strcmp(e, val) == 0;
+}
+
+}  // namespace
+}  // namespace ph
+
+using namespace ph;
+
+// ---- V-trace / advantage normalisation --------------------------------------------------------
+extern "C" int ph_cuda_vtrace(const double* rew, const double* val, const double* term, const double* imp,
+                              size_t B, size_t T, double gamma, double lam, double rhoClip, double cClip,
+                              double* adv) {
+  PH_REQUIRE(B * T == 0 || (rew && val && term && imp && adv), "ph_cuda_vtrace: null buffer");
+  if (B * T == 0) return PH_OK;
+  const size_t n = B * T;
+  double *dR, *dV, *dT, *dI, *dA;
+  PH_TRY(carve(kHsVtrace, [&](Carve& c) {
+    dR = c.take<double>(n); dV = c.take<double>(n); dT = c.take<double>(n); dI = c.take<double>(n);
+    dA = c.take<double>(n);
+  }));
+  PH_TRY(up(dR, rew, n * 8)); PH_TRY(up(dV, val, n * 8)); PH_TRY(up(dT, term, n * 8)); PH_TRY(up(dI, imp, n * 8));
+  PH_TRY(ph_vtrace(PH_F64, dR, dV, dT, dI, nullptr, B, T, 0, 0, 0, 1, gamma, lam, rhoClip, cClip, dA,
+                   nullptr, nullptr));
+  PH_TRY(finish());
+  return down(adv, dA, n * 8);
+}
+
+extern "C" int ph_cuda_vtrace_mingru(const double* rew, const double* val, const double* term,
+                                     const double* imp, const double* bootv, size_t B, size_t T,
+                                     double gamma, double lam, double rhoClip, double cClip, double* adv) {
+  PH_REQUIRE(B * T == 0 || (rew && val && term && imp && bootv && adv), "ph_cuda_vtrace_mingru: null buffer");
+  if (B * T == 0) return PH_OK;
+  const size_t n = B * T;
+  double *dR, *dV, *dT, *dI, *dB, *dA;
+  PH_TRY(carve(kHsVtrace, [&](Carve& c) {
+    dR = c.take<double>(n); dV = c.take<double>(n); dT = c.take<double>(n); dI = c.take<double>(n);
+    dB = c.take<double>(B); dA = c.take<double>(n);
+  }));
+  PH_TRY(up(dR, rew, n * 8)); PH_TRY(up(dV, val, n * 8)); PH_TRY(up(dT, term, n * 8));
+  PH_TRY(up(dI, imp, n * 8)); PH_TRY(up(dB, bootv, B * 8));
+  PH_TRY(ph_vtrace(PH_F64, dR, dV, dT, dI, dB, B, T, 1, 0, 0, 1, gamma, lam, rhoClip, cClip, dA, nullptr,
+                   nullptr));
+  PH_TRY(finish());
+  return down(adv, dA, n * 8);
+}
+
+extern "C" int ph_cuda_adv_normalize(const double* adv, size_t n, double* out) {
+  PH_REQUIRE(n == 0 || (adv && out), "ph_cuda_adv_normalize: null buffer");
+  if (n == 0) return PH_OK;
+  double *dA, *dO, *dS;
+  PH_TRY(carve(kHsVtrace, [&](Carve& c) {
+    dA = c.take<double>(n); dO = c.take<double>(n); dS = c.take<double>(8);
+  }));
+  PH_TRY(up(dA, adv, n * 8));
+  PH_TRY(moments_normalize(PH_F64, dA, n, dO, dS, nullptr));
+  PH_TRY(finish());
+  return down(out, dO, n * 8);
+}
+
+// ---- MLP PPO gradient and whole steps -----------------------------------------------------------
+extern "C" int ph_cuda_mlp_ppo_grad(const double* params, const double* obs, const double* acts,
+                                    const double* advs, const double* rets, const double* oldlps, size_t N,
+                                    size_t H, size_t D, size_t A, double vfCoef, double entCoef,
+                                    double clipEps, uint8_t bf16, double* g) {
+  PH_REQUIRE(N > 0 && H > 0 && D > 0 && A >= 1 && A <= 64, "ph_cuda_mlp_ppo_grad: bad shape");
+  PH_REQUIRE(params && obs && acts && advs && rets && oldlps && g, "ph_cuda_mlp_ppo_grad: null buffer");
+  const MlpShape s = mlp_shape(N, H, D, A);
+  MlpWork w;
+  PH_TRY(mlp_work(s, s.N, w));
+  double *dp, *dx, *dc, *dg;
+  PH_TRY(carve(kHsCols, [&](Carve& c) {
+    dp = c.take<double>(s.P); dx = c.take<double>((size_t)N * D); dc = c.take<double>(4 * N);
+    dg = c.take<double>(s.P);
+  }));
+  PH_TRY(up(dp, params, s.P * 8)); PH_TRY(up(dx, obs, N * D * 8));
+  PH_TRY(up(dc, acts, N * 8)); PH_TRY(up(dc + N, advs, N * 8));
+  PH_TRY(up(dc + 2 * N, rets, N * 8)); PH_TRY(up(dc + 3 * N, oldlps, N * 8));
+  PH_TRY(to_f32(dp, w.Wf, s.P, nullptr));
+  PH_TRY(to_f32(dx, w.X, (long)N * D, nullptr));
+  k_gather_cols<<<ceil_div(N, kT), kT>>>(nullptr, (long)N, dc, dc + N, dc + 2 * N, dc + 3 * N, nullptr, w.act,
+                                         w.advn, w.ret, w.old, nullptr);
+  PH_LAUNCH_CHECK();
+  PH_TRY(mlp_grad_dev(s, s.N, w, bf16, vfCoef, entCoef, clipEps, 0.0, false, nullptr, nullptr));
+  k_f32_f64<<<ceil_div(s.P, kT), kT>>>(w.gf, dg, s.P, 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(g, dg, s.P * 8);
+}
+
+extern "C" int ph_cuda_train_step(const double* pm, const double* obs, const double* acts,
+                                  const double* advRaw, const double* rets, const double* oldlps, size_t N,
+                                  size_t H, size_t D, size_t A, double lr, double wd, double mu, double eps,
+                                  double vfCoef, double entCoef, double clipEps, uint8_t bf16, double* out) {
+  PH_REQUIRE(N > 0 && H > 0 && D > 0 && A >= 1 && A <= 64, "ph_cuda_train_step: bad shape");
+  PH_REQUIRE(pm && obs && acts && advRaw && rets && oldlps && out, "ph_cuda_train_step: null buffer");
+  const MlpShape s = mlp_shape(N, H, D, A);
+  MlpWork w;
+  State t;
+  PH_TRY(mlp_work(s, s.N, w));
+  PH_TRY(state_bufs(s.P, t));
+  double *dx, *dc;
+  float* obsf;
+  PH_TRY(carve(kHsCols, [&](Carve& c) {
+    dx = c.take<double>((size_t)N * D); dc = c.take<double>(4 * N); obsf = c.take<float>((size_t)N * D);
+  }));
+  PH_TRY(up(t.par, pm, 2 * s.P * 8)); PH_TRY(up(dx, obs, N * D * 8));
+  PH_TRY(up(dc, acts, N * 8)); PH_TRY(up(dc + N, advRaw, N * 8));
+  PH_TRY(up(dc + 2 * N, rets, N * 8)); PH_TRY(up(dc + 3 * N, oldlps, N * 8));
+  PH_TRY(to_f32(dx, obsf, (long)N * D, nullptr));
+  const Cols cols{obsf, dc, dc + N, dc + 2 * N, dc + 3 * N, nullptr};
+  // bf16 tier: bf16-MFMA gradient GEMMs and fp32-MFMA Newton-Schulz (the reference's bf16 Muon runs
+  // fp32 Sgemm, puffercuda.cu:937-941); fp32 tier: fp32 GEMMs and the exact f64 Newton-Schulz.
+  PH_TRY(mlp_minibatch(s, cols, nullptr, s.N, w, t.par, t.mom, t.G, bf16, bf16 != 0, lr, wd, mu, eps, vfCoef,
+                       entCoef, clipEps, 0.0, 0.0, false, nullptr));
+  PH_TRY(finish());
+  return down(out, t.par, 2 * s.P * 8);
+}
+
+namespace {
+// Shared body of the whole-update entries: columns uploaded once, epochs x minibatches on device.
+int train_update_impl(double* par, double* mom, const double* obs, const double* acts, const double* adv,
+                      const double* ret, const double* olp, const double* ov, const double* perm, size_t NT,
+                      size_t D, size_t H, size_t A, size_t epochs, size_t numMB, double lr, double wd,
+                      double mu, double eps, double vfCoef, double entCoef, double clipEps, double vfClip,
+                      double maxGradNorm, int bf, bool mixed, bool losses) {
+  const MlpShape s = mlp_shape(NT, H, D, A);
+  const size_t mbSize = numMB > 0 && NT / numMB > 0 ? NT / numMB : 1;
+  MlpWork w;
+  PH_TRY(mlp_work(s, s.N, w));
+  double *dx, *dc, *dperm, *G;
+  float* obsf;
+  PH_TRY(carve(kHsCols, [&](Carve& c) {
+    dx = c.take<double>(NT * D); dc = c.take<double>(5 * NT); dperm = c.take<double>(epochs * NT);
+    obsf = c.take<float>(NT * D); G = c.take<double>(s.P);
+  }));
+  PH_TRY(up(dx, obs, NT * D * 8));
+  PH_TRY(up(dc, acts, NT * 8)); PH_TRY(up(dc + NT, adv, NT * 8));
+  PH_TRY(up(dc + 2 * NT, ret, NT * 8)); PH_TRY(up(dc + 3 * NT, olp, NT * 8));
+  if (ov) PH_TRY(up(dc + 4 * NT, ov, NT * 8));
+  PH_TRY(up(dperm, perm, epochs * NT * 8));
+  PH_TRY(to_f32(dx, obsf, (long)(NT * D), nullptr));
+  const Cols cols{obsf, dc, dc + NT, dc + 2 * NT, dc + 3 * NT, ov ? dc + 4 * NT : nullptr};
+  for (size_t e = 0; e < epochs; e++)
+    for (size_t m = 0; m < numMB; m++) {
+      const size_t lo = m * mbSize;
+      size_t hi = (m + 1 == numMB) ? NT : (m + 1) * mbSize;
+      if (hi > NT) hi = NT;
+      if (hi <= lo) continue;
+      const bool last = losses && e + 1 == epochs && m + 1 == numMB;
+      PH_TRY(mlp_minibatch(s, cols, dperm + e * NT + lo, (long)(hi - lo), w, par, mom, G, bf, mixed, lr, wd,
+                           mu, eps, vfCoef, entCoef, clipEps, vfClip, maxGradNorm, last, nullptr));
+    }
+  return PH_OK;
+}
+}  // namespace
+
+extern "C" int ph_cuda_train_update(const double* pm, const double* obs, const double* acts, const double* adv,
+                                    const double* ret, const double* olp, const double* perm, size_t NT,
+                                    size_t D, size_t H, size_t A, size_t epochs, size_t numMB, double lr,
+                                    double wd, double mu, double eps, double vfCoef, double entCoef,
+                                    double clipEps, uint8_t bf16, double* out) {
+  PH_REQUIRE(NT > 0 && H > 0 && D > 0 && A >= 1 && A <= 64 && numMB > 0, "ph_cuda_train_update: bad shape");
+  PH_REQUIRE(pm && obs && acts && adv && ret && olp && perm && out, "ph_cuda_train_update: null buffer");
+  const MlpShape s = mlp_shape(NT, H, D, A);
+  State t;
+  PH_TRY(state_bufs(s.P, t));
+  PH_TRY(up(t.par, pm, 2 * s.P * 8));
+  // the whole-update twin always orthogonalises in exact f64 (puffercuda.cu:1168-1171)
+  PH_TRY(train_update_impl(t.par, t.mom, obs, acts, adv, ret, olp, nullptr, perm, NT, D, H, A, epochs, numMB,
+                           lr, wd, mu, eps, vfCoef, entCoef, clipEps, 0.0, 0.0, bf16, false, false));
+  PH_TRY(finish());
+  return down(out, t.par, 2 * s.P * 8);
+}
+
+extern "C" int ph_cuda_train_update_resident(size_t policyH, const double* obs, const double* acts,
+                                             const double* adv, const double* ret, const double* olp,
+                                             const double* ov, size_t ovN, const double* perm, size_t NT,
+                                             size_t D, size_t H, size_t A, size_t epochs, size_t numMB,
+                                             double lr, double wd, double mu, double eps, double vfCoef,
+                                             double entCoef, double clipEps, double vfClip,
+                                             double maxGradNorm, uint8_t bf16, double* out1) {
+  PH_REQUIRE(policyH != 0, "ph_cuda_train_update_resident: no policy handle");
+  PH_REQUIRE(NT > 0 && H > 0 && D > 0 && A >= 1 && A <= 64 && numMB > 0,
+             "ph_cuda_train_update_resident: bad shape");
+  PH_REQUIRE(obs && acts && adv && ret && olp && perm && out1, "ph_cuda_train_update_resident: null buffer");
+  const MlpShape s = mlp_shape(NT, H, D, A);
+  double* par = (double*)policyH;
+  const bool vclip = vfClip > 0.0 && ov && ovN >= NT;  // an empty old-value column turns the clip off
+  PH_TRY(train_update_impl(par, par + s.P, obs, acts, adv, ret, olp, vclip ? ov : nullptr, perm, NT, D, H, A,
+                           epochs, numMB, lr, wd, mu, eps, vfCoef, entCoef, clipEps, vclip ? vfClip : 0.0,
+                           maxGradNorm, bf16, bf16 != 0, g_mgLossOn != 0));
+  PH_TRY(finish());
+  return down(out1, par, 8);  // params[0], the caller's divergence guard
+}
+
+// ---- Muon -----------------------------------------------------------------------------------------
+extern "C" int ph_cuda_muon_stepmat(const double* W, const double* G, const double* M, size_t rows,
+                                    size_t cols, double lr, double wd, double mu, double eps, double* out) {
+  PH_REQUIRE(rows * cols == 0 || (W && G && M && out), "ph_cuda_muon_stepmat: null buffer");
+  PH_REQUIRE(rows <= INT32_MAX && cols <= INT32_MAX, "ph_cuda_muon_stepmat: extents exceed int32");
+  const size_t n = rows * cols;
+  if (n == 0) return PH_OK;
+  double *dW, *dG, *dM;
+  PH_TRY(carve(kHsState, [&](Carve& c) { dW = c.take<double>(n); dG = c.take<double>(n); dM = c.take<double>(n); }));
+  PH_TRY(up(dW, W, n * 8)); PH_TRY(up(dG, G, n * 8)); PH_TRY(up(dM, M, n * 8));
+  PH_TRY(muon_f64((int)rows, (int)cols, dW, dG, dM, 1.0, lr, wd, mu, eps, false, nullptr));
+  PH_TRY(finish());
+  PH_TRY(down(out, dW, n * 8));
+  return down(out + n, dM, n * 8);
+}
+
+extern "C" int ph_cuda_muon_step_mlp_resident(size_t policyH, const double* gRaw, size_t H, size_t D, size_t O,
+                                              double gscale, double lr, double wd, double mu, double eps,
+                                              double* newParams) {
+  PH_REQUIRE(policyH != 0, "ph_cuda_muon_step_mlp_resident: no policy handle");
+  PH_REQUIRE(O >= 2 && H > 0 && D > 0 && gRaw && newParams, "ph_cuda_muon_step_mlp_resident: bad arguments");
+  const MlpShape s = mlp_shape(1, H, D, O - 1);
+  double* par = (double*)policyH;
+  double* G = (double*)scratch(kHsGrad, (size_t)s.P * 8);
+  if (!G) return PH_ERR_NOMEM;
+  PH_TRY(up(G, gRaw, s.P * 8));
+  PH_TRY(mlp_muon(s, par, par + s.P, G, gscale, lr, wd, mu, eps, false, nullptr));
+  PH_TRY(finish());
+  return down(newParams, par, s.P * 8);
+}
+
+// ---- device-resident policy handle ([params(P); mom(P)] f64) ----------------------------------------
+extern "C" int ph_cuda_policy_load(const double* pm, size_t P, size_t* handle) {
+  PH_REQUIRE(pm && handle && P > 0, "ph_cuda_policy_load: bad arguments");
+  double* d = nullptr;
+  PH_CHECK_HIP(hipMalloc((void**)&d, 16 * P));
+  if (hipMemcpy(d, pm, 16 * P, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(d);
+    set_error("ph_cuda_policy_load: upload failed");
+    return PH_ERR_HIP;
+  }
+  *handle = (size_t)d;
+  return PH_OK;
+}
+extern "C" int ph_cuda_policy_download(size_t handle, size_t P, double* pm) {
+  PH_REQUIRE(handle != 0 && pm, "ph_cuda_policy_download: bad arguments");
+  PH_TRY(finish());
+  return down(pm, (const void*)handle, 16 * P);
+}
+extern "C" int ph_cuda_policy_free(size_t handle) {
+  if (handle) {
+    PH_CHECK_HIP(hipDeviceSynchronize());
+    PH_CHECK_HIP(hipFree((void*)handle));
+  }
+  return PH_OK;
+}
+
+// ---- dashboard-loss channel --------------------------------------------------------------------
+extern "C" int ph_cuda_mg_loss_enable(uint8_t on) {
+  g_mgLossOn = on ? 1 : 0;
+  return PH_OK;
+}
+extern "C" int ph_cuda_mg_read_losses(double* out7) {
+  PH_REQUIRE(out7, "ph_cuda_mg_read_losses: null buffer");
+  for (int i = 0; i < 7; i++) out7[i] = g_mgLoss[i];
+  return PH_OK;
+}
+
+// ---- dense forward entries of pufferblas.c -----------------------------------------------------------
+extern "C" int ph_ffi_dense_forward_gpu(const double* X, const double* W, const double* b, size_t N, size_t D,
+                                        size_t H, double* Y) {
+  PH_REQUIRE(N * H == 0 || (X && W && b && Y), "ph_ffi_dense_forward_gpu: null buffer");
+  if (N * H == 0) return PH_OK;
+  double *dX, *dW, *db, *dY;
+  PH_TRY(carve(kHsDense, [&](Carve& c) {
+    dX = c.take<double>(N * D); dW = c.take<double>(H * D); db = c.take<double>(H); dY = c.take<double>(N * H);
+  }));
+  PH_TRY(up(dX, X, N * D * 8)); PH_TRY(up(dW, W, H * D * 8)); PH_TRY(up(db, b, H * 8));
+  k_dense_f64<<<ceil_div(N * H, kT), kT>>>(dX, dW, db, dY, (long)N, (int)D, (int)H);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(Y, dY, N * H * 8);
+}
+
+extern "C" int ph_ffi_dense_forward_bf16(const double* X, const double* W, const double* b, size_t N, size_t D,
+                                         size_t H, double* Y) {
+  PH_REQUIRE(N * H == 0 || (X && W && b && Y), "ph_ffi_dense_forward_bf16: null buffer");
+  if (N * H == 0) return PH_OK;
+  double *dX, *dW, *db, *dY;
+  uint16_t *xb, *wb;
+  float* yf;
+  PH_TRY(carve(kHsDense, [&](Carve& c) {
+    dX = c.take<double>(N * D); dW = c.take<double>(H * D); db = c.take<double>(H); dY = c.take<double>(N * H);
+    xb = c.take<uint16_t>(N * D); wb = c.take<uint16_t>(H * D); yf = c.take<float>(N * H);
+  }));
+  PH_TRY(up(dX, X, N * D * 8)); PH_TRY(up(dW, W, H * D * 8)); PH_TRY(up(db, b, H * 8));
+  k_f64_bf16<<<ceil_div(N * D, kT), kT>>>(dX, xb, (long)(N * D));
+  k_f64_bf16<<<ceil_div(H * D, kT), kT>>>(dW, wb, (long)(H * D));
+  PH_LAUNCH_CHECK();
+  PhGemmDesc g{};
+  g.trans_a = 0; g.trans_b = 1; g.M = (int)N; g.N = (int)H; g.K = (int)D;
+  g.a_dtype = PH_BF16; g.A = xb; g.lda = (long)D; g.b_dtype = PH_BF16; g.B = wb; g.ldb = (long)D;
+  g.c_dtype = PH_F32; g.C = yf; g.ldc = (long)H; g.math = PH_MATH_BF16; g.alpha = 1.f;
+  PH_TRY(gemm(g, nullptr));
+  k_f32_f64<<<ceil_div(N * H, kT), kT>>>(yf, dY, (long)(N * H), 1.0);
+  k_bias_relu_f64<<<ceil_div(N * H, kT), kT>>>(dY, db, (long)N, (int)H, 1);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(Y, dY, N * H * 8);
+}
+
+extern "C" int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, size_t D, size_t H,
+                                             size_t O, double* Y) {
+  PH_REQUIRE(N * O == 0 || (p && X && Y), "ph_ffi_mlp_forward_batch_bf16: null buffer");
+  if (N * O == 0) return PH_OK;
+  const size_t P = H * D + H + O * H + O;
+  double *dp, *dX, *dY;
+  float *pf, *xf, *h1, *of;
+  PH_TRY(carve(kHsDense, [&](Carve& c) {
+    dp = c.take<double>(P); dX = c.take<double>(N * D); dY = c.take<double>(N * O);
+    pf = c.take<float>(P); xf = c.take<float>(N * D); h1 = c.take<float>(N * H); of = c.take<float>(N * O);
+  }));
+  PH_TRY(up(dp, p, P * 8)); PH_TRY(up(dX, X, N * D * 8));
+  PH_TRY(to_f32(dp, pf, (long)P, nullptr));
+  PH_TRY(to_f32(dX, xf, (long)(N * D), nullptr));
+  PhGemmDesc g = f32desc(0, 1, (long)N, (long)H, (long)D, xf, (long)D, pf, (long)D, h1, (long)H, PH_MATH_BF16);
+  g.epi = PH_EPI_BIAS_RELU; g.bias = pf + H * D;
+  PH_TRY(gemm(g, nullptr));
+  g = f32desc(0, 1, (long)N, (long)O, (long)H, h1, (long)H, pf + H * D + H, (long)H, of, (long)O, PH_MATH_BF16);
+  g.epi = PH_EPI_BIAS; g.bias = pf + H * D + H + O * H;
+  PH_TRY(gemm(g, nullptr));
+  k_f32_f64<<<ceil_div(N * O, kT), kT>>>(of, dY, (long)(N * O), 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(Y, dY, N * O * 8);
+}
+
+// Device-resident bf16 dense-layer throughput in GFLOP/s (2*N*D*H per rep); -1 without a device.
+extern "C" double ph_ffi_bench_bf16_resident(size_t N, size_t D, size_t H, size_t reps) {
+  if (N * D * H == 0 || reps == 0) return -1.0;
+  uint16_t *xb = nullptr, *wb = nullptr;
+  float* yf = nullptr;
+  if (carve(kHsDense, [&](Carve& c) {
+        xb = c.take<uint16_t>(N * D); wb = c.take<uint16_t>(H * D); yf = c.take<float>(N * H);
+      }) != PH_OK)
+    return -1.0;
+  PhGemmDesc g{};
+  g.trans_a = 0; g.trans_b = 1; g.M = (int)N; g.N = (int)H; g.K = (int)D;
+  g.a_dtype = PH_BF16; g.A = xb; g.lda = (long)D; g.b_dtype = PH_BF16; g.B = wb; g.ldb = (long)D;
+  g.c_dtype = PH_F32; g.C = yf; g.ldc = (long)H; g.math = PH_MATH_BF16; g.alpha = 1.f;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
+  if (gemm(g, nullptr) != PH_OK) return -1.0;
+  (void)hipEventRecord(e0, nullptr);
+  for (size_t r = 0; r < reps; r++)
+    if (gemm(g, nullptr) != PH_OK) return -1.0;
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return ms > 0.f ? 2.0 * (double)N * D * H * reps / (ms * 1e-3) / 1e9 : -1.0;
+}
+
+extern "C" uint8_t ph_ffi_cuda_available(void) { return ph_device_count() > 0 ? 1 : 0; }
+
+// Link-time contract of pufferblas.c (pufferblas.c:46-50): the GPU LSTM BPTT is not part of this
+// library, and returning 0 is the reference's documented "no usable device / unsupported shape" answer
+// that makes the caller run its own CPU path.
+extern "C" int cuda_lstm_ppo_grad_batch(const double*, const double*, const double*, const double*,
+                                        const double*, const double*, const double*, const double*,
+                                        const double*, size_t, size_t, size_t, size_t, size_t, double, double,
+                                        double, double*, double*, int) {
+  return 0;
+}
+
+// ---- MinGRU ---------------------------------------------------------------------------------------
+// Host mode of lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, f64), obs [T*B*D]
+// time-major, scal = [act | adv | ret | old | term | ov] (6*T*B, K = 1); writes out[P + 2*T*B] =
+// [summed gradient | new_logp | new_value]. The device-resident modes (empty obs/scal, segment
+// indices, priority weights) and multi-discrete heads (K > 1) are not provided here.
+extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
+                                       size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L,
+                                       size_t A, size_t K, double vfCoef, double entCoef, double clipEps,
+                                       double vfClip, size_t nseg, size_t nprio, double* out) {
+  PH_REQUIRE(K <= 1, "ph_cuda_mingru_ppo_grad: multi-discrete heads (K=%zu) are not supported", K);
+  PH_REQUIRE(nseg == 0 && nprio == 0,
+             "ph_cuda_mingru_ppo_grad: segment-index / priority (device-resident) modes are not supported");
+  const size_t TB = T * B;
+  PH_REQUIRE(nobs >= TB * D && nscal >= 6 * TB,
+             "ph_cuda_mingru_ppo_grad: host obs and scal are required (device-resident inputs not supported)");
+  PH_REQUIRE(params && obs && scal && out, "ph_cuda_mingru_ppo_grad: null buffer");
+  ph_mingru_dims d{(int)B, (int)T, (int)D, (int)H, (int)L, (int)A, env_is("PUFFER_MG_PREC", "bf16") ? 0 : 1};
+  const long P = mingru_param_count(d);
+  ph_ppo_coefs c{};
+  c.vf_coef = vfCoef; c.ent_coef = entCoef; c.clip_eps = clipEps; c.vf_clip = vfClip;
+  double *dp, *dx, *ds, *losses;
+  float *pf, *xf, *sf, *G, *nlp, *nv;
+  int* act;
+  PH_TRY(carve(kHsMg, [&](Carve& cv) {
+    dp = cv.take<double>(P); dx = cv.take<double>(TB * D); ds = cv.take<double>(6 * TB);
+    losses = cv.take<double>(8); pf = cv.take<float>(P); xf = cv.take<float>(TB * D);
+    sf = cv.take<float>(6 * TB); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
+    act = cv.take<int>(TB);
+  }));
+  PH_TRY(up(dp, params, P * 8)); PH_TRY(up(dx, obs, TB * D * 8)); PH_TRY(up(ds, scal, 6 * TB * 8));
+  PH_TRY(to_f32(dp, pf, P, nullptr));
+  PH_TRY(to_f32(dx, xf, (long)(TB * D), nullptr));
+  PH_TRY(to_f32(ds, sf, (long)(6 * TB), nullptr));
+  k_f64_i32<<<ceil_div(TB, kT), kT>>>(ds, act, (long)TB);
+  PH_LAUNCH_CHECK();
+  PH_TRY(ph_mingru_ppo_grad(&d, &c, pf, xf, act, sf + TB, sf + 2 * TB, sf + 3 * TB, sf + 5 * TB, sf + 4 * TB, G,
+                            nlp, nv, g_mgLossOn ? losses : nullptr, nullptr));
+  double* o = (double*)scratch(kHsMgOut, (P + 2 * TB) * 8);
+  if (!o) return PH_ERR_NOMEM;
+  k_f32_f64<<<ceil_div(P, kT), kT>>>(G, o, P, 1.0);
+  k_f32_f64<<<ceil_div(TB, kT), kT>>>(nlp, o + P, (long)TB, 1.0);
+  k_f32_f64<<<ceil_div(TB, kT), kT>>>(nv, o + P + TB, (long)TB, 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  if (g_mgLossOn) PH_TRY(down(g_mgLoss, losses, 7 * 8));
+  return down(out, o, (P + 2 * TB) * 8);
+}
+
+// Host-gradient mode of lean_cuda_mingru_muon_resident (puffercuda.cu:5727): the clipped gradient
+// gClip[P] is uploaded and every flattenMG matrix takes a Muon step on the resident [weights; mom]
+// (fp32-MFMA Newton-Schulz with f64 state; PUFFER_MUON_EXACT=1 selects the exact f64 tier), every
+// bias a Nesterov stepvec; writes the new weights (P). The resident-gradient mode (empty gClip) is
+// not provided.
+extern "C" int ph_cuda_mingru_muon_resident(size_t policyH, const double* gClip, size_t nG, size_t H, size_t D,
+                                            size_t L, size_t A, double lr, double wd, double mu, double eps,
+                                            double maxGradNorm, double gscale, double* wOut) {
+  (void)maxGradNorm;
+  (void)gscale;
+  PH_REQUIRE(policyH != 0, "ph_cuda_mingru_muon_resident: no policy handle");
+  const size_t szE = H * D, szL = 3 * H * H;
+  const size_t P = szE + H + L * szL + A * H + A + H + 1;
+  PH_REQUIRE(gClip && nG >= P, "ph_cuda_mingru_muon_resident: the host gradient (P=%zu) is required", P);
+  PH_REQUIRE(wOut, "ph_cuda_mingru_muon_resident: null output");
+  const bool mixed = !env_is("PUFFER_MUON_EXACT", "1");
+  double* W = (double*)policyH;
+  double* M = W + P;
+  double* G = (double*)scratch(kHsGrad, P * 8);
+  if (!G) return PH_ERR_NOMEM;
+  PH_TRY(up(G, gClip, P * 8));
+  const size_t offW = szE + H, offDec = offW + L * szL, offBDec = offDec + A * H, offVal = offBDec + A,
+               offBVal = offVal + H;
+  PH_TRY(muon_f64((int)H, (int)D, W, G, M, 1.0, lr, wd, mu, eps, mixed, nullptr));
+  PH_TRY(stepvec_f64((long)H, W + szE, G + szE, M + szE, 1.0, lr, wd, mu, nullptr));
+  for (size_t l = 0; l < L; l++)
+    PH_TRY(muon_f64((int)(3 * H), (int)H, W + offW + l * szL, G + offW + l * szL, M + offW + l * szL, 1.0, lr,
+                    wd, mu, eps, mixed, nullptr));
+  PH_TRY(muon_f64((int)A, (int)H, W + offDec, G + offDec, M + offDec, 1.0, lr, wd, mu, eps, mixed, nullptr));
+  PH_TRY(stepvec_f64((long)A, W + offBDec, G + offBDec, M + offBDec, 1.0, lr, wd, mu, nullptr));
+  PH_TRY(muon_f64(1, (int)H, W + offVal, G + offVal, M + offVal, 1.0, lr, wd, mu, eps, mixed, nullptr));
+  PH_TRY(stepvec_f64(1, W + offBVal, G + offBVal, M + offBVal, 1.0, lr, wd, mu, nullptr));
+  PH_TRY(finish());
+  return down(wOut, W, P * 8);
+}

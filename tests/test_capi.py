@@ -38,6 +38,37 @@ def test_signatures_cover_exports():
         assert name in declared_symbols(), f"{name} bound in _lib but not declared"
 
 
+def test_link_time_contract_symbols():
+    """The externs the reference's pufferblas.c resolves at link time (pufferblas.c:38-50)."""
+    import ctypes as C
+    lib = L.lib()
+    assert hasattr(lib, "cuda_lstm_ppo_grad_batch")
+    assert C.c_int.in_dll(lib, "g_mgLossOn").value in (0, 1)
+    losses = (C.c_double * 7).in_dll(lib, "g_mgLoss")
+    assert len(list(losses)) == 7
+
+
+def test_loss_channel_without_device():
+    import ctypes as C
+    lib = L.lib()
+    L.call("ph_cuda_mg_loss_enable", 1)
+    assert C.c_int.in_dll(lib, "g_mgLossOn").value == 1
+    L.call("ph_cuda_mg_loss_enable", 0)
+    assert C.c_int.in_dll(lib, "g_mgLossOn").value == 0
+    out = (C.c_double * 7)()
+    L.call("ph_cuda_mg_read_losses", out)
+
+
+def test_host_entries_reject_bad_arguments_without_device():
+    # argument checks run before any device work
+    import ctypes as C
+    lib = L.lib()
+    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, 0.5, 0.01, 0.2, 0.0,
+                                       0, 0, None) == L.PH_ERR_ARG
+    assert b"multi-discrete" in lib.ph_last_error()
+    assert lib.ph_cuda_policy_download(0, 4, None) == L.PH_ERR_ARG
+
+
 def test_no_device_calls_fail_cleanly():
     lib = L.lib()
     assert lib.ph_version() == 100
