@@ -237,6 +237,41 @@ def bench_vtrace(steps, warmup):
             "bytes": bytes_, "single_call_us": round(ms1 * 1e3, 2)}
 
 
+def traffic_kernels():
+    """Launches for the two HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
+    the dominant kernel (layer-forward GEMM) 3 times, then a plain 512 MiB device copy 3 times, whose
+    known byte count scales the counters."""
+    import torch
+    from pufferlean_amd import device as D
+    rows = B5 * T5
+    x = torch.randn(rows, H5, device="cuda").bfloat16()
+    w = (torch.randn(3 * H5, H5, device="cuda") / 22.6).bfloat16()
+    y = torch.empty(rows, 3 * H5, device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        D.gemm(x, w, trans_b=True, out=y)
+    torch.cuda.synchronize()
+    a = torch.ones(1 << 28, device="cuda", dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"gemm": [rows, 3 * H5, H5], "copy_bytes": 2 * a.numel()}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_layer_fwd_262144x1536x512_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed counter summary (null if the
+    summary is absent or was taken on another tile configuration)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t.get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 # ------------------------------------------------------------------------------------------------
 def cpu_baseline_ppo(budget_s=15.0):
     """The oracle's single-sequence MinGRU PPO gradient (f64, one thread, the reference CPU path's
@@ -284,6 +319,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.only == "traffic":
+        print(json.dumps(traffic_kernels()))
+        return 0
     comps = {}
     head = None
     if args.only in ("all", "ppo"):
@@ -315,7 +353,8 @@ def main():
         dk = head["dominant_kernel"]
         line["roofline"] = {"bound": "mfma", "achieved": dk["tflops"], "peak": BF16_PEAK_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(dk["tflops"] / BF16_PEAK_TFLOPS, 4),
-                            "traffic": None, "kernel": dk["name"], "kernel_us": dk["us"]}
+                            "traffic": measured_traffic(), "kernel": dk["name"], "kernel_us": dk["us"],
+                            "algorithmic_bytes": dk["hbm_bytes"]}
         line["step"] = {k: v for k, v in head.items() if k != "dominant_kernel"}
     line["components"] = comps
     if not args.no_cpu_baseline and head:
