@@ -14,7 +14,9 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
   gemm    policy GEMMs M=16384, K=N=512 in the three forms (forward X.W^T, dgrad dY.W, wgrad dY^T.X)
   ns      Newton-Schulz batch: 4 x (512x512) + 2 x (512x1024), 5 steps, constant coefficients
   vtrace  V-trace, fp32 time-major, 4096 segments x 64, replicated 64x in one launch (403 MB)
-Kernel times are HIP-event times on the stream the kernels run on.
+Component times are HIP-event times of a HIP graph holding `steps` launches (device time per launch,
+no host launch path; "us_eager" is the same loop launched from Python). Events are recorded on the
+stream the kernels run on.
 """
 from __future__ import annotations
 
@@ -153,6 +155,33 @@ def bench_ppo_step(steps, warmup, eager=False):
     return out
 
 
+def time_graph(fn, steps, warmup):
+    """Average ms per call of fn() with `steps` calls captured in one HIP graph and replayed, so the
+    figure is device time per call without the host launch path (kernel-scale components are shorter
+    than a Python-level launch). fn must not allocate; the warm-up calls size the library's buffers."""
+    import torch
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(steps):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = _ev()
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
 def bench_gemm(steps, warmup):
     import numpy as np
     import torch
@@ -181,9 +210,11 @@ def bench_gemm(steps, warmup):
     }
     out = {}
     for name, (fn, peak) in forms.items():
-        ms = time_loop(fn, steps, warmup)
+        ms = time_graph(fn, steps, warmup)
+        ms_eager = time_loop(fn, steps, warmup)
         tf = flops / (ms * 1e-3) / 1e12
-        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / peak, 4)}
+        out[name] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac": round(tf / peak, 4),
+                     "us_eager": round(ms_eager * 1e3, 2)}
     return out
 
 
@@ -197,15 +228,14 @@ def bench_ns(steps, warmup):
     mats = [_t(rng.normal(rng.seed_for(3, i), r * c, 0.0, 0.02)).view(r, c) for i, (r, c) in enumerate(shapes)]
     work = [m.clone() for m in mats]
 
-    def run():
-        for w in work:
-            D.newton_schulz(w, coeffs=D.CONST_COEFFS, math="bf16")
-
-    ms = time_loop(run, max(steps // 5, 3), warmup)
+    # the six matrices run concurrently on the library's stream lanes (ph_newton_schulz_batch)
+    run = lambda: D.newton_schulz_batch(work, coeffs=D.CONST_COEFFS, math="bf16")
+    ms = time_graph(run, max(steps // 5, 3), warmup)
+    ms_eager = time_loop(run, max(steps // 5, 3), warmup)
     flops = sum(5 * (4 * min(r, c) ** 2 * max(r, c) + 2 * min(r, c) ** 3) for r, c in shapes)
     tf = flops / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-            "flops": flops, "matrices": len(shapes)}
+            "flops": flops, "matrices": len(shapes), "us_eager": round(ms_eager * 1e3, 1)}
 
 
 def bench_vtrace(steps, warmup):
@@ -225,14 +255,14 @@ def bench_vtrace(steps, warmup):
     tgt = torch.empty_like(val)
     fn = lambda: D.vtrace(rew, val, done, logr, boot, variant=1, time_major=True, rho_is_log=True,
                           out_adv=adv, out_tgt=tgt)
-    ms = time_loop(fn, steps, warmup)
+    ms = time_graph(fn, steps, warmup)
     bytes_ = 24.0 * n * R + 4.0 * B * R
     gbs = bytes_ / (ms * 1e-3) / 1e9
     v1, r1, d1, l1 = (c[:, :B].contiguous() for c in cols)
     b1 = boot[:B].contiguous()
     a1, t1 = torch.empty_like(v1), torch.empty_like(v1)
-    ms1 = time_loop(lambda: D.vtrace(r1, v1, d1, l1, b1, variant=1, time_major=True, rho_is_log=True,
-                                     out_adv=a1, out_tgt=t1), steps, warmup)
+    ms1 = time_graph(lambda: D.vtrace(r1, v1, d1, l1, b1, variant=1, time_major=True, rho_is_log=True,
+                                      out_adv=a1, out_tgt=t1), steps, warmup)
     return {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "bytes": bytes_, "single_call_us": round(ms1 * 1e3, 2)}
 

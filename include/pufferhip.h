@@ -125,6 +125,11 @@ int ph_stepvec_f64(size_t n, const double* b, const double* g, const double* m, 
  * puffercuda.cu:942-966). coeffs: host float[nsteps][3]. */
 int ph_newton_schulz(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,
                      int math, void* stream);
+/* The same for a batch of independent matrices X[i] (rows[i] x cols[i]), run concurrently on the
+ * library's stream lanes (forked from and joined back into `stream`); results equal n calls of
+ * ph_newton_schulz. No counterpart in the reference (its NS walks the matrices in sequence). */
+int ph_newton_schulz_batch(float* const* X, const int* rows, const int* cols, int n,
+                           const float* coeffs, int nsteps, float eps, int math, void* stream);
 /* In-place Muon matrix step on fp32 state: M <- mu*M + gscale*G; U = gscale*G + mu*M;
  * W <- (1-lr*wd)*W + lr*sqrt(max(1,rows/cols))*NS(U). */
 int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,

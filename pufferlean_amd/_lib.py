@@ -55,6 +55,7 @@ SIGNATURES: dict[str, list] = {
     "ph_muon_mat_f64": [i32, i32, vp, vp, vp, vp, vp, dbl, dbl, dbl, dbl, dbl, vp, i32, vp],
     "ph_stepvec_f64": [sz, vp, vp, vp, vp, vp, dbl, dbl, dbl, dbl, vp],
     "ph_newton_schulz": [vp, i32, i32, vp, i32, flt, i32, vp],
+    "ph_newton_schulz_batch": [vp, vp, vp, i32, vp, i32, flt, i32, vp],
     "ph_muon_mat": [vp, vp, vp, i32, i32, flt, flt, flt, flt, flt, vp, i32, i32, vp],
     "ph_stepvec": [vp, vp, vp, sz, flt, flt, flt, flt, vp],
     "ph_gclip": [vp, sz, flt, flt, vp],

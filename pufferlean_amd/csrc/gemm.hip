@@ -944,10 +944,9 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
 
   // Tile choice (measured on the policy shapes). bf16 x bf16 with >= 512 tiles of 256x128: the
   // 256x128 kernel. Otherwise 128x128 when that gives >= 128 tiles. Otherwise, for long reductions
-  // (the wgrad forms, K = rows of the minibatch) split-K over 256x256 (bf16) or 128x128 tiles up to
-  // the resident block count (one 256x256 or two 128x128 blocks on each of the 256 CUs, so all
-  // splits run in one round), >= 2048 of k per split; for short reductions 64x64 tiles when those
-  // reach 128, else split-K with >= 256 of k each.
+  // (the wgrad forms, K = rows of the minibatch) split-K up to the resident block count (one 256x256
+  // or two 128x128 blocks on each of the 256 CUs, so all splits run in one round); for short
+  // reductions 64x64 tiles when those reach 128, else split-K with >= 256 of k each.
   int splits = d.splits > 0 ? d.splits : 1;
   const long tiles256 = (long)((d.M + 255) / 256) * ((d.N + 255) / 256);
   const long tiles256x128 = (long)((d.M + 255) / 256) * ((d.N + 127) / 128);
@@ -958,10 +957,12 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   int big_bn = 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
     if (d.K >= 4096) {
-      big = big_ok;
+      // 256x256 splits when both output extents fill the tile and the reduction is long enough to
+      // give every one of the 256 resident blocks >= 2048 of k; else 128x128 splits of >= 512
+      big = big_ok && d.M >= 256 && d.N >= 256 && d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
       big_bn = 256;
       const long want = big ? 256 / tiles256 : 512 / tiles128;
-      const long maxs = d.K / 2048;
+      const long maxs = d.K / (big ? 2048 : 512);
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
     } else if (tiles64 >= 128 || d.K < 512) {

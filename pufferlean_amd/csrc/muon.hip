@@ -392,6 +392,28 @@ extern "C" int ph_newton_schulz(float* X, int rows, int cols, const float* coeff
   return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, 0, as_stream(stream));
 }
 
+extern "C" int ph_newton_schulz_batch(float* const* X, const int* rows, const int* cols, int n,
+                                      const float* coeffs, int nsteps, float eps, int math, void* stream) {
+  PH_REQUIRE(n >= 0 && (n == 0 || (X && rows && cols)), "ph_newton_schulz_batch: bad arguments");
+  PH_REQUIRE(nsteps >= 0 && nsteps <= 64 && (coeffs != nullptr || nsteps == 0),
+             "ph_newton_schulz_batch: bad coefficient table");
+  PH_REQUIRE(math == PH_MATH_BF16 || math == PH_MATH_F32 || math == PH_MATH_BF16X3,
+             "ph_newton_schulz_batch: unknown math");
+  for (int i = 0; i < n; i++) PH_REQUIRE(rows[i] >= 0 && cols[i] >= 0, "ph_newton_schulz_batch: bad shape");
+  if (n == 0) return PH_OK;
+  // The matrices are independent: matrix i runs on stream lane i % kLanes with that lane's scratch;
+  // the lanes fork from and join back into `stream`.
+  hipStream_t st = as_stream(stream);
+  const int nl = n < kLanes ? n : kLanes;
+  PH_TRY(fork_lanes(st, nl));
+  for (int i = 0; i < n; i++) {
+    const LaneSlots sl = lane_slots(i % kLanes);
+    PH_TRY(newton_schulz_fast(X[i], rows[i], cols[i], coeffs, nsteps, eps, math, sl.ns, sl.gemm_ws,
+                              lane_stream(i % kLanes)));
+  }
+  return join_lanes(st, nl);
+}
+
 extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale,
                            float lr, float wd, float mu, float eps, const float* coeffs, int nsteps,
                            int math, void* stream) {

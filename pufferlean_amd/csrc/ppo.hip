@@ -35,9 +35,11 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
   double lsum[6] = {0, 0, 0, 0, 0, 0};  // pg, v, ent, old_kl, kl, nclip
   if (n < N) {
     const float* lg = logits + (size_t)n * ldl;
+    // All AMAX loads are issued unconditionally (columns past A re-read column A-1, in bounds) so
+    // they are in flight together; the values past A are masked where they are used.
     float x[AMAX];
 #pragma unroll
-    for (int k = 0; k < AMAX; k++) x[k] = k < A ? lg[k] : 0.f;
+    for (int k = 0; k < AMAX; k++) x[k] = lg[k < A ? k : A - 1];
     float lse;
     if (max_shift) {
       float mx = x[0];

@@ -58,44 +58,63 @@ __global__ void __launch_bounds__(256) k_vtrace(const R* __restrict__ rew, const
     vnext = boot[b];
     tEnd = T;
   }
+  // Two register buffers of CH steps: chunk k+1 is loaded while chunk k is computed. Every load is
+  // unconditional (a step before t = 0 re-reads row 0, a few L2-resident bytes), so the loads of a
+  // chunk issue together and the compiler waits for exactly the older buffer.
+  R ra[CH], va[CH], da[CH], wa[CH], rb[CH], vb[CH], db[CH], wb[CH];
+  auto ld = [&](R (&rr)[CH], R (&vv)[CH], R (&dd)[CH], R (&ww)[CH], int t0) {
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+      const int tc = t0 - c >= 0 ? t0 - c : 0;
+      const size_t i = at(tc);
+      rr[c] = rew[i];
+      vv[c] = val[i];
+      dd[c] = term[i];
+      ww[c] = rho ? rho[i] : R(1);
+    }
+  };
+  auto step = [&](R r0, R v0, R d0, R w0, int tc) {
+    const R w = ratio_of(w0, rho_is_log);
+    const R rh = w < rhoClip ? w : rhoClip;
+    const R cc = w < cClip ? w : cClip;
+    const R r = clamp ? clamp_unit(r0) : r0;
+    R nnt, delta;
+    if (VARIANT == 0) {
+      nnt = (d0 != R(0)) ? R(0) : R(1);
+      delta = rh * (r + gamma * vnext * nnt - v0);
+    } else {
+      nnt = (d0 > R(0.5)) ? R(0) : R(1);
+      delta = rh * r + gamma * vnext * nnt - v0;
+    }
+    last = delta + gl * cc * last * nnt;
+    const size_t i = at(tc);
+    adv[i] = last;
+    if (tgt) tgt[i] = last + v0;
+    vnext = v0;
+  };
+  // steps t0, t0-1, ..., t0-CH+1 (the tail chunk stops at t = 0)
+  auto run = [&](const R (&rr)[CH], const R (&vv)[CH], const R (&dd)[CH], const R (&ww)[CH], int t0) {
+    if (t0 >= CH - 1) {
+#pragma unroll
+      for (int c = 0; c < CH; c++) step(rr[c], vv[c], dd[c], ww[c], t0 - c);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CH; c++)
+        if (t0 - c >= 0) step(rr[c], vv[c], dd[c], ww[c], t0 - c);
+    }
+  };
   int t = tEnd - 1;
-  // Chunked: load CH steps (t, t-1, ..., t-CH+1), then run them.
-  for (; t >= 0; t -= CH) {
-    R rr[CH], vv[CH], dd[CH], ww[CH];
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-      const int tc = t - c;
-      if (tc >= 0) {
-        const size_t i = at(tc);
-        rr[c] = rew[i];
-        vv[c] = val[i];
-        dd[c] = term[i];
-        ww[c] = rho ? rho[i] : R(1);
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-      const int tc = t - c;
-      if (tc >= 0) {
-        const R w = ratio_of(ww[c], rho_is_log);
-        const R rh = w < rhoClip ? w : rhoClip;
-        const R cc = w < cClip ? w : cClip;
-        const R r = clamp ? clamp_unit(rr[c]) : rr[c];
-        R nnt, delta;
-        if (VARIANT == 0) {
-          nnt = (dd[c] != R(0)) ? R(0) : R(1);
-          delta = rh * (r + gamma * vnext * nnt - vv[c]);
-        } else {
-          nnt = (dd[c] > R(0.5)) ? R(0) : R(1);
-          delta = rh * r + gamma * vnext * nnt - vv[c];
-        }
-        last = delta + gl * cc * last * nnt;
-        const size_t i = at(tc);
-        adv[i] = last;
-        if (tgt) tgt[i] = last + vv[c];
-        vnext = vv[c];
-      }
-    }
+  if (t < 0) return;
+  ld(ra, va, da, wa, t);
+  while (true) {
+    ld(rb, vb, db, wb, t - CH);
+    run(ra, va, da, wa, t);
+    t -= CH;
+    if (t < 0) break;
+    ld(ra, va, da, wa, t - CH);
+    run(rb, vb, db, wb, t);
+    t -= CH;
+    if (t < 0) break;
   }
 }
 

@@ -156,6 +156,23 @@ def newton_schulz(X, *, coeffs=CONST_COEFFS, eps=1e-7, math="bf16"):
     return X
 
 
+def newton_schulz_batch(Xs, *, coeffs=CONST_COEFFS, eps=1e-7, math="bf16"):
+    """In-place fast-tier NS of several independent fp32 matrices, run concurrently on the library's
+    stream lanes; equal to calling newton_schulz on each."""
+    _dev(*Xs)
+    for X in Xs:
+        if X.dtype != torch.float32 or not X.is_contiguous():
+            raise TypeError("newton_schulz_batch needs contiguous fp32 matrices")
+    c, cp, ns = _coeffs(coeffs, "float32")
+    m = L.PH_MATH_BF16 if math == "bf16" else L.PH_MATH_F32
+    n = len(Xs)
+    ptrs = (C.c_void_p * n)(*[X.data_ptr() for X in Xs])
+    rows = (C.c_int * n)(*[X.shape[0] for X in Xs])
+    cols = (C.c_int * n)(*[X.shape[1] for X in Xs])
+    L.call("ph_newton_schulz_batch", ptrs, rows, cols, n, cp, ns, eps, m, _stream())
+    return Xs
+
+
 def muon_mat(W, G, M, *, gscale=1.0, lr=0.015, wd=0.0, mu=0.95, eps=1e-7, coeffs=CONST_COEFFS,
              math="bf16"):
     """In-place fast-tier Muon matrix step on fp32 W and momentum M."""

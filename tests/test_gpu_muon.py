@@ -70,6 +70,23 @@ def test_fast_ns_vs_oracle(gpu, shape, coeffs):
     assert rel(gb, gf.astype(np.float64)) < 1e-2
 
 
+@pytest.mark.parametrize("math_", ["bf16", "f32"])
+def test_ns_batch_equals_single_calls(gpu, math_):
+    """The config-3 batch (4 x 512x512 + 2 x 512x1024, plus a tall and a small matrix, 8 matrices
+    over 8 lanes, and 11 so that lanes are reused) through the batched entry equals one call per
+    matrix, bit for bit (same kernels; the lanes only change where they run)."""
+    shapes = CONFIG3 + [(1024, 512), (64, 32), (512, 512), (100, 300), (32, 32)]
+    mats = [rng.normal(0x310 + i, r * c, 0.0, 0.02).reshape(r, c).astype(np.float32)
+            for i, (r, c) in enumerate(shapes)]
+    batch = [torch.from_numpy(m).cuda() for m in mats]
+    D.newton_schulz_batch(batch, coeffs=O.BASELINE_COEFFS, math=math_)
+    torch.cuda.synchronize()
+    for m, b in zip(mats, batch):
+        single = torch.from_numpy(m).cuda()
+        D.newton_schulz(single, coeffs=O.BASELINE_COEFFS, math=math_)
+        assert torch.equal(b, single)
+
+
 def test_fast_ns_orthogonalises(gpu):
     # size-independent property at the full config-3 size: singular values pushed into the
     # quintic's fixed band (the constant-coefficient schedule leaves them in about [0.68, 1.2])
