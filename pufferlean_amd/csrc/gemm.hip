@@ -20,6 +20,7 @@
 #include "kernels.hpp"
 
 #include <type_traits>
+#include <utility>
 
 namespace ph {
 namespace {
@@ -136,13 +137,33 @@ __device__ __forceinline__ void chunk_rk(int tid, int c, int& r, int& k) {
   }
 }
 
+// LDS placement of operand element (row, k) inside one k-tile buffer.
+//  BK == 32: unpadded 64-byte rows. The four 16-byte k-chunks of a row are XOR-swizzled by row bits
+//    2-3, and the rows of each aligned group of four are permuted by row bits 3-4. Both MFMA operand
+//    reads (16 rows x one chunk per 16 lanes), 16-byte tile stores (4 rows x 4 chunks) and the
+//    transposed 8/4-byte stores (rows 8 apart in one instruction) then hit distinct banks.
+//  otherwise: rows padded by 8 elements (a 144-byte pitch at BK = 64 is already conflict-free).
+template <int BK>
+struct LdsLayout {
+  static constexpr bool kSwz = BK == 32;
+  static constexpr int kPitch = kSwz ? BK : BK + 8;  // elements per row
+  __device__ static __forceinline__ int off(int row, int k) {
+    if constexpr (kSwz) {
+      const int pr = row ^ ((row >> 3) & 3);
+      return pr * 32 + ((((k >> 3) ^ (row >> 2)) & 3) << 3) + (k & 7);
+    } else {
+      return row * kPitch + k;
+    }
+  }
+};
+
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int j) {
   return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
 
 // v[c] holds the 8 bf16 of source k row (k + c) at columns r..r+7. Writes LDS rows r..r+7, each
 // the CH elements k..k+CH-1 (one 8-byte or 4-byte store per row).
-template <int CH, int LDK>
+template <int CH, typename Lay>
 __device__ __forceinline__ void put_trans(uint16_t* dst, int r, int k, const uint4 (&v)[CH]) {
   static_assert(CH == 2 || CH == 4, "transposed store width");
 #pragma unroll
@@ -155,10 +176,16 @@ __device__ __forceinline__ void put_trans(uint16_t* dst, int r, int k, const uin
       // column r+q of rows k+2p (low half) and k+2p+1 (high half)
       w[p] = (q & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
     }
-    uint16_t* p = &dst[(r + q) * LDK + k];
+    uint16_t* p = &dst[Lay::off(r + q, k)];  // CH elements stay inside one 8-element chunk
     if constexpr (CH == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
     else *reinterpret_cast<uint32_t*>(p) = w[0];
   }
+}
+
+// Runs f(kt + i, set i % NS, LDS buffer i % 2) for i = 0..U-1 with compile-time set and buffer ids.
+template <int NS, typename F, int... I>
+__device__ __forceinline__ void unroll_steps(F& f, int kt, std::integer_sequence<int, I...>) {
+  (f(kt + I, std::integral_constant<int, I % NS>{}, std::integral_constant<int, I % 2>{}), ...);
 }
 
 // Thread-block tile id -> (tile_m, tile_n). With remap, the blocks that land on one XCD (blocks are
@@ -407,8 +434,8 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   static_assert(!X3 || (sizeof(TIA) == 4 && sizeof(TIB) == 4), "split-bf16 needs fp32 operands");
   constexpr int NSPLIT = X3 ? 2 : 1;
   constexpr int NT = WGM * WGN * 64;
-  constexpr int PAD = 8;
-  constexpr int LDK = BK + PAD;             // LDS row pitch in bf16 elements
+  using Lay = LdsLayout<BK>;
+  constexpr int LDK = Lay::kPitch;          // LDS row pitch in bf16 elements
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int SM = WM / 32, SN = WN / 32; // 32x32 sub-tiles per wave
   constexpr int CA = BM * BK / 8 / NT;      // 8-element chunks per thread (A)
@@ -447,8 +474,12 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   const gptr<TIA> A = (gptr<TIA>)g.A;
   const gptr<TIB> B = (gptr<TIB>)g.B;
 
-  Raw8<TIA> ra[2][CA];
-  Raw8<TIB> rb[2][CB];
+  // Prefetch depth: NSETS register sets of k-tiles in flight. Two measured best on the policy shapes
+  // (a depth of four made the 256x128 forward 37 % slower: the longer unrolled body costs more than
+  // the added latency cover).
+  constexpr int NSETS = 2;
+  Raw8<TIA> ra[NSETS][CA];
+  Raw8<TIB> rb[NSETS][CB];
 
   // Global -> register set for the k-tile starting at k0. Every load is issued unconditionally (an
   // out-of-range chunk reads the zero page), so no branch separates the loads and the compiler can
@@ -493,13 +524,13 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   // Register set -> LDS buffer `s` (transposing m/n-contiguous chunks).
   auto put = [&](uint16_t* dst, int r, int k, uint4 v, bool trans) {
     if (!trans) {
-      *reinterpret_cast<uint4*>(&dst[r * LDK + k]) = v;
+      *reinterpret_cast<uint4*>(&dst[Lay::off(r, k)]) = v;
     } else {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        dst[(r + 2 * q) * LDK + k] = (uint16_t)(w[q] & 0xffffu);
-        dst[(r + 2 * q + 1) * LDK + k] = (uint16_t)(w[q] >> 16);
+        dst[Lay::off(r + 2 * q, k)] = (uint16_t)(w[q] & 0xffffu);
+        dst[Lay::off(r + 2 * q + 1, k)] = (uint16_t)(w[q] >> 16);
       }
     }
   };
@@ -517,8 +548,8 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
       }
       int r, k;
       chunk_rk<TR, R, BK, CH, NT>(tid, 0, r, k);
-      put_trans<CH, LDK>(dst, r, k, v);
-      if constexpr (X3) put_trans<CH, LDK>(dstl, r, k, l);
+      put_trans<CH, Lay>(dst, r, k, v);
+      if constexpr (X3) put_trans<CH, Lay>(dstl, r, k, l);
     } else {
 #pragma unroll
       for (int c = 0; c < CH; c++) {
@@ -556,15 +587,15 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
       uint4 a0[SM], a1[SM], b0[SN], b1[SN];
 #pragma unroll
       for (int i = 0; i < SM; i++) {
-        const uint16_t* p = &sA[s][(wm0 + i * 32 + lr) * LDK + kb + lk];
-        a0[i] = *reinterpret_cast<const uint4*>(p);
-        a1[i] = *reinterpret_cast<const uint4*>(p + 8);
+        const int row = wm0 + i * 32 + lr;
+        a0[i] = *reinterpret_cast<const uint4*>(&sA[s][Lay::off(row, kb + lk)]);
+        a1[i] = *reinterpret_cast<const uint4*>(&sA[s][Lay::off(row, kb + lk + 8)]);
       }
 #pragma unroll
       for (int j = 0; j < SN; j++) {
-        const uint16_t* p = &sB[s][(wn0 + j * 32 + lr) * LDK + kb + lk];
-        b0[j] = *reinterpret_cast<const uint4*>(p);
-        b1[j] = *reinterpret_cast<const uint4*>(p + 8);
+        const int row = wn0 + j * 32 + lr;
+        b0[j] = *reinterpret_cast<const uint4*>(&sB[s][Lay::off(row, kb + lk)]);
+        b1[j] = *reinterpret_cast<const uint4*>(&sB[s][Lay::off(row, kb + lk + 8)]);
       }
       // all accumulators once with the first k half, then once with the second: consecutive
       // MFMAs never depend on each other
@@ -581,9 +612,9 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
         // hi(A) * lo(B)
 #pragma unroll
         for (int j = 0; j < SN; j++) {
-          const uint16_t* p = &sBl[s][(wn0 + j * 32 + lr) * LDK + kb + lk];
-          l0[j] = *reinterpret_cast<const uint4*>(p);
-          l1[j] = *reinterpret_cast<const uint4*>(p + 8);
+          const int row = wn0 + j * 32 + lr;
+          l0[j] = *reinterpret_cast<const uint4*>(&sBl[s][Lay::off(row, kb + lk)]);
+          l1[j] = *reinterpret_cast<const uint4*>(&sBl[s][Lay::off(row, kb + lk + 8)]);
         }
 #pragma unroll
         for (int i = 0; i < SM; i++)
@@ -596,9 +627,9 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
         // lo(A) * hi(B)
 #pragma unroll
         for (int i = 0; i < SM; i++) {
-          const uint16_t* p = &sAl[s][(wm0 + i * 32 + lr) * LDK + kb + lk];
-          l0[i] = *reinterpret_cast<const uint4*>(p);
-          l1[i] = *reinterpret_cast<const uint4*>(p + 8);
+          const int row = wm0 + i * 32 + lr;
+          l0[i] = *reinterpret_cast<const uint4*>(&sAl[s][Lay::off(row, kb + lk)]);
+          l1[i] = *reinterpret_cast<const uint4*>(&sAl[s][Lay::off(row, kb + lk + 8)]);
         }
 #pragma unroll
         for (int i = 0; i < SM; i++)
@@ -612,35 +643,35 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
     }
   };
 
-  // The k loop runs over an even number of tiles with no conditional work inside: a tile at or past
-  // kend is loaded from a clamped address and written to LDS as zeros (so an odd tile count gets one
-  // zero tile), and the prefetch of the two tiles past the end is issued the same way. Every load
-  // is therefore issued on every path, which lets the compiler wait for exactly the register set a
+  // The k loop runs over a multiple of U = lcm(NSETS, 2) tiles with no conditional work inside: a
+  // tile at or past kend is loaded from the zero page and written to LDS as zeros (so the padding
+  // tiles add nothing), and the prefetches past the end are issued the same way. Every load is
+  // therefore issued on every path, which lets the compiler wait for exactly the register set a
   // store needs and keep the accumulators in place across iterations.
-  const int nk2 = (nk + 1) & ~1;
-  // Prologue: tile 0 -> LDS buffer 0, tile 1 -> register set 1 (in flight).
-  if (nk2 > 0) {
-    gload(ra[0], rb[0], kbeg);
-    gload(ra[1], rb[1], kbeg + BK);
+  constexpr int U = NSETS % 2 == 0 ? NSETS : 2 * NSETS;
+  const int nkU = (nk + U - 1) / U * U;
+  // Prologue: tiles 0..NSETS-1 into register sets 0..NSETS-1, tile 0 -> LDS buffer 0.
+  if (nkU > 0) {
+#pragma unroll
+    for (int q = 0; q < NSETS; q++) gload(ra[q], rb[q], kbeg + q * BK);
     sstore(ra[0], rb[0], 0);
     lds_barrier();
   }
-  // Step for tile kt held in LDS buffer P; register set P^1 holds tile kt+1; set P receives kt+2.
-  // The phases are fenced against the instruction scheduler: the prefetch is issued first and the
-  // LDS store of the older set comes after the MFMAs, so each set has a full step to arrive.
-  auto step = [&](int kt, auto Pc) {
-    constexpr int P = decltype(Pc)::value;
-    gload(ra[P], rb[P], kbeg + (kt + 2) * BK);
+  // Step for tile kt held in LDS buffer P = kt % 2: register set S = kt % NSETS receives tile
+  // kt + NSETS, set (S + 1) % NSETS (tile kt + 1) goes to the other LDS buffer. The phases are fenced
+  // against the instruction scheduler: the prefetch is issued first and the LDS store of the older
+  // set comes after the MFMAs, so each set has NSETS - 1 full steps to arrive.
+  auto step = [&](int kt, auto Sc, auto Pc) {
+    constexpr int S = decltype(Sc)::value, P = decltype(Pc)::value;
+    constexpr int S1 = (S + 1) % NSETS;
+    gload(ra[S], rb[S], kbeg + (kt + NSETS) * BK);
     __builtin_amdgcn_sched_barrier(0);
     compute(P);
     __builtin_amdgcn_sched_barrier(0);
-    sstore(ra[P ^ 1], rb[P ^ 1], P ^ 1);
+    sstore(ra[S1], rb[S1], P ^ 1);
     lds_barrier();
   };
-  for (int kt = 0; kt < nk2; kt += 2) {
-    step(kt, std::integral_constant<int, 0>{});
-    step(kt + 1, std::integral_constant<int, 1>{});
-  }
+  for (int kt = 0; kt < nkU; kt += U) unroll_steps<NSETS>(step, kt, std::make_integer_sequence<int, U>{});
 
   // the last loop iteration ended with a barrier: the pipeline buffers are free for the C tile
   if constexpr (EPR == BM) {
