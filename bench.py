@@ -228,7 +228,7 @@ def bench_ns(steps, warmup):
     mats = [_t(rng.normal(rng.seed_for(3, i), r * c, 0.0, 0.02)).view(r, c) for i, (r, c) in enumerate(shapes)]
     work = [m.clone() for m in mats]
 
-    # the six matrices run concurrently on the library's stream lanes (ph_newton_schulz_batch)
+    # the six matrices in one fused launch (ph_newton_schulz_batch)
     run = lambda: D.newton_schulz_batch(work, coeffs=D.CONST_COEFFS, math="bf16")
     ms = time_graph(run, max(steps // 5, 3), warmup)
     ms_eager = time_loop(run, max(steps // 5, 3), warmup)

@@ -14,6 +14,8 @@ enum : int {
   kSlotPpoCounter = 5,
   kSlotGemmWs = 6,
   kSlotNs = 8,        // Newton-Schulz buffers of the stand-alone entry points
+  kSlotNsCtl = 9,     // work-item counters of the fused Newton-Schulz launch (256 bytes)
+  kSlotMuonU = 10,    // Nesterov updates of a batched Muon step
   kSlotMuonExact = 16,
   kSlotMuonFastU = 17,
   kSlotGclip = 18,
@@ -84,6 +86,26 @@ int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int ns
 int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,
               float wd, float mu, float eps, const float* coeffs, int nsteps, int math,
               const LaneSlots& slots, hipStream_t st);
+
+// Fused bf16-MFMA Newton-Schulz of up to kNsMaxMats matrices per launch (more are run as further
+// launches on `st`): X[i] (rows[i] x cols[i], fp32) is normalised and orthogonalised in place.
+// ws_slot holds the per-matrix, per-step iterates and products (ns_fused_ws_bytes per matrix),
+// ctl_slot the launch's work-item counters; two calls that overlap in time must not share either.
+constexpr int kNsMaxMats = 16;
+constexpr int kNsMaxSteps = 64;
+int ns_fused(float* const* X, const int* rows, const int* cols, int n, const float* coeffs, int nsteps,
+             float eps, int ws_slot, int ctl_slot, hipStream_t st);
+size_t ns_fused_ws_bytes(int rows, int cols, int nsteps);
+
+// Muon on several fp32 matrices: Nesterov into scratch, one Newton-Schulz batch, weight update.
+struct MuonMat {
+  float* W;
+  const float* G;
+  float* M;
+  int rows, cols;
+};
+int muon_fast_batch(const MuonMat* mats, int n, float gscale, float lr, float wd, float mu, float eps,
+                    const float* coeffs, int nsteps, int math, hipStream_t st);
 int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
                 hipStream_t st);
 int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);

@@ -441,8 +441,7 @@ int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float*
 }
 
 // Clip the summed gradient and apply Muon to every matrix (fp32 master weights), stepvec to biases.
-// The matrix updates are independent: each runs on its own library stream lane (own scratch),
-// forked from and joined back into `st`; the bias updates run on `st` meanwhile.
+// The matrices' Newton-Schulz iterations run together in one fused launch.
 int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, float* mom, float* G,
                 hipStream_t st) {
   const int H = d.H, D = d.D, L = d.L, A = d.A;
@@ -451,27 +450,23 @@ int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, 
   const long szE = (long)H * D, szL = 3L * H * H;
   const long offBEnc = szE, offW = szE + H, offDec = offW + (long)L * szL, offBDec = offDec + (long)A * H,
              offVal = offBDec + A, offBVal = offVal + H;
-  struct Mat { long off; int rows, cols; };
-  Mat mats[kLanes];
+  PH_REQUIRE(L + 3 <= kNsMaxMats, "mingru: at most %d layers", kNsMaxMats - 3);
+  MuonMat mats[kNsMaxMats];
   int nm = 0;
-  mats[nm++] = {0, H, D};
-  for (int l = 0; l < L; l++) mats[nm++] = {offW + l * szL, 3 * H, H};
-  mats[nm++] = {offDec, A, H};
-  mats[nm++] = {offVal, 1, H};
-  PH_REQUIRE(nm <= kLanes, "mingru: at most %d weight matrices (layers <= %d)", kLanes, kLanes - 3);
-  PH_TRY(fork_lanes(st, nm));
-  for (int i = 0; i < nm; i++)
-    PH_TRY(muon_fast(params + mats[i].off, G + mats[i].off, mom + mats[i].off, mats[i].rows,
-                     mats[i].cols, 1.f, m.lr, m.wd, m.mu, m.eps, m.coeffs, m.nsteps, m.math,
-                     lane_slots(i), lane_stream(i)));
+  auto mat = [&](long off, int rows, int cols) {
+    mats[nm++] = MuonMat{params + off, G + off, mom + off, rows, cols};
+  };
+  mat(0, H, D);
+  for (int l = 0; l < L; l++) mat(offW + l * szL, 3 * H, H);
+  mat(offDec, A, H);
+  mat(offVal, 1, H);
   auto vec = [&](long off, long n) {
     return stepvec_f32(params + off, G + off, mom + off, n, 1.f, m.lr, m.wd, m.mu, st);
   };
   PH_TRY(vec(offBEnc, H));
   PH_TRY(vec(offBDec, A));
   PH_TRY(vec(offBVal, 1));
-  PH_TRY(join_lanes(st, nm));
-  return PH_OK;
+  return muon_fast_batch(mats, nm, 1.f, m.lr, m.wd, m.mu, m.eps, m.coeffs, m.nsteps, m.math, st);
 }
 
 int mingru_step(const ph_mingru_dims& d, const ph_ppo_coefs& c, const ph_muon_coefs& m,

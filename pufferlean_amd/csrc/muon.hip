@@ -5,7 +5,8 @@
 //  * exact (f64): naive matmuls that sum over the shared index in ascending order, the two-level
 //    Frobenius fold (rows in parallel, then rows summed in order by one lane) and contraction
 //    disabled, so every value matches the reference CPU step (pufferblas.c:1369-1406) bit for bit.
-//  * fast: the quintic iterate on MFMA GEMMs (bf16 or fp32 math, fp32 state), wide form
+//  * fast, bf16 MFMA: the whole batch's quintic in one fused launch (ns.hip).
+//  * fast, fp32 MFMA: the quintic iterate as a chain of GEMMs (fp32 state), wide form
 //    X <- aX + (bA + cA^2)X with A = XX^T; A and A^2 are symmetric, so A^2 = A A^T is computed by
 //    the same NT kernel as XX^T, and the b/c/a combinations are fused into the GEMM epilogues.
 //    Tall matrices are transposed to wide on the way in and back on the way out.
@@ -264,7 +265,8 @@ int stepvec_exact(long n, const double* b, const double* g, const double* m, dou
   return PH_OK;
 }
 
-// ---- fast tier: in-place NS of one fp32 matrix --------------------------------------------------
+// ---- fast tier as a GEMM chain: in-place NS of one fp32 matrix -------------------------------------
+// Used for fp32 MFMA math and for zero steps (normalisation only); bf16 runs fused (ns.hip).
 // Per step, all operands read straight from fp32 buffers:
 //   A  = X X^T                 (bf16 MFMA; math == PH_MATH_F32: fp32 MFMA)
 //   B  = b A + c A A^T         (split-bf16 MFMA, epilogue b*A + c*acc)
@@ -343,6 +345,48 @@ int muon_fast(float* W, const float* G, float* M, int rows, int cols, float gsca
   return PH_OK;
 }
 
+int muon_fast_batch(const MuonMat* mats, int n, float gscale, float lr, float wd, float mu, float eps,
+                    const float* coeffs, int nsteps, int math, hipStream_t st) {
+  if (n <= 0) return PH_OK;
+  if (n > kNsMaxMats) {
+    set_error("muon: at most %d matrices per batch", kNsMaxMats);
+    return PH_ERR_UNSUPPORTED;
+  }
+  size_t tot = 0;
+  long off[kNsMaxMats];
+  for (int i = 0; i < n; i++) {
+    off[i] = (long)tot;
+    tot += ((size_t)mats[i].rows * mats[i].cols + 63) & ~(size_t)63;  // 256-byte aligned updates
+  }
+  float* U = (float*)scratch(kSlotMuonU, tot * 4 + 4);
+  if (!U) return PH_ERR_NOMEM;
+  float* X[kNsMaxMats];
+  int rows[kNsMaxMats], cols[kNsMaxMats];
+  for (int i = 0; i < n; i++) {
+    const long e = (long)mats[i].rows * mats[i].cols;
+    X[i] = U + off[i];
+    rows[i] = mats[i].rows;
+    cols[i] = mats[i].cols;
+    if (e == 0) continue;
+    k_nesterov_f32<<<ceil_div(e, kB), kB, 0, st>>>(mats[i].G, mats[i].M, X[i], e, gscale, mu);
+    PH_LAUNCH_CHECK();
+  }
+  if (math == PH_MATH_F32 || nsteps == 0) {
+    for (int i = 0; i < n; i++)
+      PH_TRY(newton_schulz_fast(X[i], rows[i], cols[i], coeffs, nsteps, eps, math, kSlotNs, 0, st));
+  } else {
+    PH_TRY(ns_fused(X, rows, cols, n, coeffs, nsteps, eps, kSlotNs, kSlotNsCtl, st));
+  }
+  for (int i = 0; i < n; i++) {
+    const long e = (long)rows[i] * cols[i];
+    if (e == 0) continue;
+    const float scale = sqrtf(fmaxf(1.f, (float)rows[i] / (float)cols[i]));
+    k_finalize_f32<<<ceil_div(e, kB), kB, 0, st>>>(mats[i].W, X[i], e, 1.f - lr * wd, lr * scale);
+    PH_LAUNCH_CHECK();
+  }
+  return PH_OK;
+}
+
 int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
                 hipStream_t st) {
   if (n == 0) return PH_OK;
@@ -389,7 +433,9 @@ extern "C" int ph_newton_schulz(float* X, int rows, int cols, const float* coeff
   PH_REQUIRE(math == PH_MATH_BF16 || math == PH_MATH_F32 || math == PH_MATH_BF16X3,
              "ph_newton_schulz: unknown math");
   PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_newton_schulz: coefficient table missing");
-  return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, 0, as_stream(stream));
+  if (math == PH_MATH_F32 || nsteps == 0)
+    return newton_schulz_fast(X, rows, cols, coeffs, nsteps, eps, math, kSlotNs, 0, as_stream(stream));
+  return ns_fused(&X, &rows, &cols, 1, coeffs, nsteps, eps, kSlotNs, kSlotNsCtl, as_stream(stream));
 }
 
 extern "C" int ph_newton_schulz_batch(float* const* X, const int* rows, const int* cols, int n,
@@ -401,9 +447,12 @@ extern "C" int ph_newton_schulz_batch(float* const* X, const int* rows, const in
              "ph_newton_schulz_batch: unknown math");
   for (int i = 0; i < n; i++) PH_REQUIRE(rows[i] >= 0 && cols[i] >= 0, "ph_newton_schulz_batch: bad shape");
   if (n == 0) return PH_OK;
-  // The matrices are independent: matrix i runs on stream lane i % kLanes with that lane's scratch;
-  // the lanes fork from and join back into `stream`.
   hipStream_t st = as_stream(stream);
+  // bf16: the whole batch in fused launches on `stream`
+  if (math != PH_MATH_F32 && nsteps > 0)
+    return ns_fused(X, rows, cols, n, coeffs, nsteps, eps, kSlotNs, kSlotNsCtl, st);
+  // fp32 MFMA: matrix i runs on stream lane i % kLanes with that lane's scratch; the lanes fork
+  // from and join back into `stream`.
   const int nl = n < kLanes ? n : kLanes;
   PH_TRY(fork_lanes(st, nl));
   for (int i = 0; i < n; i++) {
@@ -419,8 +468,10 @@ extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int col
                            int math, void* stream) {
   PH_REQUIRE(rows >= 0 && cols >= 0 && nsteps >= 0 && nsteps <= 64, "ph_muon_mat: bad shape");
   PH_REQUIRE(coeffs != nullptr || nsteps == 0, "ph_muon_mat: coefficient table missing");
-  return muon_fast(W, G, M, rows, cols, gscale, lr, wd, mu, eps, coeffs, nsteps, math,
-                   LaneSlots{kSlotMuonFastU, kSlotNs, 0}, as_stream(stream));
+  PH_REQUIRE(math == PH_MATH_BF16 || math == PH_MATH_F32 || math == PH_MATH_BF16X3,
+             "ph_muon_mat: unknown math");
+  const MuonMat mm{W, G, M, rows, cols};
+  return muon_fast_batch(&mm, 1, gscale, lr, wd, mu, eps, coeffs, nsteps, math, as_stream(stream));
 }
 
 extern "C" int ph_stepvec(float* b, const float* g, float* m, size_t n, float gscale, float lr,
