@@ -40,6 +40,8 @@ int join_lanes(hipStream_t main, int n);  // main waits for everything queued on
 
 // Zero a 256-byte arrival-counter block once per pointer (fill kernel, no memset node).
 int ensure_zeroed_counter(unsigned* counter, hipStream_t st);
+// The same for a block of n words (a fixed-size scratch slot: its pointer never changes).
+int ensure_zeroed_words(unsigned* words, int n, hipStream_t st);
 
 struct PhGemmDesc {
   int trans_a, trans_b, M, N, K;

@@ -51,8 +51,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 8 bf16 (native v
 
 constexpr int kT = 64;          // output tile edge and k chunk
 constexpr int kPitch = kT + 8;  // LDS row pitch in bf16 elements (144 B: conflict-free MFMA reads)
-constexpr int kThreads = 256;
-constexpr int kSets = 4;        // k chunks in flight per block (register prefetch depth)
+constexpr int kGroups = 2;      // k-groups per block: each takes every other k chunk of a tile
+constexpr int kThreads = 256 * kGroups;  // a k-group is 4 wavefronts, one per 32x32 quadrant
+constexpr int kSets = 4;        // k chunks in flight per k-group (register prefetch depth)
 constexpr unsigned kSpinLimit = 1u << 20;  // bounded wait (about a second); never reached in a valid run
 
 struct NsMat {
@@ -61,11 +62,15 @@ struct NsMat {
   int rows, cols;
 };
 
+// Control words, each polled or updated one on its own 128-byte line: next ticket, blocks finished,
+// wait limit hit in this launch (+1: ever hit, never cleared), items done per matrix.
+constexpr int kCtlTicket = 0, kCtlOut = 32, kCtlFlag = 64, kCtlDone = 96, kCtlStride = 32;
+constexpr int kCtlWords = kCtlDone + kCtlStride * kNsMaxMats;
+
 struct NsLaunch {
   NsMat mat[kNsMaxMats];
   float coef[3 * kNsMaxSteps];
-  unsigned* ctl;  // [0] next ticket, [1] blocks finished, [2] wait limit hit in this launch,
-                  // [3] wait limit ever hit (never cleared), [4 + g] items done of matrix g
+  unsigned* ctl;  // control words (kCtl*)
   long n0, nt, n3;  // item counts of P0, of P1 (= P2) and of P3, summed over the matrices
   int nmat, nsteps;
   float eps;
@@ -182,13 +187,13 @@ __device__ inline void tri_coords(long r, int& ti, int& tj) {
   tj = (int)(r - (long)i * (i + 1) / 2);
 }
 
-// acc0 + acc1 = sum over the nseg operand pairs of A_s[64 rows][K] . B_s[64 rows][K]^T for this
-// wavefront's 32x32 quadrant (wr, wc). A_s / B_s point at the tile's first row; rows are ld apart;
-// K is a multiple of 64. Chunks are loaded kSets - 1 ahead into registers, staged through
-// double-buffered LDS, and read as one 16-byte fragment per lane per MFMA.
-// Segment s of the A operand starts at a + ((amask >> s) & 1) * da (likewise B): the products'
-// operand buffers (hi/lo halves) sit at fixed distances, so a segment's source is plain arithmetic
-// (a pointer table indexed by the segment would be placed in scratch memory).
+// acc0 + acc1 = this k-group's share of the sum over the nseg operand pairs of
+// A_s[64 rows][K] . B_s[64 rows][K]^T, for this wavefront's 32x32 quadrant (wr, wc): k-group g
+// takes chunks g, g + kGroups, ... of the concatenated k range. A_s / B_s point at the tile's first
+// row; rows are ld apart; K is a multiple of 64. Chunks are loaded kSets - 1 steps ahead into
+// registers, staged through the group's double-buffered LDS, and read as one 16-byte fragment per
+// lane per MFMA. Both groups run the same number of steps (block barriers stay matched); a step
+// whose chunk is past the end only skips its MFMAs.
 struct TileOps {
   const uint16_t *a, *b;
   long da, db;
@@ -199,18 +204,23 @@ struct TileOps {
 };
 
 template <int... I>
-__device__ __forceinline__ void mma_tile(const TileOps& op, uint16_t (*sA)[kT * kPitch],
-                                         uint16_t (*sB)[kT * kPitch], floatx16& acc0, floatx16& acc1,
+__device__ __forceinline__ void mma_tile(const TileOps& op, uint16_t (*sA)[2][kT * kPitch],
+                                         uint16_t (*sB)[2][kT * kPitch], floatx16& acc0, floatx16& acc1,
                                          std::integer_sequence<int, I...>) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int grp = wave >> 2, gw = wave & 3;
+  const int wr = gw >> 1, wc = gw & 1;
   const int lr = lane & 31, lk = (lane >> 5) * 16;
   const int kc = op.K / kT;
   const int nc = op.nseg * kc;
+  const int nsteps = (nc + kGroups - 1) / kGroups;
+  uint16_t (*gA)[kT * kPitch] = sA[grp];
+  uint16_t (*gB)[kT * kPitch] = sB[grp];
   // this thread's two 16-byte pieces of each 64x64 operand chunk
-  const int prow = tid >> 3, pk = (tid & 7) * 8;
+  const int gt = tid & 255, prow = gt >> 3, pk = (gt & 7) * 8;
   u32x4 ra[kSets][2], rb[kSets][2];
-  auto gload = [&](u32x4 (&xa)[2], u32x4 (&xb)[2], int c) __attribute__((always_inline)) {
+  auto gload = [&](u32x4 (&xa)[2], u32x4 (&xb)[2], int i) __attribute__((always_inline)) {
+    int c = i * kGroups + grp;
     c = c < nc ? c : nc - 1;  // past the end: reload the last chunk (never computed on)
     const int s = c / kc, k0 = (c - s * kc) * kT;
     const uint16_t* A = op.a + ((op.amask >> s) & 1) * op.da;
@@ -224,8 +234,8 @@ __device__ __forceinline__ void mma_tile(const TileOps& op, uint16_t (*sA)[kT * 
   auto sstore = [&](const u32x4 (&xa)[2], const u32x4 (&xb)[2], int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      *reinterpret_cast<u32x4*>(&sA[buf][(prow + 32 * h) * kPitch + pk]) = xa[h];
-      *reinterpret_cast<u32x4*>(&sB[buf][(prow + 32 * h) * kPitch + pk]) = xb[h];
+      *reinterpret_cast<u32x4*>(&gA[buf][(prow + 32 * h) * kPitch + pk]) = xa[h];
+      *reinterpret_cast<u32x4*>(&gB[buf][(prow + 32 * h) * kPitch + pk]) = xb[h];
     }
   };
   auto mfma = [&](floatx16& c, const u32x4& a, const u32x4& b) __attribute__((always_inline)) {
@@ -235,8 +245,8 @@ __device__ __forceinline__ void mma_tile(const TileOps& op, uint16_t (*sA)[kT * 
   auto compute = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < kT; kb += 32) {
-      const uint16_t* pa = &sA[buf][(wr * 32 + lr) * kPitch + kb + lk];
-      const uint16_t* pb = &sB[buf][(wc * 32 + lr) * kPitch + kb + lk];
+      const uint16_t* pa = &gA[buf][(wr * 32 + lr) * kPitch + kb + lk];
+      const uint16_t* pb = &gB[buf][(wc * 32 + lr) * kPitch + kb + lk];
       const u32x4 a0 = *reinterpret_cast<const u32x4*>(pa), a1 = *reinterpret_cast<const u32x4*>(pa + 8);
       const u32x4 b0 = *reinterpret_cast<const u32x4*>(pb), b1 = *reinterpret_cast<const u32x4*>(pb + 8);
       mfma(acc0, a0, b0);
@@ -248,28 +258,29 @@ __device__ __forceinline__ void mma_tile(const TileOps& op, uint16_t (*sA)[kT * 
   (gload(ra[I], rb[I], I), ...);
   sstore(ra[0], rb[0], 0);
   lds_barrier();
-  // step c (set S = c % kSets): refill set S with chunk c + kSets, compute chunk c, stage c + 1
-  auto step = [&](int c, auto Sc) __attribute__((always_inline)) {
+  // step i (set S = i % kSets): refill set S with step i + kSets's chunk, compute step i's chunk,
+  // stage step i + 1's
+  auto step = [&](int i, auto Sc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value, S1 = (S + 1) % kSets;
-    if (c >= nc) return;
-    gload(ra[S], rb[S], c + kSets);
+    if (i >= nsteps) return;
+    gload(ra[S], rb[S], i + kSets);
     __builtin_amdgcn_sched_barrier(0);
-    compute(c & 1);
+    if (i * kGroups + grp < nc) compute(i & 1);
     __builtin_amdgcn_sched_barrier(0);
-    sstore(ra[S1], rb[S1], (c + 1) & 1);
+    sstore(ra[S1], rb[S1], (i + 1) & 1);
     lds_barrier();
   };
-  for (int c = 0; c < nc; c += kSets) (step(c + I, std::integral_constant<int, I>{}), ...);
+  for (int i = 0; i < nsteps; i += kSets) (step(i + I, std::integral_constant<int, I>{}), ...);
 }
 
 // Accumulator element e of this lane sits at tile row wr*32 + 8*(e/4) + 4*(lane/32) + e%4 and
 // tile column wc*32 + lane%32.
 __device__ __forceinline__ int acc_row(int e) {
-  const int lane = threadIdx.x & 63, wr = (threadIdx.x >> 6) >> 1;
+  const int lane = threadIdx.x & 63, wr = ((threadIdx.x >> 6) & 3) >> 1;
   return wr * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
 }
 __device__ __forceinline__ int acc_col() {
-  const int lane = threadIdx.x & 63, wc = (threadIdx.x >> 6) & 1;
+  const int lane = threadIdx.x & 63, wc = ((threadIdx.x >> 6) & 3) & 1;
   return wc * 32 + (lane & 31);
 }
 
@@ -318,19 +329,23 @@ __device__ void p0_convert(const NsMat& mt, const Geo& g, long r, float* stage) 
   __syncthreads();
   if ((tid & 63) == 0) stage[tid >> 6] = ss;
   __syncthreads();
-  if (tid == 0) st_dev(&g.part[r], (stage[0] + stage[1]) + (stage[2] + stage[3]));
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kThreads / 64; w++) t += stage[w];
+    st_dev(&g.part[r], t);
+  }
 }
 
-__global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
-  __shared__ __align__(16) uint16_t sA[2][kT * kPitch];
-  __shared__ __align__(16) uint16_t sB[2][kT * kPitch];
+__global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
+  __shared__ __align__(16) uint16_t sA[kGroups][2][kT * kPitch];
+  __shared__ __align__(16) uint16_t sB[kGroups][2][kT * kPitch];
   __shared__ unsigned s_ticket;
   unsigned* ctl = L.ctl;
   const long per = 2 * L.nt + L.n3;
   const long total = L.n0 + (long)L.nsteps * per;
   const int tid = threadIdx.x;
   for (;;) {
-    if (tid == 0) s_ticket = __hip_atomic_fetch_add(&ctl[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) s_ticket = __hip_atomic_fetch_add(&ctl[kCtlTicket], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const long t = (long)s_ticket;
     __syncthreads();
@@ -358,14 +373,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
       r -= cnt;
     }
     const NsMat mt = L.mat[gi];  // a copy: a reference would move the kernel argument to scratch
-    unsigned* done = &ctl[4 + gi];
+    unsigned* done = &ctl[kCtlDone + kCtlStride * gi];
     if (p == 0) {
-      p0_convert(mt, g, r, reinterpret_cast<float*>(&sA[0][0]));
+      p0_convert(mt, g, r, reinterpret_cast<float*>(&sA[0][0][0]));
       signal_done(done);
       continue;
     }
     const long need = g.n0 + (long)s * (2 * g.nt + g.n3) + (p - 1) * g.nt;
-    wait_done(done, (unsigned)need, &ctl[2]);
+    wait_done(done, (unsigned)need, &ctl[kCtlFlag]);
     const float a = L.coef[3 * s], b = L.coef[3 * s + 1], c = L.coef[3 * s + 2];
     const float sc = s == 0 ? norm_scale(g.part, g.n0, L.eps) : 1.f;
     const long xs = (long)s * g.mw, es = (long)s * g.mm;  // this step's buffers
@@ -409,9 +424,22 @@ __global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
     }
     floatx16 acc0, acc1;
     mma_tile(op, sA, sB, acc0, acc1, std::make_integer_sequence<int, kSets>{});
+    // fold k-group 1's partial tile into group 0's (fixed order), through LDS
+    float* red = reinterpret_cast<float*>(&sA[0][0][0]);
+    if (tid >= 256) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) red[e * 256 + (tid - 256)] = acc0[e] + acc1[e];
+    }
+    __syncthreads();
+    if (tid < 256) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc0[e] = (acc0[e] + acc1[e]) + red[e * 256 + tid];
+    }
     const int col = tj * kT + acc_col();
     const int row0 = ti * kT;
-    if (p == 1 || p == 2) {
+    if (tid >= 256) {
+      // k-group 1 is done with this item
+    } else if (p == 1 || p == 2) {
       uint16_t* hi = (p == 1 ? g.eh : g.bh) + es;
       uint16_t* lo = (p == 1 ? g.el : g.bl) + es;
       float* ef = g.ef + es;
@@ -424,7 +452,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
           const int e = 4 * q + e4;
           const int row = row0 + acc_row(e);
           const long o = (long)row * g.mp + col;
-          const float v = acc0[e] + acc1[e];
+          const float v = acc0[e];
           float val;
           if (p == 1) {
             val = sc * sc * v - (row == col ? 1.f : 0.f);
@@ -457,7 +485,7 @@ __global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
           const int e = 4 * q + e4;
           const int row = row0 + acc_row(e);
           const long o = (long)row * g.wp + col;
-          const float v = sc * (abc * xfc[o] + (acc0[e] + acc1[e]));
+          const float v = sc * (abc * xfc[o] + acc0[e]);
           if (last) {
             if (row < g.m && col < g.w) {
               if (g.tall) mt.x[(long)col * mt.cols + row] = v;
@@ -477,12 +505,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_ns_fused(const NsLaunch L) {
   // leave; the last block out resets the counters (every other block has taken its final ticket
   // and finished its items)
   if (tid == 0) {
-    const unsigned out = __hip_atomic_fetch_add(&ctl[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned out = __hip_atomic_fetch_add(&ctl[kCtlOut], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (out == gridDim.x - 1) {
-      __hip_atomic_store(&ctl[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ctl[2], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int i = 0; i < L.nmat; i++) __hip_atomic_store(&ctl[4 + i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ctl[1], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kCtlTicket], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kCtlFlag], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < L.nmat; i++)
+        __hip_atomic_store(&ctl[kCtlDone + kCtlStride * i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[kCtlOut], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -512,9 +541,9 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
     set_error("newton_schulz (fused): steps must be in 1..%d", kNsMaxSteps);
     return PH_ERR_UNSUPPORTED;
   }
-  unsigned* ctl = (unsigned*)scratch(ctl_slot, 256);
+  unsigned* ctl = (unsigned*)scratch(ctl_slot, kCtlWords * 4);
   if (!ctl) return PH_ERR_NOMEM;
-  PH_TRY(ensure_zeroed_counter(ctl, st));
+  PH_TRY(ensure_zeroed_words(ctl, kCtlWords, st));
   int i = 0;
   while (i < n) {
     // next group of at most kNsMaxMats non-empty matrices

@@ -57,22 +57,23 @@ void* scratch(int slot, size_t bytes) {
 
 namespace {
 __global__ void k_zero_words(unsigned* p, int n) {
-  int i = threadIdx.x;
-  if (i < n) p[i] = 0u;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
 }
 std::set<void*> g_zeroed;
 }  // namespace
 
-int ensure_zeroed_counter(unsigned* counter, hipStream_t st) {
+int ensure_zeroed_words(unsigned* words, int n, hipStream_t st) {
   {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (g_zeroed.count(counter)) return PH_OK;
-    g_zeroed.insert(counter);
+    if (g_zeroed.count(words)) return PH_OK;
+    g_zeroed.insert(words);
   }
-  k_zero_words<<<1, 64, 0, st>>>(counter, 64);
+  k_zero_words<<<1, 256, 0, st>>>(words, n);
   PH_LAUNCH_CHECK();
   return PH_OK;
 }
+
+int ensure_zeroed_counter(unsigned* counter, hipStream_t st) { return ensure_zeroed_words(counter, 64, st); }
 
 namespace {
 struct LaneTable {
