@@ -80,6 +80,27 @@ def test_fp32_bit_exact_vs_f32_twin(gpu, variant, time_major, B, T):
 
 
 @pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("with_rho,want_targets", [(True, True), (False, False)])
+def test_fp32_streaming_path_bit_exact(gpu, variant, with_rho, want_targets):
+    """Large time-major fp32 batches take the two-segments-per-lane, nontemporal kernel; it is still
+    bit-identical to the f32 twin (with ratios, and as plain GAE without targets)."""
+    B, T = 131072, 16
+    rew, val, done, logr, boot = _bench_inputs(B, T, seed=0x4400)
+    ratio = np.exp(logr.astype(np.float32)) if with_rho else np.ones(B * T, np.float32)
+    a32, t32 = O.vtrace(rew, val, done, ratio, boot, B, T, variant=variant, time_major=True,
+                        dtype=np.float32)
+    c = lambda x: _cuda(x, torch.float32).reshape(T, B)
+    adv, tgt = D.vtrace(c(rew), c(val), c(done), c(ratio) if with_rho else None,
+                        _cuda(boot, torch.float32), variant=variant, time_major=True,
+                        want_targets=want_targets)
+    assert np.array_equal(adv.cpu().numpy().ravel(), a32)
+    if want_targets:
+        assert np.array_equal(tgt.cpu().numpy().ravel(), t32)
+    else:
+        assert tgt is None
+
+
+@pytest.mark.parametrize("variant", [0, 1])
 def test_log_ratio_input_within_tolerance(gpu, variant):
     B, T = 4096, 64
     rew, val, done, logr, boot = _bench_inputs(B, T, seed=0x4100)
