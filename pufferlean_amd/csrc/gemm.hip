@@ -690,6 +690,180 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// NT bf16 GEMM (C = A B^T, both operands k-contiguous) with the operand tiles copied global -> LDS
+// by the load-to-LDS path (global_load_lds_dwordx4): three LDS stages, two in flight while the third
+// is multiplied, and no prefetch registers, so the deeper pipeline costs no occupancy.
+//
+// A DMA instruction writes 64 consecutive 16-byte LDS slots, lane l into slot l. Thread tid's slot
+// in round i is p = i*256 + tid; it loads the source chunk (row, kc) that the swizzled BK = 32 layout
+// places at slot p (the inverse of LdsLayout<32>::off), so the MFMA reads are the same as the
+// register-staged kernel's. Rows past M and k past the end read the zero page.
+//
+// Ordering is explicit: each wave waits until only the next stage's copies are outstanding
+// (vmcnt), then a barrier makes every wave's copies of this stage visible and guarantees that all
+// waves are done reading the buffer the next copy overwrites. The barrier and waits are asm with a
+// memory clobber: the compiler's own LDS fences would wait for every copy in flight.
+// Wait until at most N of this wave's vector-memory operations are outstanding, and for all its LDS
+// reads (so no read of a buffer is still in flight when the barrier lets a copy overwrite it).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
+// One 16-byte global -> LDS copy per lane into the wave's 1 KB window at lds (lane l -> +16 l). Issued
+// as asm, like the waits: the compiler's own waits for the builtin form are vmcnt(0) before every LDS
+// read, which would drain the copies in flight. M0 carries the window address; nothing else in the
+// kernel uses M0 (the compiler needs it only for the builtin form).
+__device__ __forceinline__ void copy_to_lds(gptr<uint16_t> src, const uint16_t* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(la) : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+template <int BM, int BN, typename TC>
+__global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
+  constexpr int BK = 32, NT = 256, NSTG = 3;
+  using Lay = LdsLayout<BK>;
+  static_assert(Lay::kSwz && Lay::kPitch == BK, "DMA slots follow the unpadded swizzled layout");
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int SM = WM / 32, SN = WN / 32;
+  constexpr int IA = BM * BK / 8 / NT, IB = BN * BK / 8 / NT;  // DMA rounds per stage
+  static_assert(IA * NT * 8 == BM * BK && IB * NT * 8 == BN * BK, "tile/threads");
+  constexpr int A_EL = BM * BK, B_EL = BN * BK;  // elements per stage
+  constexpr int STAGE_EL = A_EL + B_EL;
+  constexpr int LDC = BN + 4;
+  constexpr int PIPE_BYTES = NSTG * STAGE_EL * 2;
+  constexpr int EPR = epilogue_rows(BM, LDC * 4, PIPE_BYTES);
+  static_assert(EPR >= 32 && BM % EPR == 0, "epilogue staging rows");
+  constexpr int C_BYTES = EPR * LDC * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
+  uint16_t* const stages = reinterpret_cast<uint16_t*>(smem);  // stage s: A at s*STAGE_EL, B after
+  float* sC = reinterpret_cast<float*>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / 2) * WM, wn0 = (wave % 2) * WN;
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  int bm, bn;
+  tile_coords(tm, tn, g.remap, bm, bn);
+  const int m0 = bm * BM, n0 = bn * BN;
+  const int kbeg = blockIdx.z * g.kps;
+  const int kend = min(g.K, kbeg + g.kps);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  const gptr<uint16_t> A = (gptr<uint16_t>)g.A;
+  const gptr<uint16_t> B = (gptr<uint16_t>)g.B;
+
+  // this thread's source chunk in each DMA round
+  auto slot_chunk = [](int p, int& row, int& kc) {
+    const int pr = p >> 2;
+    row = pr ^ ((pr >> 3) & 3);
+    kc = (p & 3) ^ ((row >> 2) & 3);
+  };
+  long offA[IA], offB[IB];
+  int kcA[IA], kcB[IB];
+  uint32_t rowA = 0u, rowB = 0u;
+#pragma unroll
+  for (int i = 0; i < IA; i++) {
+    int r, kc;
+    slot_chunk(i * NT + tid, r, kc);
+    offA[i] = (long)(m0 + r) * g.lda + kc * 8;
+    kcA[i] = kc * 8;
+    rowA |= (m0 + r < g.M ? 1u : 0u) << i;
+  }
+#pragma unroll
+  for (int i = 0; i < IB; i++) {
+    int r, kc;
+    slot_chunk(i * NT + tid, r, kc);
+    offB[i] = (long)(n0 + r) * g.ldb + kc * 8;
+    kcB[i] = kc * 8;
+    rowB |= (n0 + r < g.N ? 1u : 0u) << i;
+  }
+  // copy the k-tile at k0 into stage st (a k-tile past the end copies zeros)
+  auto issue = [&](int st, int k0) {
+    uint16_t* base = stages + st * STAGE_EL;
+#pragma unroll
+    for (int i = 0; i < IA; i++) {
+      const bool ok = ((rowA >> i) & 1u) && k0 + kcA[i] < kend;
+      copy_to_lds(ok ? A + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < IB; i++) {
+      const bool ok = ((rowB >> i) & 1u) && k0 + kcB[i] < kend;
+      copy_to_lds(ok ? B + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * NT + wave * 64) * 8);
+    }
+  };
+
+  floatx16 acc[SM][SN];
+#pragma unroll
+  for (int i = 0; i < SM; i++)
+#pragma unroll
+    for (int j = 0; j < SN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  const int lr = lane & 31, lk = (lane >> 5) * 16;
+  auto mfma = [&](floatx16& c, const uint4& a, const uint4& b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  };
+  auto compute = [&](int st) {
+    const uint16_t* sa = stages + st * STAGE_EL;
+    const uint16_t* sb = sa + A_EL;
+    uint4 a0[SM], a1[SM], b0[SN], b1[SN];
+#pragma unroll
+    for (int i = 0; i < SM; i++) {
+      const int row = wm0 + i * 32 + lr;
+      a0[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(row, lk)]);
+      a1[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(row, lk + 8)]);
+    }
+#pragma unroll
+    for (int j = 0; j < SN; j++) {
+      const int row = wn0 + j * 32 + lr;
+      b0[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(row, lk)]);
+      b1[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(row, lk + 8)]);
+    }
+#pragma unroll
+    for (int i = 0; i < SM; i++)
+#pragma unroll
+      for (int j = 0; j < SN; j++) mfma(acc[i][j], a0[i], b0[j]);
+#pragma unroll
+    for (int i = 0; i < SM; i++)
+#pragma unroll
+      for (int j = 0; j < SN; j++) mfma(acc[i][j], a1[i], b1[j]);
+  };
+
+  if (nk > 0) {
+    issue(0, kbeg);
+    issue(1, kbeg + BK);
+    int st = 0;
+#pragma unroll 1
+    for (int kt = 0; kt < nk; kt++) {
+      wait_vm<IA + IB>();  // this wave's copies of stage kt have landed (kt + 1's may be in flight)
+      barrier_mem();       // ... and every wave's; all waves are done with stage kt - 1
+      issue(st == 0 ? 2 : st - 1, kbeg + (kt + 2) * BK);
+      compute(st);
+      st = st == 2 ? 0 : st + 1;
+    }
+    wait_vm<0>();  // the two copies issued past the end land before the LDS is reused
+  }
+  barrier_mem();
+  if constexpr (EPR == BM) {
+    stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
+    lds_barrier();
+    flush_tile<TC, BM, BN, NT, LDC>(g, sC, m0, n0);
+  } else {
+#pragma unroll 1
+    for (int p = 0; p < BM / EPR; p++) {
+      if (p > 0) lds_barrier();
+      stage_acc_rows<SM, SN, LDC>(sC, acc, wm0 - p * EPR, wn0, lane, EPR);
+      lds_barrier();
+      flush_tile<TC, EPR, BN, NT, LDC>(g, sC, m0 + p * EPR, n0);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // fp32-math kernel (fp32 inputs only).
 template <int BM, int BN, int BK, bool TA, bool TB, typename TC>
 __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
@@ -868,9 +1042,18 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
 // Larger tiles for bf16 operands: 256x128 (four 128x64 wavefronts) for big outputs, 256x256 (four
 // 128x128 wavefronts, one block per CU) for split-K over long reductions. Per MFMA they move 3/4
 // and 1/2 of the 128x128 tile's LDS bytes.
+// The NT form at 256x128 (both operands k-contiguous: the layer forward and the dgrad against the
+// transposed weight copy) copies its tiles through the load-to-LDS path instead (bit-identical, about
+// 5 % faster on the policy shapes).
 void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStream_t st) {
-  if (bn == 256) dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
-  else dispatch_bf16_t<256, 128, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  if (bn == 256) {
+    dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  } else if (!ta && tb) {
+    if (g.c_bf16) k_gemm_nt_dma<256, 128, uint16_t><<<grid, 256, 0, st>>>(g);
+    else k_gemm_nt_dma<256, 128, float><<<grid, 256, 0, st>>>(g);
+  } else {
+    dispatch_bf16_t<256, 128, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  }
 }
 
 // fp32 operands are kept raw (8 floats per chunk) in the two prefetch register sets, so they use
