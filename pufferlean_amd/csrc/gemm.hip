@@ -761,23 +761,26 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
     row = pr ^ ((pr >> 3) & 3);
     kc = (p & 3) ^ ((row >> 2) & 3);
   };
-  long offA[IA], offB[IB];
-  int kcA[IA], kcB[IB];
-  uint32_t rowA = 0u, rowB = 0u;
+  // Per round: the chunk's offset from the tile's first row (32-bit: 256 rows of a row-major operand),
+  // its k offset (2 bits, x8) and whether its row is inside the matrix (1 bit); kept compact so the
+  // accumulators and fragments fit two wavefronts per SIMD without spilling.
+  const gptr<uint16_t> Ablk = A + (long)m0 * g.lda, Bblk = B + (long)n0 * g.ldb;
+  int offA[IA], offB[IB];
+  uint32_t kcA = 0u, kcB = 0u, rowA = 0u, rowB = 0u;
 #pragma unroll
   for (int i = 0; i < IA; i++) {
     int r, kc;
     slot_chunk(i * NT + tid, r, kc);
-    offA[i] = (long)(m0 + r) * g.lda + kc * 8;
-    kcA[i] = kc * 8;
+    offA[i] = r * (int)g.lda + kc * 8;
+    kcA |= (uint32_t)kc << (2 * i);
     rowA |= (m0 + r < g.M ? 1u : 0u) << i;
   }
 #pragma unroll
   for (int i = 0; i < IB; i++) {
     int r, kc;
     slot_chunk(i * NT + tid, r, kc);
-    offB[i] = (long)(n0 + r) * g.ldb + kc * 8;
-    kcB[i] = kc * 8;
+    offB[i] = r * (int)g.ldb + kc * 8;
+    kcB |= (uint32_t)kc << (2 * i);
     rowB |= (n0 + r < g.N ? 1u : 0u) << i;
   }
   // copy the k-tile at k0 into stage st (a k-tile past the end copies zeros)
@@ -785,13 +788,13 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
     uint16_t* base = stages + st * STAGE_EL;
 #pragma unroll
     for (int i = 0; i < IA; i++) {
-      const bool ok = ((rowA >> i) & 1u) && k0 + kcA[i] < kend;
-      copy_to_lds(ok ? A + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
+      const bool ok = ((rowA >> i) & 1u) && k0 + (int)((kcA >> (2 * i)) & 3u) * 8 < kend;
+      copy_to_lds(ok ? Ablk + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < IB; i++) {
-      const bool ok = ((rowB >> i) & 1u) && k0 + kcB[i] < kend;
-      copy_to_lds(ok ? B + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * NT + wave * 64) * 8);
+      const bool ok = ((rowB >> i) & 1u) && k0 + (int)((kcB >> (2 * i)) & 3u) * 8 < kend;
+      copy_to_lds(ok ? Bblk + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * NT + wave * 64) * 8);
     }
   };
 
