@@ -23,7 +23,9 @@ __device__ inline float vloss_grad(float vnew, float ret, float vold, bool has_o
   return 0.f;
 }
 
-template <int AMAX>
+// VEC: logit and gradient rows are 16-byte aligned with a pitch that covers A rounded up to 4, so each
+// row moves as float4s (a quarter of the memory instructions of the scalar form; same arithmetic).
+template <int AMAX, bool VEC>
 __global__ void __launch_bounds__(256) k_ppo_grad(
     const float* __restrict__ logits, int ldl, const float* __restrict__ values, int ldv,
     const int* __restrict__ act, const float* __restrict__ adv, const float* __restrict__ ret,
@@ -38,8 +40,19 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
     // All AMAX loads are issued unconditionally (columns past A re-read column A-1, in bounds) so
     // they are in flight together; the values past A are masked where they are used.
     float x[AMAX];
+    if constexpr (VEC && AMAX % 4 == 0) {
 #pragma unroll
-    for (int k = 0; k < AMAX; k++) x[k] = lg[k < A ? k : A - 1];
+      for (int k4 = 0; k4 < AMAX; k4 += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(lg + (k4 < A ? k4 : 0));
+        x[k4] = v.x;
+        x[k4 + 1] = v.y;
+        x[k4 + 2] = v.z;
+        x[k4 + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < AMAX; k++) x[k] = lg[k < A ? k : A - 1];
+    }
     float lse;
     if (max_shift) {
       float mx = x[0];
@@ -76,9 +89,23 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
     if (s1 <= s2) dpol = av * ratio;
     else dpol = av * ((lo < ratio && ratio < hi) ? 1.f : 0.f) * ratio;
     float* dl = dlogits + (size_t)n * ldd;
+    auto dlk = [&](int k) { return dpol * ((k == a ? 1.f : 0.f) - pk[k]) + entCoef * pk[k] * (pout - x[k]); };
+    if constexpr (VEC && AMAX % 4 == 0) {
 #pragma unroll
-    for (int k = 0; k < AMAX; k++)
-      if (k < A) dl[k] = dpol * ((k == a ? 1.f : 0.f) - pk[k]) + entCoef * pk[k] * (pout - x[k]);
+      for (int k4 = 0; k4 < AMAX; k4 += 4) {
+        if (k4 + 4 <= A) {
+          *reinterpret_cast<float4*>(dl + k4) = make_float4(dlk(k4), dlk(k4 + 1), dlk(k4 + 2), dlk(k4 + 3));
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            if (k4 + q < A) dl[k4 + q] = dlk(k4 + q);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < AMAX; k++)
+        if (k < A) dl[k] = dlk(k);
+    }
     const float vnew = values[(size_t)n * ldv];
     const float vold = ov ? ov[n] : 0.f;
     dvalues[(size_t)n * lddv] = -vfCoef * vloss_grad(vnew, rv, vold, ov != nullptr, vfClip);
@@ -182,11 +209,23 @@ int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, c
     if (!part || !counter) return PH_ERR_NOMEM;
     PH_TRY(ensure_zeroed_counter(counter, st));
   }
-#define PH_PPO(AM)                                                                              \
-  k_ppo_grad<AM><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv, ret, old, ov, \
-                                       (int)N, (int)A, vfCoef, entCoef, clipEps, vfClip, max_shift, \
-                                       dlogits, (int)ldd, dvalues, (int)lddv, newlp, newval, part,  \
-                                       counter, losses)
+  const size_t A4 = (A + 3) / 4 * 4;
+  const bool vec = ldl % 4 == 0 && ldl >= A4 && ((uintptr_t)logits & 15) == 0 && ldd % 4 == 0 &&
+                   ((uintptr_t)dlogits & 15) == 0;
+#define PH_PPO(AM)                                                                                  \
+  do {                                                                                              \
+    if (vec)                                                                                        \
+      k_ppo_grad<AM, true><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv, ret, \
+                                                 old, ov, (int)N, (int)A, vfCoef, entCoef, clipEps, \
+                                                 vfClip, max_shift, dlogits, (int)ldd, dvalues,     \
+                                                 (int)lddv, newlp, newval, part, counter, losses);  \
+    else                                                                                            \
+      k_ppo_grad<AM, false><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv,    \
+                                                  ret, old, ov, (int)N, (int)A, vfCoef, entCoef,   \
+                                                  clipEps, vfClip, max_shift, dlogits, (int)ldd,   \
+                                                  dvalues, (int)lddv, newlp, newval, part, counter, \
+                                                  losses);                                          \
+  } while (0)
   if (A <= 2) PH_PPO(2);
   else if (A <= 4) PH_PPO(4);
   else if (A <= 8) PH_PPO(8);

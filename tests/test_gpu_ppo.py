@@ -73,6 +73,26 @@ def test_ppo_grad_strided_combined_head(gpu):
     assert rel(d[:, A], rdv) < 1e-5
 
 
+def test_ppo_grad_padded_rows_partial_chunk(gpu):
+    """Head rows padded to 16 columns (A = 10 logits, value in column 10), the layout of the
+    MinGRU head: the rows move as float4s, the last chunk of each row partially; padding columns of
+    the gradient rows are left untouched."""
+    N, A, W = 4096, 10, 16
+    out = rng.normal(410, N * W).reshape(N, W).astype(np.float32)
+    _, _, act, adv, ret, old, _ = _rows(N, A, 411)
+    g = torch.from_numpy(out).cuda()
+    dout = torch.full_like(g, 7.0)
+    c = lambda x: torch.from_numpy(x).cuda()
+    D.ppo_grad(g[:, :A], g[:, A], c(act), c(adv), c(ret), c(old), max_shift=True,
+               dlogits=dout[:, :A], dvalues=dout[:, A])
+    rdl, rdv, _, _ = O.ppo_grad(out[:, :A].copy(), out[:, A].copy(), act, adv, ret, old,
+                                max_shift=True)
+    d = dout.cpu().numpy()
+    assert rel(d[:, :A], rdl) < 1e-5
+    assert rel(d[:, A], rdv) < 1e-5
+    assert np.all(d[:, A + 1:] == 7.0)
+
+
 @pytest.mark.parametrize("n", [1, 257, 4096, 262144, 1000003])
 def test_adv_normalize(gpu, n):
     x = rng.randf(0xAD7 + n, n, -3.0, 3.0)
