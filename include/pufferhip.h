@@ -143,6 +143,57 @@ int ph_stepvec(float* b, const float* g, float* m, size_t n, float gscale, float
 int ph_gclip(float* g, size_t n, float sc, float maxNorm, void* stream);
 
 /* ---------------------------------------------------------------------------------------------- */
+/* Prioritised replay: the step between V-trace and the MinGRU BPTT in the reference's trainer
+ * (MinGRUTrain.lean:814-834). The rollout columns of N segments x T steps, as the library reads them:
+ *   dtype       PH_F64 (the reference's resident columns) or PH_F32, for every column below
+ *   time_major  element (e,t) at t*N+e, else e*T+t (the reference's segment-major rows)
+ *   K           action components per row (act row holds K values; 0 means 1)
+ *   adv         advantages (the V-trace output); value, ratio: the columns the iterate rewrites;
+ *   act, logp, term: actions, behaviour log-probs, terminal flags.
+ * Unused members may be NULL. */
+typedef struct {
+  int dtype, time_major;
+  size_t N, T, K;
+  const void* adv;
+  void* value;
+  void* ratio;
+  const void* act;
+  const void* logp;
+  const void* term;
+} ph_replay_cols;
+/* L1[e] = sum_t |adv(e,t)|, t ascending, f64 (k_adv_l1, puffercuda.cu:311-312). Bit-identical to
+ * the reference's per-segment sum. L1: device double[N]. */
+int ph_seg_l1(const ph_replay_cols* c, double* L1, void* stream);
+/* Prioritised draws of Bmb segments with replacement (k_prio_w/sum/scan/draw, puffercuda.cu:400-446;
+ * CPU twin lean_ffi_prio_sample, pufferffi.c:1094-1125): w = exp(alpha*log(L1+1e-12)),
+ * p = (w+1e-6)/(sum w+1e-6), draw i takes the splitmix64 word of rng+(i+1)*GOLD, u = word>>11 / 2^53
+ * * sum p, seg[i] = first e with cum p >= u (N-1 if none), mbprio[i] = exp(-beta*log(N*p[seg]+1e-12)).
+ * The caller advances rng by Bmb*GOLD afterwards. One workgroup launch. Sums use a fixed tree
+ * order: reproducible, equal to the sequential CPU twin to rounding (a draw within rounding of a
+ * cumulative boundary may take the neighbouring segment, as the reference's device sampler may).
+ * L1 device double[N]; seg device int[Bmb]; mbprio device double[Bmb]. */
+int ph_prio_sample(const double* L1, size_t N, size_t Bmb, double alpha, double beta, uint64_t rng,
+                   int* seg, double* mbprio, void* stream);
+/* Minibatch gather of the Bmb sampled segments (k_mg_advpart/k_mg_ms_fin/k_mg_gather_scal,
+ * puffercuda.cu:472-502; CPU twin lean_ffi_gather_seq_minibatch, pufferffi.c:1126-1200). out (device,
+ * the columns' dtype) is the packed [(K+5)*T*Bmb] = [act (K wide) | adv | ret | old | term | ov],
+ * timestep-major (row t*Bmb+bi reads segment seg[bi] at step t): act truncated to an integer,
+ * adv = mbprio[bi]*(a-mean)/(std+1e-8) with mean and population std of the gathered raw adv,
+ * ret = a + value, old = logp, term = term > 0.5, ov = value. mbprio NULL: weight 1. stats (device
+ * double[2], may be NULL) receives [mean, std]. A seg entry outside [0,N) gives NaN for its rows.
+ * Every column but adv is bit-identical to the CPU twin; mean and std are merged per block in a fixed
+ * order (equal to the twin's sequential sums to rounding). */
+int ph_mb_gather(const ph_replay_cols* c, const int* seg, const double* mbprio, size_t Bmb, void* out,
+                 double* stats, void* stream);
+/* Value/ratio iterate from the BPTT outputs (k_mg_lastw/k_mg_iterate, puffercuda.cu:503-511): for every
+ * segment drawn, the last draw bi that took it (the writer of an in-order loop over bi) stores
+ * ratio(e,t) = exp(newlp[t*Bmb+bi] - logp(e,t)) and value(e,t) = newval[t*Bmb+bi] for all t. newlp and
+ * newval are device float[T*Bmb]. seg entries outside [0,N) are ignored. Calls on one device share a
+ * last-writer table: calls that overlap in time on different streams race. */
+int ph_mb_iterate(const ph_replay_cols* c, const int* seg, size_t Bmb, const float* newlp,
+                  const float* newval, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
 /* MinGRU policy PPO+Muon minibatch step (the reference's MinGRU trainer chain: cudaMgVtracePrioFFI ->
  * cudaMinGRUPpoGradFFI -> cudaMinGRUMuonResidentFFI, Puffer/RL/MinGRUTrain.lean:814-849;
  * lean_cuda_mingru_ppo_grad puffercuda.cu:5206, lean_cuda_mingru_muon_resident puffercuda.cu:5727).
@@ -276,14 +327,53 @@ int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, si
 double ph_ffi_bench_bf16_resident(size_t N, size_t D, size_t H, size_t reps);
 /* lean_ffi_cuda_available (pufferblas.c:1348-1352). */
 uint8_t ph_ffi_cuda_available(void);
-/* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206), host mode: params (flattenMG, P), obs (nobs >=
- * T*B*D, time-major), scal = [act|adv|ret|old|term|ov] (nscal >= 6*T*B), K = 1, no segment indices
- * (nseg = 0) or priorities (nprio = 0). out: [g (P); new_logp (T*B); new_value (T*B)]. Precision:
- * bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
+/* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, P), obs (nobs >= T*B*D, host,
+ * time-major), K = 1. Two modes, chosen as the reference chooses them:
+ *   device-column mode: (nseg > 0 and nprio > 0: host segIdx[B] as doubles and mbPrio[B]) or (both 0
+ *     and a fresh sampler result of B draws from ph_cuda_mg_vtrace_prio, consumed here), with the
+ *     resident columns of ph_cuda_mg_prep for this T: the 6 scalars are gathered on the device
+ *     (ph_mb_gather) and, after the BPTT, value/ratio of the drawn segments are iterated in place
+ *     (ph_mb_iterate), exactly the reference's order;
+ *   host mode: scal = [act|adv|ret|old|term|ov] (nscal >= 6*T*B).
+ * Either way out receives the reference's host form [g (P); new_logp (T*B); new_value (T*B)] (the
+ * reference also returns this form in device-column mode when its resident gradient buffer is
+ * unavailable). Precision: bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
 int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
                             size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L, size_t A,
                             size_t K, double vfCoef, double entCoef, double clipEps, double vfClip,
-                            size_t nseg, size_t nprio, double* out);
+                            const double* segIdx, size_t nseg, const double* mbPrio, size_t nprio,
+                            double* out);
+/* Prioritised replay, host-buffer forms. The resident columns are library-owned, one set per
+ * process (the reference's g_dc* buffers), bound to the device current at ph_cuda_mg_prep. */
+/* lean_cuda_mg_prep (puffercuda.cu:316-336): upload the rollout columns rew, term, logp, val (N*T
+ * each, segment-major), act (N*T*K) and boot (N); value := val, ratio := 1. K = 0 means 1. */
+int ph_cuda_mg_prep(const double* rew, const double* term, const double* act, const double* logp,
+                    const double* val, const double* boot, size_t N, size_t T, size_t K);
+/* lean_cuda_mg_cols_ready (puffercuda.cu:305-309): *ready = 1 when a rollout stamped the resident
+ * columns for (N, T). This library has no rollout, so it is always 0 and ph_cuda_mg_prep is needed. */
+int ph_cuda_mg_cols_ready(size_t N, size_t T, uint8_t* ready);
+/* lean_cuda_mg_vtrace (puffercuda.cu:386-399): bootstrapped V-trace on the resident columns (ratio,
+ * value) into the resident advantages, and L1out[N] = sum_t |adv| per segment. */
+int ph_cuda_mg_vtrace(size_t N, size_t T, double gamma, double lam, double rhoClip, double cClip,
+                      double* L1out);
+/* lean_cuda_mg_vtrace_prio (puffercuda.cu:447-470): V-trace, L1 and the prioritised sampler of
+ * mbSegs draws, all on the device; the draws stay resident for the next ph_cuda_mingru_ppo_grad.
+ * *used = 1, or 0 when PUFFER_MG_DEVPRIO=0 (the caller then takes the two-call path: ph_cuda_mg_vtrace
+ * + ph_ffi_prio_sample). Fails when ph_cuda_mg_prep was not called for (N, T). Does not synchronise. */
+int ph_cuda_mg_vtrace_prio(size_t N, size_t T, double gamma, double lam, double rhoClip, double cClip,
+                           size_t mbSegs, double prioAlpha, double annealBeta, uint64_t rng,
+                           uint8_t* used);
+/* lean_ffi_prio_sample (pufferffi.c:1094-1125) on the device: advL1[N] in, idx[mbSegs] (segment
+ * indices as doubles) and mbPrio[mbSegs] out. Same formulas and tolerance as ph_prio_sample. */
+int ph_ffi_prio_sample(const double* advL1, size_t N, size_t T, size_t mbSegs, double prioAlpha,
+                       double annealBeta, uint64_t rng, double* idx, double* mbPrio);
+/* lean_ffi_gather_seq_minibatch (pufferffi.c:1126-1200) on the device: the N*T segment-major columns
+ * act, logp, term, advFlat, valueBuf and segIdx/mbPrio[Bmb] in; out[6*T*Bmb] = [act|adv|ret|old|
+ * term|ov] timestep-major. obsCol is not read (the reference ignores it too; may be NULL). */
+int ph_ffi_gather_seq_minibatch(const double* obsCol, const double* actCol, const double* logpCol,
+                                const double* termCol, const double* advFlat, const double* valueBuf,
+                                const double* segIdx, const double* mbPrio, size_t T, size_t Bmb,
+                                size_t D, size_t N, double* out);
 /* lean_cuda_mingru_muon_resident (puffercuda.cu:5727), host-gradient mode: gClip (nG >= P) is the
  * clipped gradient; Muon on every flattenMG matrix of the handle (fp32-MFMA Newton-Schulz on f64
  * state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the biases, in place. wOut: P. */

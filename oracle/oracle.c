@@ -30,6 +30,17 @@
  *   orc_gclip                    closed form
  *   orc_mingru_ppo_grad_seq      finite differences of its own forward objective (orc_mingru_objective)
  *   orc_mingru_heinsen           equals the sequential recurrence within roundoff
+ *   orc_seg_l1                   exact on dyadic inputs (every summation order gives the same bits);
+ *                                numpy row sums of |adv| within roundoff
+ *   orc_prio_sample              draws equal numpy searchsorted (side left, the Python reference's
+ *                                tools/puffer_ref.py:157) and the first-hit linear scan of
+ *                                weightedSampleReplace (VecTrain.lean:147-165) on the pinned splitmix64
+ *                                words; probabilities and weights equal the numpy power forms
+ *                                (tools/puffer_ref.py:151-159) within roundoff; uniform-L1 closed form
+ *                                idx = floor(u*N); empirical draw frequencies match the probabilities
+ *   orc_gather_seq_minibatch     numpy fancy-index construction of the six columns (exact), numpy mean
+ *                                and population std; exact mean/std closed form on dyadic inputs
+ *   orc_mb_iterate               a dictionary of last assignments per segment (exact)
  */
 #include "oracle.h"
 #include <math.h>
@@ -692,6 +703,116 @@ void orc_mingru_heinsen(const double* gate, const double* hid, size_t T, size_t 
       if (x > m) { s = s * exp(m - x) + 1.0; m = x; }
       else s = s + exp(x - m);
       o[t * H + j] = exp(astar + m + log(s));
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Prioritised replay. */
+
+/* k_adv_l1 (puffercuda.cu:311-312): one segment at a time, t ascending. */
+void orc_seg_l1(const double* adv, size_t N, size_t T, double* L1) {
+  for (size_t e = 0; e < N; e++) {
+    const double* a = adv + e * T;
+    double s = 0.0;
+    for (size_t t = 0; t < T; t++) s += fabs(a[t]);
+    L1[e] = s;
+  }
+}
+
+/* lean_ffi_prio_sample (pufferffi.c:1094-1125): weights, sequential normaliser and running sum, then
+ * each draw takes the splitmix64 word of rng + (i+1)*GOLD, scales its top 53 bits by the total, and
+ * takes the first segment whose running sum reaches it (binary search; the running sum is strictly
+ * increasing because every probability is positive). */
+void orc_prio_sample(const double* L1, size_t N, size_t mbSegs, double alpha, double beta, uint64_t rng,
+                     double* idx, double* mbPrio, double* probs, double* cum) {
+  double* w = (double*)malloc(N * sizeof(double));
+  double* p = (double*)malloc(N * sizeof(double));
+  double* c = (double*)malloc(N * sizeof(double));
+  double sumW = 0.0;
+  for (size_t e = 0; e < N; e++) {
+    w[e] = exp(alpha * log(L1[e] + 1e-12));
+    sumW += w[e];
+  }
+  const double denom = sumW + 1e-6;
+  double acc = 0.0;
+  for (size_t e = 0; e < N; e++) {
+    p[e] = (w[e] + 1e-6) / denom;
+    acc += p[e];
+    c[e] = acc;
+  }
+  const double total = acc;
+  for (size_t i = 0; i < mbSegs; i++) {
+    uint64_t s = rng + (uint64_t)i * 0x9E3779B97F4A7C15ULL;
+    const double u = orc_uniform01(orc_rng_next(&s)) * total;
+    size_t lo = 0, hi = N;
+    while (lo < hi) {
+      const size_t mid = (lo + hi) >> 1;
+      if (c[mid] >= u) hi = mid;
+      else lo = mid + 1;
+    }
+    const size_t k = lo < N ? lo : N - 1;
+    idx[i] = (double)k;
+    mbPrio[i] = exp((-beta) * log((double)N * p[k] + 1e-12));
+  }
+  if (probs) memcpy(probs, p, N * sizeof(double));
+  if (cum) memcpy(cum, c, N * sizeof(double));
+  free(w);
+  free(p);
+  free(c);
+}
+
+/* lean_ffi_gather_seq_minibatch (pufferffi.c:1126-1200): mean and population std over the sampled
+ * rows in (bi outer, t inner) order, then the six columns. */
+void orc_gather_seq_minibatch(const double* act, const double* logp, const double* term,
+                              const double* adv, const double* value, const double* segIdx,
+                              const double* mbPrio, size_t T, size_t Bmb, double* out, double* stats2) {
+  const size_t nb = T * Bmb;
+  const double navd = (double)(nb > 0 ? nb : 1);
+  double sum = 0.0;
+  for (size_t bi = 0; bi < Bmb; bi++) {
+    const double* a = adv + (size_t)segIdx[bi] * T;
+    for (size_t t = 0; t < T; t++) sum += a[t];
+  }
+  const double mean = sum / navd;
+  double sq = 0.0;
+  for (size_t bi = 0; bi < Bmb; bi++) {
+    const double* a = adv + (size_t)segIdx[bi] * T;
+    for (size_t t = 0; t < T; t++) {
+      const double d = a[t] - mean;
+      sq += d * d;
+    }
+  }
+  const double sd = sqrt(sq / navd), stde = sd + 1e-8;
+  double *oact = out, *oadv = out + nb, *oret = out + 2 * nb, *oold = out + 3 * nb, *oterm = out + 4 * nb,
+         *oov = out + 5 * nb;
+  for (size_t bi = 0; bi < Bmb; bi++) {
+    const size_t e = (size_t)segIdx[bi];
+    for (size_t t = 0; t < T; t++) {
+      const size_t si = e * T + t, os = t * Bmb + bi;
+      const double a = adv[si], v = value[si];
+      oact[os] = (double)(unsigned long long)act[si];
+      oadv[os] = mbPrio[bi] * (a - mean) / stde;
+      oret[os] = a + v;
+      oold[os] = logp[si];
+      oov[os] = v;
+      oterm[os] = term[si] > 0.5 ? 1.0 : 0.0;
+    }
+  }
+  if (stats2) {
+    stats2[0] = mean;
+    stats2[1] = sd;
+  }
+}
+
+void orc_mb_iterate(double* value, double* ratio, const double* logp, const float* newlp,
+                    const float* newval, const double* seg, size_t Bmb, size_t T) {
+  for (size_t bi = 0; bi < Bmb; bi++) {
+    const size_t e = (size_t)seg[bi];
+    for (size_t t = 0; t < T; t++) {
+      const size_t si = e * T + t, os = t * Bmb + bi;
+      ratio[si] = exp((double)newlp[os] - logp[si]);
+      value[si] = (double)newval[os];
     }
   }
 }

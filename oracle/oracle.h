@@ -123,6 +123,24 @@ void orc_mingru_ppo_grad_seq(const double* params, const double* obsSeq, const d
  * (Puffer/Net/MinGRU.lean:116-168; tools/mingru_ref.py:113-154). */
 void orc_mingru_heinsen(const double* gate, const double* hid, size_t T, size_t H, double* o);
 
+/* ---- prioritised replay (the MinGRU minibatch chain, MinGRUTrain.lean:814-834) ---- */
+/* L1[e] = sum_t |adv[e*T+t]|, t ascending (k_adv_l1, puffercuda.cu:311-312). */
+void orc_seg_l1(const double* adv, size_t N, size_t T, double* L1);
+/* lean_ffi_prio_sample (pufferffi.c:1094-1125): idx[mbSegs] (as doubles) and mbPrio[mbSegs]; probs and
+ * cum (N each, may be NULL) receive the normalised probabilities and their running sum. */
+void orc_prio_sample(const double* L1, size_t N, size_t mbSegs, double alpha, double beta, uint64_t rng,
+                     double* idx, double* mbPrio, double* probs, double* cum);
+/* lean_ffi_gather_seq_minibatch (pufferffi.c:1126-1200): out[6*T*Bmb] = [act|adv|ret|old|term|ov],
+ * timestep-major; stats2 (may be NULL) = [advMean, advStd]. Columns are N*T segment-major. */
+void orc_gather_seq_minibatch(const double* act, const double* logp, const double* term,
+                              const double* adv, const double* value, const double* segIdx,
+                              const double* mbPrio, size_t T, size_t Bmb, double* out, double* stats2);
+/* The value/ratio iterate as an in-order loop over the draws (puffercuda.cu:500-511: the device form
+ * is defined as equal to this loop): for bi = 0..Bmb-1, t = 0..T-1 with e = seg[bi], si = e*T+t,
+ * os = t*Bmb+bi: ratio[si] = exp((double)newlp[os] - logp[si]); value[si] = newval[os]. */
+void orc_mb_iterate(double* value, double* ratio, const double* logp, const float* newlp,
+                    const float* newval, const double* seg, size_t Bmb, size_t T);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,12 @@ class MuonCoefs(C.Structure):
                 ("max_grad_norm", C.c_float), ("gscale", C.c_float), ("nsteps", C.c_int),
                 ("math", C.c_int), ("coeffs", C.c_void_p)]
 
+class ReplayCols(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("time_major", C.c_int), ("N", C.c_size_t), ("T", C.c_size_t),
+                ("K", C.c_size_t), ("adv", C.c_void_p), ("value", C.c_void_p), ("ratio", C.c_void_p),
+                ("act", C.c_void_p), ("logp", C.c_void_p), ("term", C.c_void_p)]
+
+
 # name -> argtypes (all return int status unless listed in _RESTYPES)
 SIGNATURES: dict[str, list] = {
     "ph_last_error": [],
@@ -63,6 +69,10 @@ SIGNATURES: dict[str, list] = {
     "ph_mingru_ppo_grad": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_mingru_muon": [vp, vp, vp, vp, vp, vp],
     "ph_mingru_step": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "ph_seg_l1": [vp, vp, vp],
+    "ph_prio_sample": [vp, sz, sz, dbl, dbl, u64, vp, vp, vp],
+    "ph_mb_gather": [vp, vp, vp, sz, vp, vp, vp],
+    "ph_mb_iterate": [vp, vp, sz, vp, vp, vp],
     # host-buffer layer (reference Lean @[extern] GPU symbols)
     "ph_cuda_vtrace": [dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_vtrace_mingru": [dptr, dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
@@ -86,8 +96,14 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_mlp_forward_batch_bf16": [dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_ffi_bench_bf16_resident": [sz, sz, sz, sz],
     "ph_ffi_cuda_available": [],
-    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, sz,
-                                sz, dptr],
+    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl,
+                                dptr, sz, dptr, sz, dptr],
+    "ph_cuda_mg_prep": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz],
+    "ph_cuda_mg_cols_ready": [sz, sz, C.POINTER(C.c_uint8)],
+    "ph_cuda_mg_vtrace": [sz, sz, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_mg_vtrace_prio": [sz, sz, dbl, dbl, dbl, dbl, sz, dbl, dbl, u64, C.POINTER(C.c_uint8)],
+    "ph_ffi_prio_sample": [dptr, sz, sz, sz, dbl, dbl, u64, dptr, dptr],
+    "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }
 _RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long,

@@ -48,6 +48,9 @@ inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b
 // Growable per-slot device buffers owned by the library (allocated on first use, reused across
 // calls, freed at process exit). Slot ids are private to each translation unit's range.
 void* scratch(int slot, size_t bytes);
+// scratch() whose memory is zero-filled (a fill kernel on st) whenever the slot is newly allocated;
+// the caller keeps it zero between uses.
+void* scratch_zeroed(int slot, size_t bytes, hipStream_t st);
 
 // bf16 <-> f32 with round-to-nearest-even (IEEE bit trick; NaN kept quiet).
 __host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {

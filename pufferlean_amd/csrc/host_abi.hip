@@ -47,6 +47,10 @@ enum : int {
   kHsClip = kSlotHost + 8,
   kHsGrad = kSlotHost + 9,    // uploaded f64 gradient of the resident Muon entries
   kHsMgOut = kSlotHost + 10,  // MinGRU host-mode result staging
+  kHsDc = kSlotHost + 11,     // resident rollout columns of the MinGRU minibatch chain
+  kHsPrio = kSlotHost + 12,   // resident sampler draws (segment indices, importance weights)
+  kHsPrioHost = kSlotHost + 13,
+  kHsGather = kSlotHost + 14,
 };
 
 // Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
@@ -768,36 +772,249 @@ extern "C" int cuda_lstm_ppo_grad_batch(const double*, const double*, const doub
   return 0;
 }
 
+// ---- prioritised replay: resident rollout columns ------------------------------------------------
+namespace {
+// The resident columns of the MinGRU minibatch chain (the reference's g_dc* buffers,
+// puffercuda.cu:286-336), segment-major [N][T] f64, bound to the device current at prep; and the
+// sampler's resident draws (the reference's bg 75/76 with the g_prio_fresh stamp).
+struct DcState {
+  bool valid = false;
+  int dev = -1;
+  long N = 0, T = 0, K = 1;
+  double *rew = nullptr, *term = nullptr, *act = nullptr, *logp = nullptr, *value = nullptr,
+         *ratio = nullptr, *boot = nullptr, *adv = nullptr, *L1 = nullptr;
+  bool prio_fresh = false;
+  long prioB = 0;
+  int* seg = nullptr;
+  double* mp = nullptr;
+};
+DcState g_dc;
+
+__global__ void k_fill_f64(double* __restrict__ x, long n, double v) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = v;
+}
+__global__ void k_i32_f64(const int* __restrict__ x, double* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (double)x[i];
+}
+
+ph_replay_cols dc_cols() {
+  ph_replay_cols c{};
+  c.dtype = PH_F64;
+  c.time_major = 0;
+  c.N = (size_t)g_dc.N; c.T = (size_t)g_dc.T; c.K = (size_t)g_dc.K;
+  c.adv = g_dc.adv; c.value = g_dc.value; c.ratio = g_dc.ratio;
+  c.act = g_dc.act; c.logp = g_dc.logp; c.term = g_dc.term;
+  return c;
+}
+
+int dc_check(size_t N, size_t T, const char* who) {
+  int dev = -1;
+  PH_CHECK_HIP(hipGetDevice(&dev));
+  PH_REQUIRE(g_dc.valid && g_dc.N == (long)N && g_dc.T == (long)T && g_dc.dev == dev,
+             "%s: no resident columns for N=%zu T=%zu on this device (call ph_cuda_mg_prep first)", who, N,
+             T);
+  return PH_OK;
+}
+
+// Segment indices arrive as doubles; every one must name a segment.
+int check_seg_host(const double* seg, size_t B, size_t N, const char* who) {
+  for (size_t i = 0; i < B; i++)
+    PH_REQUIRE(seg[i] >= 0.0 && seg[i] < (double)N && seg[i] == (double)(long)seg[i],
+               "%s: segIdx[%zu] = %g is not a segment index in [0, %zu)", who, i, seg[i], N);
+  return PH_OK;
+}
+}  // namespace
+
+extern "C" int ph_cuda_mg_prep(const double* rew, const double* term, const double* act, const double* logp,
+                               const double* val, const double* boot, size_t N, size_t T, size_t K) {
+  g_dc.valid = false;
+  g_dc.prio_fresh = false;
+  if (K < 1) K = 1;
+  PH_REQUIRE(N > 0 && T > 0 && N <= 0x7fffffffUL && T <= 0x7fffffffUL, "ph_cuda_mg_prep: N=%zu T=%zu", N, T);
+  PH_REQUIRE(rew && term && act && logp && val && boot, "ph_cuda_mg_prep: null buffer");
+  const size_t n = N * T;
+  DcState d;
+  PH_TRY(carve(kHsDc, [&](Carve& c) {
+    d.rew = c.take<double>(n); d.term = c.take<double>(n); d.act = c.take<double>(n * K);
+    d.logp = c.take<double>(n); d.value = c.take<double>(n); d.ratio = c.take<double>(n);
+    d.boot = c.take<double>(N); d.adv = c.take<double>(n); d.L1 = c.take<double>(N);
+  }));
+  PH_TRY(up(d.rew, rew, n * 8)); PH_TRY(up(d.term, term, n * 8)); PH_TRY(up(d.act, act, n * K * 8));
+  PH_TRY(up(d.logp, logp, n * 8)); PH_TRY(up(d.value, val, n * 8)); PH_TRY(up(d.boot, boot, N * 8));
+  k_fill_f64<<<ceil_div(n, kT), kT>>>(d.ratio, (long)n, 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  PH_CHECK_HIP(hipGetDevice(&d.dev));
+  d.N = (long)N; d.T = (long)T; d.K = (long)K;
+  d.valid = true;
+  g_dc = d;
+  return PH_OK;
+}
+
+extern "C" int ph_cuda_mg_cols_ready(size_t N, size_t T, uint8_t* ready) {
+  (void)N;
+  (void)T;
+  PH_REQUIRE(ready, "ph_cuda_mg_cols_ready: null output");
+  *ready = 0;
+  return PH_OK;
+}
+
+namespace {
+int dc_vtrace_l1(double gamma, double lam, double rhoClip, double cClip) {
+  PH_TRY(ph_vtrace(PH_F64, g_dc.rew, g_dc.value, g_dc.term, g_dc.ratio, g_dc.boot, (size_t)g_dc.N,
+                   (size_t)g_dc.T, 1, 0, 0, 1, gamma, lam, rhoClip, cClip, g_dc.adv, nullptr, nullptr));
+  const ph_replay_cols c = dc_cols();
+  return seg_l1(c, g_dc.L1, nullptr);
+}
+}  // namespace
+
+extern "C" int ph_cuda_mg_vtrace(size_t N, size_t T, double gamma, double lam, double rhoClip, double cClip,
+                                 double* L1out) {
+  PH_TRY(dc_check(N, T, "ph_cuda_mg_vtrace"));
+  PH_REQUIRE(L1out, "ph_cuda_mg_vtrace: null output");
+  PH_TRY(dc_vtrace_l1(gamma, lam, rhoClip, cClip));
+  PH_TRY(finish());
+  return down(L1out, g_dc.L1, N * 8);
+}
+
+extern "C" int ph_cuda_mg_vtrace_prio(size_t N, size_t T, double gamma, double lam, double rhoClip,
+                                      double cClip, size_t mbSegs, double prioAlpha, double annealBeta,
+                                      uint64_t rng, uint8_t* used) {
+  PH_REQUIRE(used, "ph_cuda_mg_vtrace_prio: null output");
+  *used = 0;
+  g_dc.prio_fresh = false;
+  if (env_is("PUFFER_MG_DEVPRIO", "0")) return PH_OK;
+  PH_TRY(dc_check(N, T, "ph_cuda_mg_vtrace_prio"));
+  PH_REQUIRE(mbSegs > 0 && mbSegs <= 0x7fffffffUL, "ph_cuda_mg_vtrace_prio: mbSegs=%zu", mbSegs);
+  int* seg;
+  double* mp;
+  PH_TRY(carve(kHsPrio, [&](Carve& c) { seg = c.take<int>(mbSegs); mp = c.take<double>(mbSegs); }));
+  PH_TRY(dc_vtrace_l1(gamma, lam, rhoClip, cClip));
+  PH_TRY(prio_sample(g_dc.L1, N, mbSegs, prioAlpha, annealBeta, rng, seg, mp, nullptr));
+  g_dc.seg = seg;
+  g_dc.mp = mp;
+  g_dc.prioB = (long)mbSegs;
+  g_dc.prio_fresh = true;
+  *used = 1;
+  return PH_OK;
+}
+
+extern "C" int ph_ffi_prio_sample(const double* advL1, size_t N, size_t T, size_t mbSegs, double prioAlpha,
+                                  double annealBeta, uint64_t rng, double* idx, double* mbPrio) {
+  (void)T;
+  PH_REQUIRE(N > 0, "ph_ffi_prio_sample: N=0");
+  if (mbSegs == 0) return PH_OK;
+  PH_REQUIRE(advL1 && idx && mbPrio, "ph_ffi_prio_sample: null buffer");
+  double *dL, *dI, *dM;
+  int* dS;
+  PH_TRY(carve(kHsPrioHost, [&](Carve& c) {
+    dL = c.take<double>(N); dI = c.take<double>(mbSegs); dM = c.take<double>(mbSegs); dS = c.take<int>(mbSegs);
+  }));
+  PH_TRY(up(dL, advL1, N * 8));
+  PH_TRY(prio_sample(dL, N, mbSegs, prioAlpha, annealBeta, rng, dS, dM, nullptr));
+  k_i32_f64<<<ceil_div(mbSegs, kT), kT>>>(dS, dI, (long)mbSegs);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  PH_TRY(down(idx, dI, mbSegs * 8));
+  return down(mbPrio, dM, mbSegs * 8);
+}
+
+extern "C" int ph_ffi_gather_seq_minibatch(const double* obsCol, const double* actCol, const double* logpCol,
+                                           const double* termCol, const double* advFlat, const double* valueBuf,
+                                           const double* segIdx, const double* mbPrio, size_t T, size_t Bmb,
+                                           size_t D, size_t N, double* out) {
+  (void)obsCol;
+  (void)D;
+  if (T * Bmb == 0) return PH_OK;
+  PH_REQUIRE(N > 0 && N <= 0x7fffffffUL && Bmb <= 0x7fffffffUL, "ph_ffi_gather_seq_minibatch: N=%zu Bmb=%zu",
+             N, Bmb);
+  PH_REQUIRE(actCol && logpCol && termCol && advFlat && valueBuf && segIdx && mbPrio && out,
+             "ph_ffi_gather_seq_minibatch: null buffer");
+  PH_TRY(check_seg_host(segIdx, Bmb, N, "ph_ffi_gather_seq_minibatch"));
+  const size_t n = N * T, nb = T * Bmb;
+  double *dAct, *dLogp, *dTerm, *dAdv, *dVal, *dSegD, *dMp, *dOut;
+  int* dSeg;
+  PH_TRY(carve(kHsGather, [&](Carve& c) {
+    dAct = c.take<double>(n); dLogp = c.take<double>(n); dTerm = c.take<double>(n); dAdv = c.take<double>(n);
+    dVal = c.take<double>(n); dSegD = c.take<double>(Bmb); dMp = c.take<double>(Bmb);
+    dOut = c.take<double>(6 * nb); dSeg = c.take<int>(Bmb);
+  }));
+  PH_TRY(up(dAct, actCol, n * 8)); PH_TRY(up(dLogp, logpCol, n * 8)); PH_TRY(up(dTerm, termCol, n * 8));
+  PH_TRY(up(dAdv, advFlat, n * 8)); PH_TRY(up(dVal, valueBuf, n * 8)); PH_TRY(up(dSegD, segIdx, Bmb * 8));
+  PH_TRY(up(dMp, mbPrio, Bmb * 8));
+  k_f64_i32<<<ceil_div(Bmb, kT), kT>>>(dSegD, dSeg, (long)Bmb);
+  PH_LAUNCH_CHECK();
+  ph_replay_cols c{};
+  c.dtype = PH_F64; c.time_major = 0; c.N = N; c.T = T; c.K = 1;
+  c.adv = dAdv; c.value = dVal; c.act = dAct; c.logp = dLogp; c.term = dTerm;
+  PH_TRY(mb_gather(c, dSeg, dMp, Bmb, dOut, nullptr, nullptr));
+  PH_TRY(finish());
+  return down(out, dOut, 6 * nb * 8);
+}
+
 // ---- MinGRU ---------------------------------------------------------------------------------------
-// Host mode of lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, f64), obs [T*B*D]
-// time-major, scal = [act | adv | ret | old | term | ov] (6*T*B, K = 1); writes out[P + 2*T*B] =
-// [summed gradient | new_logp | new_value]. The device-resident modes (empty obs/scal, segment
-// indices, priority weights) and multi-discrete heads (K > 1) are not provided here.
+// lean_cuda_mingru_ppo_grad (puffercuda.cu:5206) with the reference's two scalar sources: host scal,
+// or the device-column mode (puffercuda.cu:5226-5240 mode choice; 5366-5383 gather; 5554-5558
+// iterate). obs is always the host array: the resident obs trajectory belongs to a rollout, which
+// this library does not run. Writes out[P + 2*T*B] = [summed gradient | new_logp | new_value].
 extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
                                        size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L,
                                        size_t A, size_t K, double vfCoef, double entCoef, double clipEps,
-                                       double vfClip, size_t nseg, size_t nprio, double* out) {
+                                       double vfClip, const double* segIdx, size_t nseg, const double* mbPrio,
+                                       size_t nprio, double* out) {
   PH_REQUIRE(K <= 1, "ph_cuda_mingru_ppo_grad: multi-discrete heads (K=%zu) are not supported", K);
-  PH_REQUIRE(nseg == 0 && nprio == 0,
-             "ph_cuda_mingru_ppo_grad: segment-index / priority (device-resident) modes are not supported");
   const size_t TB = T * B;
-  PH_REQUIRE(nobs >= TB * D && nscal >= 6 * TB,
-             "ph_cuda_mingru_ppo_grad: host obs and scal are required (device-resident inputs not supported)");
-  PH_REQUIRE(params && obs && scal && out, "ph_cuda_mingru_ppo_grad: null buffer");
+  int dev = -1;
+  const bool prioRes = nseg == 0 && nprio == 0 && g_dc.prio_fresh && g_dc.prioB == (long)B;
+  g_dc.prio_fresh = false;
+  if (prioRes || (nseg > 0 && nprio > 0)) PH_CHECK_HIP(hipGetDevice(&dev));
+  const bool devCol = (prioRes || (nseg > 0 && nprio > 0)) && g_dc.valid && g_dc.T == (long)T &&
+                      g_dc.K == 1 && g_dc.dev == dev;
+  PH_REQUIRE(devCol || nscal >= 6 * TB,
+             "ph_cuda_mingru_ppo_grad: no scalar source: scal holds %zu of %zu values and the device-column "
+             "mode is off (needs segIdx+mbPrio or a fresh ph_cuda_mg_vtrace_prio draw, and resident columns "
+             "for T=%zu)", nscal, 6 * TB, T);
+  PH_REQUIRE(nobs >= TB * D, "ph_cuda_mingru_ppo_grad: obs holds %zu of %zu values", nobs, TB * D);
+  PH_REQUIRE(params && obs && out && (devCol || scal), "ph_cuda_mingru_ppo_grad: null buffer");
+  if (devCol && !prioRes) {
+    PH_REQUIRE(nseg >= B && nprio >= B && segIdx && mbPrio,
+               "ph_cuda_mingru_ppo_grad: segIdx/mbPrio hold %zu/%zu of %zu draws", nseg, nprio, B);
+    PH_TRY(check_seg_host(segIdx, B, (size_t)g_dc.N, "ph_cuda_mingru_ppo_grad"));
+  }
   ph_mingru_dims d{(int)B, (int)T, (int)D, (int)H, (int)L, (int)A, env_is("PUFFER_MG_PREC", "bf16") ? 0 : 1};
   const long P = mingru_param_count(d);
   ph_ppo_coefs c{};
   c.vf_coef = vfCoef; c.ent_coef = entCoef; c.clip_eps = clipEps; c.vf_clip = vfClip;
-  double *dp, *dx, *ds, *losses;
+  double *dp, *dx, *ds, *losses, *segd, *mpd;
   float *pf, *xf, *sf, *G, *nlp, *nv;
-  int* act;
+  int *act, *segi;
   PH_TRY(carve(kHsMg, [&](Carve& cv) {
     dp = cv.take<double>(P); dx = cv.take<double>(TB * D); ds = cv.take<double>(6 * TB);
     losses = cv.take<double>(8); pf = cv.take<float>(P); xf = cv.take<float>(TB * D);
     sf = cv.take<float>(6 * TB); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
-    act = cv.take<int>(TB);
+    act = cv.take<int>(TB); segd = cv.take<double>(B); mpd = cv.take<double>(B); segi = cv.take<int>(B);
   }));
-  PH_TRY(up(dp, params, P * 8)); PH_TRY(up(dx, obs, TB * D * 8)); PH_TRY(up(ds, scal, 6 * TB * 8));
+  PH_TRY(up(dp, params, P * 8)); PH_TRY(up(dx, obs, TB * D * 8));
+  const int* seg = nullptr;
+  if (devCol) {
+    const double* mp = nullptr;
+    if (prioRes) {
+      seg = g_dc.seg;
+      mp = g_dc.mp;
+    } else {
+      PH_TRY(up(segd, segIdx, B * 8)); PH_TRY(up(mpd, mbPrio, B * 8));
+      k_f64_i32<<<ceil_div(B, kT), kT>>>(segd, segi, (long)B);
+      PH_LAUNCH_CHECK();
+      seg = segi;
+      mp = mpd;
+    }
+    const ph_replay_cols cols = dc_cols();
+    PH_TRY(mb_gather(cols, seg, mp, B, ds, nullptr, nullptr));
+  } else {
+    PH_TRY(up(ds, scal, 6 * TB * 8));
+  }
   PH_TRY(to_f32(dp, pf, P, nullptr));
   PH_TRY(to_f32(dx, xf, (long)(TB * D), nullptr));
   PH_TRY(to_f32(ds, sf, (long)(6 * TB), nullptr));
@@ -805,6 +1022,10 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   PH_LAUNCH_CHECK();
   PH_TRY(ph_mingru_ppo_grad(&d, &c, pf, xf, act, sf + TB, sf + 2 * TB, sf + 3 * TB, sf + 5 * TB, sf + 4 * TB, G,
                             nlp, nv, g_mgLossOn ? losses : nullptr, nullptr));
+  if (devCol) {
+    const ph_replay_cols cols = dc_cols();
+    PH_TRY(mb_iterate(cols, seg, B, nlp, nv, nullptr));
+  }
   double* o = (double*)scratch(kHsMgOut, (P + 2 * TB) * 8);
   if (!o) return PH_ERR_NOMEM;
   k_f32_f64<<<ceil_div(P, kT), kT>>>(G, o, P, 1.0);

@@ -16,6 +16,11 @@ enum : int {
   kSlotNs = 8,        // Newton-Schulz buffers of the stand-alone entry points
   kSlotNsCtl = 9,     // work-item counters of the fused Newton-Schulz launch (256 bytes)
   kSlotMuonU = 10,    // Nesterov updates of a batched Muon step
+  kSlotPrio = 11,     // prioritised sampler: probabilities and (large N) the cumulative table
+  kSlotReplayPart = 12,    // minibatch gather: per-block (count, mean, M2)
+  kSlotReplayCtr = 13,     // minibatch gather: arrival counter (256 bytes)
+  kSlotReplayStats = 14,   // minibatch gather: [mean, std] when the caller passes none
+  kSlotReplayLastw = 15,   // iterate: last-writer table, N ints, zero between calls
   kSlotMuonExact = 16,
   kSlotMuonFastU = 17,
   kSlotGclip = 18,
@@ -120,5 +125,14 @@ int colsum_bf16(const uint16_t* X, long N, int J, long ld, float* out, float sca
 int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st);
 
 long mingru_param_count(const ph_mingru_dims& d);
+
+// Prioritised replay (replay.hip). Column descriptor as in the C ABI.
+int seg_l1(const ph_replay_cols& c, double* L1, hipStream_t st);
+int prio_sample(const double* L1, size_t N, size_t B, double alpha, double beta, uint64_t rng, int* seg,
+                double* mp, hipStream_t st);
+int mb_gather(const ph_replay_cols& c, const int* seg, const double* mp, size_t B, void* out, double* stats,
+              hipStream_t st);
+int mb_iterate(const ph_replay_cols& c, const int* seg, size_t B, const float* newlp, const float* newval,
+               hipStream_t st);
 
 }  // namespace ph

@@ -23,6 +23,8 @@ constexpr int kSlots = 128;
 struct SlotTable {
   void* ptr[kSlots] = {};
   size_t bytes[kSlots] = {};
+  unsigned gen[kSlots] = {};   // allocations made for the slot so far
+  unsigned zgen[kSlots] = {};  // the allocation scratch_zeroed last cleared
 };
 SlotTable g_tables[kMaxDev];
 std::mutex g_mu;
@@ -52,6 +54,7 @@ void* scratch(int slot, size_t bytes) {
   }
   tb.ptr[slot] = p;
   tb.bytes[slot] = rounded;
+  tb.gen[slot]++;
   return p;
 }
 
@@ -74,6 +77,39 @@ int ensure_zeroed_words(unsigned* words, int n, hipStream_t st) {
 }
 
 int ensure_zeroed_counter(unsigned* counter, hipStream_t st) { return ensure_zeroed_words(counter, 64, st); }
+
+namespace {
+__global__ void k_zero_words_grid(unsigned* p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+}  // namespace
+
+void* scratch_zeroed(int slot, size_t bytes, hipStream_t st) {
+  void* p = scratch(slot, bytes);
+  if (!p) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  size_t sz = 0;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    SlotTable& tb = g_tables[dev];
+    if (tb.zgen[slot] != tb.gen[slot]) {
+      tb.zgen[slot] = tb.gen[slot];
+      sz = tb.bytes[slot];
+    }
+  }
+  if (sz) {
+    const long words = (long)(sz / 4);
+    const unsigned g = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+    k_zero_words_grid<<<g, 256, 0, st>>>((unsigned*)p, words);
+    if (hipGetLastError() != hipSuccess) {
+      set_error("scratch_zeroed: fill launch failed (slot %d)", slot);
+      return nullptr;
+    }
+  }
+  return p;
+}
 
 namespace {
 struct LaneTable {

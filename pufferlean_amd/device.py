@@ -246,3 +246,75 @@ def mingru_step(cfg, params, mom, obs, act, oldlp, oldval, rew, done, logrho, bo
            _p(mom), _p(obs), _p(act), _p(oldlp), _p(oldval), _p(rew), _p(done), _p(logrho),
            _p(boot), _p(G), _p(losses), _stream())
     return params, mom, G
+
+
+# ---- prioritised replay ----------------------------------------------------------------------------
+class ReplayColumns:
+    """The rollout columns of N segments x T steps as ph_replay_cols describes them.
+
+    All given tensors share one dtype (float32 or float64) and layout: [T, N] when time_major, else
+    [N, T] (the reference's segment-major rows); act holds K values per row ([T, N, K] / [N, T, K]).
+    """
+
+    def __init__(self, N, T, *, adv=None, value=None, ratio=None, act=None, logp=None, term=None,
+                 time_major=False, K=1):
+        ts = [t for t in (adv, value, ratio, act, logp, term) if t is not None]
+        if not ts:
+            raise ValueError("ReplayColumns needs at least one column")
+        dt = ts[0].dtype
+        if dt not in (torch.float32, torch.float64):
+            raise TypeError("replay columns must be float32 or float64")
+        for t in ts:
+            _dev(t)
+            if t.dtype != dt or not t.is_contiguous():
+                raise TypeError("replay columns must share dtype and be contiguous")
+        for t in (adv, value, ratio, logp, term):
+            if t is not None and t.numel() != N * T:
+                raise ValueError("a replay column must hold N*T values")
+        if act is not None and act.numel() != N * T * K:
+            raise ValueError("act must hold N*T*K values")
+        self.N, self.T, self.K, self.dtype = N, T, K, dt
+        self.tensors = (adv, value, ratio, act, logp, term)
+        self.c = L.ReplayCols(_DT[dt], int(time_major), N, T, K, *(_p(t) for t in self.tensors))
+
+    def ref(self):
+        return C.byref(self.c)
+
+
+def seg_l1(cols, out=None):
+    """sum_t |adv| per segment (float64 [N])."""
+    out = out if out is not None else torch.empty(cols.N, device="cuda", dtype=torch.float64)
+    L.call("ph_seg_l1", cols.ref(), _p(out), _stream())
+    return out
+
+
+def prio_sample(L1, n_draws, *, alpha, beta, rng_state, seg=None, mbprio=None):
+    """Prioritised draws: (seg int32 [n_draws], mbprio float64 [n_draws])."""
+    _dev(L1)
+    if L1.dtype != torch.float64:
+        raise TypeError("prio_sample takes float64 L1")
+    seg = seg if seg is not None else torch.empty(n_draws, device=L1.device, dtype=torch.int32)
+    mbprio = mbprio if mbprio is not None else torch.empty(n_draws, device=L1.device, dtype=torch.float64)
+    L.call("ph_prio_sample", _p(L1), L1.numel(), n_draws, alpha, beta, rng_state & 0xFFFFFFFFFFFFFFFF,
+           _p(seg), _p(mbprio), _stream())
+    return seg, mbprio
+
+
+def mb_gather(cols, seg, mbprio=None, out=None, stats=None):
+    """Packed minibatch columns [(K+5), T, Bmb] = act|adv|ret|old|term|ov (cols' dtype)."""
+    _dev(seg, mbprio)
+    if seg.dtype != torch.int32 or (mbprio is not None and mbprio.dtype != torch.float64):
+        raise TypeError("seg must be int32 and mbprio float64")
+    B = seg.numel()
+    out = out if out is not None else torch.empty((cols.K + 5) * cols.T * B, device=seg.device,
+                                                  dtype=cols.dtype)
+    L.call("ph_mb_gather", cols.ref(), _p(seg), _p(mbprio), B, _p(out), _p(stats), _stream())
+    return out
+
+
+def mb_iterate(cols, seg, newlp, newval):
+    """In place: value/ratio of the drawn segments from the BPTT's new_logp/new_value ([T, Bmb] f32)."""
+    _dev(seg, newlp, newval)
+    if newlp.dtype != torch.float32 or newval.dtype != torch.float32 or seg.dtype != torch.int32:
+        raise TypeError("newlp/newval must be float32 and seg int32")
+    L.call("ph_mb_iterate", cols.ref(), _p(seg), seg.numel(), _p(newlp), _p(newval), _stream())

@@ -45,6 +45,10 @@ _SIG = {
     "orc_mingru_ppo_grad_seq": ([vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d, d, d, d,
                                  vp], None),
     "orc_mingru_heinsen": ([vp, vp, sz, sz, vp], None),
+    "orc_seg_l1": ([vp, sz, sz, vp], None),
+    "orc_prio_sample": ([vp, sz, sz, d, d, C.c_uint64, vp, vp, vp, vp], None),
+    "orc_gather_seq_minibatch": ([vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, vp], None),
+    "orc_mb_iterate": ([vp, vp, vp, vp, vp, vp, sz, sz], None),
 }
 
 _lib = None
@@ -152,3 +156,40 @@ def ppo_losses(logits, values, act, adv, ret, old, ov=None, *, vf=0.5, ent=0.01,
                          P(f64(old)), P(None if ov is None else f64(ov)), N, A, vf, ent, clip,
                          vfclip, P(L))
     return L
+
+
+def seg_l1(adv, N, T):
+    out = np.zeros(N)
+    lib().orc_seg_l1(P(f64(adv)), N, T, P(out))
+    return out
+
+
+def prio_sample(L1, mb, alpha, beta, rng_state):
+    """(idx, mbPrio, probs, cum) of the CPU twin of the prioritised sampler."""
+    L1 = f64(L1)
+    N = L1.size
+    idx, mp = np.zeros(mb), np.zeros(mb)
+    probs, cum = np.zeros(N), np.zeros(N)
+    lib().orc_prio_sample(P(L1), N, mb, alpha, beta, rng_state & 0xFFFFFFFFFFFFFFFF, P(idx), P(mp),
+                          P(probs), P(cum))
+    return idx, mp, probs, cum
+
+
+def gather_seq_minibatch(act, logp, term, adv, value, seg, mp, T):
+    """(out[6*T*Bmb], [mean, std]) of the CPU twin of the minibatch gather."""
+    seg, mp = f64(seg), f64(mp)
+    Bmb = seg.size
+    out = np.zeros(6 * T * Bmb)
+    st = np.zeros(2)
+    lib().orc_gather_seq_minibatch(P(f64(act)), P(f64(logp)), P(f64(term)), P(f64(adv)), P(f64(value)),
+                                   P(seg), P(mp), T, Bmb, P(out), P(st))
+    return out, st
+
+
+def mb_iterate(value, ratio, logp, newlp, newval, seg, T):
+    """In-place value/ratio iterate (copies returned)."""
+    value, ratio = f64(value).copy(), f64(ratio).copy()
+    seg = f64(seg)
+    lib().orc_mb_iterate(P(value), P(ratio), P(f64(logp)), P(f32(newlp)), P(f32(newval)), P(seg),
+                         seg.size, T)
+    return value, ratio

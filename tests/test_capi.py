@@ -64,7 +64,7 @@ def test_host_entries_reject_bad_arguments_without_device():
     import ctypes as C
     lib = L.lib()
     assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, 0.5, 0.01, 0.2, 0.0,
-                                       0, 0, None) == L.PH_ERR_ARG
+                                       None, 0, None, 0, None) == L.PH_ERR_ARG
     assert b"multi-discrete" in lib.ph_last_error()
     assert lib.ph_cuda_policy_download(0, 4, None) == L.PH_ERR_ARG
 

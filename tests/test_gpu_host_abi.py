@@ -377,7 +377,7 @@ def test_mingru_grad_host_mode_matches_oracle(gpu, monkeypatch):
     scal = np.concatenate([a.ravel() for a in (act, adv, ret, old, term, ov)])
     out = np.zeros(Pn + 2 * n)
     L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), 6 * n, B, T, H, D, Ln, A, 1, 0.5, 0.01, 0.2,
-           0.2, 0, 0, dp(out))
+           0.2, None, 0, None, 0, dp(out))
     g = np.zeros(Pn)
     nlp = np.zeros((T, B))
     for b in range(B):
