@@ -14,6 +14,9 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
   gemm    policy GEMMs M=16384, K=N=512 in the three forms (forward X.W^T, dgrad dY.W, wgrad dY^T.X)
   ns      Newton-Schulz batch: 4 x (512x512) + 2 x (512x1024), 5 steps, constant coefficients
   vtrace  V-trace, fp32 time-major, 4096 segments x 64, replicated 64x in one launch (403 MB)
+  replay  prioritised replay between V-trace and the BPTT on 4096 segments x 64 with 4096 draws:
+          segment |adv| sums, sampler, minibatch gather (+ normalisation), value/ratio iterate, in
+          the fp32 time-major layout and in the reference's f64 segment-major layout
 Component times are HIP-event times of a HIP graph holding `steps` launches (device time per launch,
 no host launch path; "us_eager" is the same loop launched from Python). Events are recorded on the
 stream the kernels run on.
@@ -142,14 +145,15 @@ def bench_ppo_step(steps, warmup, eager=False):
     out = {"ms": round(ms, 4), "samples_per_s": round(rows / (ms * 1e-3), 1), "rows": rows,
            "params": cfg.P, "graph": graph is not None, "finite": finite,
            "losses": [round(float(x), 5) for x in losses.cpu().tolist()]}
-    # dominant kernel: the layer-forward GEMM (x_l W_l^T, 262144 x 1536 x 512, bf16 in/out)
+    # dominant kernel: the layer-forward GEMM (x_l W_l^T, 262144 x 1536 x 512, bf16 in/out), timed
+    # as 3 warm-up + 10 launches after the step loop
     x = torch.randn(rows, H5, device="cuda").bfloat16()
     w = (torch.randn(3 * H5, H5, device="cuda") / 22.6).bfloat16()
     y = torch.empty(rows, 3 * H5, device="cuda", dtype=torch.bfloat16)
     gms = time_loop(lambda: D.gemm(x, w, trans_b=True, out=y), 10, 3)
     flops = 2.0 * rows * 3 * H5 * H5
     tf = flops / (gms * 1e-3) / 1e12
-    out["dominant_kernel"] = {"name": "k_gemm_bf16 (layer forward 262144x1536x512)", "us": round(gms * 1e3, 1),
+    out["dominant_kernel"] = {"name": "k_gemm_nt_dma (layer forward 262144x1536x512, bf16)", "us": round(gms * 1e3, 1),
                               "tflops": round(tf, 1), "flops": flops,
                               "hbm_bytes": 2.0 * (rows * H5 + rows * 3 * H5 + 3 * H5 * H5)}
     return out
@@ -267,6 +271,59 @@ def bench_vtrace(steps, warmup):
             "bytes": bytes_, "single_call_us": round(ms1 * 1e3, 2)}
 
 
+def bench_replay(steps, warmup):
+    import numpy as np
+    import torch
+    from pufferlean_amd import device as D
+    from pufferlean_amd import rng
+
+    N, T, Bd = B5, T5, B5
+    n = N * T
+    out = {}
+    for name, dt, tm in (("f32_time_major", torch.float32, True), ("f64_segment_major", torch.float64, False)):
+        esz = 4 if dt == torch.float32 else 8
+        mk = lambda k, f=rng.normal: _t(f(rng.seed_for(6, k), n), np.float64).to(dt)
+        adv, val, logp = mk(0), mk(1), mk(2)
+        act = _t(rng.randint(rng.seed_for(6, 3), n, A5), np.float64).to(dt)
+        term = _t(rng.bernoulli(rng.seed_for(6, 4), n, 0.01), np.float64).to(dt)
+        ratio = torch.ones_like(val)
+        cols = D.ReplayColumns(N, T, adv=adv, value=val, ratio=ratio, act=act, logp=logp, term=term,
+                               time_major=tm)
+        L1 = torch.empty(N, device="cuda", dtype=torch.float64)
+        seg = torch.empty(Bd, device="cuda", dtype=torch.int32)
+        mp = torch.empty(Bd, device="cuda", dtype=torch.float64)
+        mb = torch.empty(6 * Bd * T, device="cuda", dtype=dt)
+        newlp = _t(rng.normal(rng.seed_for(6, 5), Bd * T) - 2.0)
+        newval = _t(rng.normal(rng.seed_for(6, 6), Bd * T))
+        f_l1 = lambda: D.seg_l1(cols, out=L1)
+        f_ps = lambda: D.prio_sample(L1, Bd, alpha=0.8, beta=0.2, rng_state=0x5EED, seg=seg, mbprio=mp)
+        f_ga = lambda: D.mb_gather(cols, seg, mp, out=mb)
+        f_it = lambda: D.mb_iterate(cols, seg, newlp, newval)
+
+        def chain():
+            f_l1(); f_ps(); f_ga(); f_it()
+        f_l1(); f_ps()
+        torch.cuda.synchronize()
+        uniq = int(torch.unique(seg).numel())
+        r = {}
+        for k, fn in (("seg_l1", f_l1), ("prio_sample", f_ps), ("gather", f_ga), ("iterate", f_it),
+                      ("chain", chain)):
+            r[k + "_us"] = round(time_graph(fn, steps, warmup) * 1e3, 2)
+        # algorithmic HBM bytes: gather reads 5 columns through the draws and writes 6, then the
+        # normalisation reads and writes adv; the iterate reads new_logp/new_value of every draw and
+        # logp of each distinct segment, and writes value/ratio of each distinct segment
+        g_bytes = n * (11 * esz + 2 * esz) + Bd * (4 + 8)
+        it_bytes = Bd * T * 8 + uniq * T * 3 * esz + Bd * 4
+        r["gather_gbs"] = round(g_bytes / (r["gather_us"] * 1e-6) / 1e9, 1)
+        r["gather_frac"] = round(r["gather_gbs"] / HBM_PEAK_GBS, 4)
+        r["gather_bytes"] = g_bytes
+        r["iterate_gbs"] = round(it_bytes / (r["iterate_us"] * 1e-6) / 1e9, 1)
+        r["distinct_segments"] = uniq
+        out[name] = r
+    out["shape"] = {"segments": N, "horizon": T, "draws": Bd}
+    return out
+
+
 def traffic_kernels():
     """Launches for the two HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
     the dominant kernel (layer-forward GEMM) 3 times, then a plain 512 MiB device copy 3 times, whose
@@ -366,6 +423,9 @@ def main():
     if args.only in ("all", "vtrace"):
         comps["vtrace"] = bench_vtrace(args.steps, args.warmup)
         print("# vtrace done", file=sys.stderr, flush=True)
+    if args.only in ("all", "replay"):
+        comps["replay"] = bench_replay(args.steps, args.warmup)
+        print("# replay done", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": head["samples_per_s"] if head else None,

@@ -36,7 +36,7 @@ namespace {
 constexpr int kPsThreads = 1024;
 constexpr long kPsLdsCum = 6144;  // cumulative table held in LDS up to this many segments (48 KiB)
 constexpr int kGaThreads = 256;
-constexpr int kGaPer = 8;         // minibatch elements per gather thread
+constexpr int kGaPer = 4;         // minibatch elements per gather thread (256 blocks at 4096 x 64)
 constexpr int kGaBlock = kGaThreads * kGaPer;
 
 // ---- per-segment |adv| sums ------------------------------------------------------------------------
@@ -169,12 +169,17 @@ __global__ void __launch_bounds__(kGaThreads) k_mb_gather(
   R* oterm = oold + n;
   R* oov = oterm + n;
   const R qnan = (R)__builtin_nan("");
+  // Workgroups are dispatched round-robin over the 8 XCDs; XCD x takes the contiguous run of
+  // logical blocks [start_x, start_x + count_x), i.e. a contiguous range of steps t, so its L2 holds
+  // about an eighth of the source rows instead of all of them.
+  const unsigned q8 = gridDim.x / 8, r8 = gridDim.x % 8, x8 = blockIdx.x % 8;
+  const unsigned lb = x8 * q8 + (x8 < r8 ? x8 : r8) + blockIdx.x / 8;
   double av[kGaPer];
   int cnt = 0;
   double s = 0.0;
 #pragma unroll
   for (int k = 0; k < kGaPer; k++) {
-    const long j = (long)blockIdx.x * kGaBlock + (long)k * kGaThreads + tid;
+    const long j = (long)lb * kGaBlock + (long)k * kGaThreads + tid;
     av[k] = 0.0;
     if (j < n) {
       const long t = j / B, bi = j - t * B;
@@ -227,9 +232,9 @@ __global__ void __launch_bounds__(kGaThreads) k_mb_gather(
     __syncthreads();
   }
   if (tid == 0) {
-    part[3 * blockIdx.x] = bn;
-    part[3 * blockIdx.x + 1] = bm;
-    part[3 * blockIdx.x + 2] = sh[2][0];
+    part[3 * lb] = bn;
+    part[3 * lb + 1] = bm;
+    part[3 * lb + 2] = sh[2][0];
     __threadfence();
     const unsigned prev = atomicAdd(counter, 1u);
     last = (prev == gridDim.x - 1);
