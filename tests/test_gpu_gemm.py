@@ -175,3 +175,41 @@ def test_gemm_big_tiles_split_k(gpu, ta, tb):
     assert rel(c, ref) < 1e-5
     c2 = D.gemm(_bf(a), _bf(b), trans_a=bool(ta), trans_b=bool(tb)).cpu().numpy()
     assert np.array_equal(c, c2)
+
+
+def test_gemm_nt_big_tile_epilogue_paths(gpu):
+    """The NT load-to-LDS kernel's epilogue paths at 256x128 tiles: AXPBY accumulating into its own
+    bf16 output (the dgrad pattern), AXPBY without aux, BIAS into bf16 (the encoder pattern), explicit
+    split-K partials, an odd N, and a second output, each against the f64 product."""
+    M, N, K = 4136, 4104, 264
+    a, b = operands(M, N, K, 0, 1, 330)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = ar.astype(np.float64) @ br.T.astype(np.float64)
+    ga, gb = _bf(a), _bf(b)
+    # AXPBY accumulating into its own output (the dgrad pattern), bf16
+    x = rng.normal(331, M * N).reshape(M, N).astype(np.float32)
+    out = _bf(x)
+    xr = out.float().cpu().numpy()
+    D.gemm(ga, gb, trans_b=True, out=out, epilogue=L.PH_EPI_AXPBY, aux=out, alpha=1.0, beta=1.0)
+    assert rel(out.float().cpu().numpy(), ref + xr) < 4e-3
+    # AXPBY without aux: alpha * acc
+    c = D.gemm(ga, gb, trans_b=True, epilogue=L.PH_EPI_AXPBY, alpha=-0.5).cpu().numpy()
+    assert rel(c, -0.5 * ref) < 1e-5
+    # BIAS into bf16 (the encoder pattern)
+    bias = torch.from_numpy(rng.normal(332, N).astype(np.float32)).cuda()
+    cb = D.gemm(ga, gb, trans_b=True, out_dtype=torch.bfloat16, epilogue=L.PH_EPI_BIAS, bias=bias)
+    assert rel(cb.float().cpu().numpy(), ref + bias.cpu().numpy()) < 4e-3
+    # explicit split-K: fp32 partials from registers, deterministic fold
+    c3 = D.gemm(ga, gb, trans_b=True, splits=3).cpu().numpy()
+    assert rel(c3, ref) < 1e-5
+    assert np.array_equal(c3, D.gemm(ga, gb, trans_b=True, splits=3).cpu().numpy())
+    # odd N: LDS-staged path
+    No = N - 7
+    c = D.gemm(ga, gb[:No].contiguous(), trans_b=True).cpu().numpy()
+    assert rel(c, ref[:, :No]) < 1e-5
+    # a second output leaves the first unchanged
+    c_one = D.gemm(ga, gb, trans_b=True).cpu().numpy()
+    c2 = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+    c_two = D.gemm(ga, gb, trans_b=True, out2=c2).cpu().numpy()
+    assert np.array_equal(c_one, c_two)
+    assert rel(c2.float().cpu().numpy(), c_one) < 4e-3
