@@ -228,6 +228,27 @@ int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c, const flo
  * on params/mom (the matrices: wEnc, each W_l, wDec, wVal). */
 int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params, float* mom,
                    float* G, void* stream);
+/* ---------------------------------------------------------------------------------------------- */
+/* Rollout policy forward and categorical sampler: the producers of the behaviour log-prob and value
+ * columns the update consumes. */
+/* Categorical draw per row (k_sample / k_sample_f32, puffercuda.cu:1429-1460; CPU twin
+ * lean_ffi_sample_actions_batch, pufferffi.c:896-918). Y: N rows of logits (dtype PH_F32 or PH_F64,
+ * row stride ldy >= A + has_value), the value at column A when has_value. Row n draws the splitmix64
+ * word of rng + (n+1)*GOLD, u = word>>11 / 2^53; the action is the first k whose running softmax sum
+ * exceeds u (A-1 if none), logp = log(softmax[a]) (max-shifted). act (int32), logp and value (Y's dtype)
+ * are device arrays of N, each may be NULL. The caller advances rng by N*GOLD. f64 rows match the CPU
+ * twin to an ulp of exp/log: a draw within that of a boundary may take the neighbouring action (as
+ * the reference's device sampler may). */
+int ph_sample_actions(int dtype, const void* Y, size_t ldy, size_t N, size_t A, int has_value,
+                      uint64_t rng, int* act, void* logp, void* value, void* stream);
+/* One rollout timestep of the MinGRU policy over N = d->B envs (lean_cuda_mingru_step,
+ * puffercuda.cu:2190-2265): params fp32 flattenMG [P], obs [N][D] fp32, state [N][L][H] fp32 updated
+ * in place, out [N][A+1] fp32 (A logits, then the value). The cell is the reference's
+ * (k_mingru_gate, puffercuda.cu:1949-1959). d->precision 0: bf16 MFMA products (fp32 operands
+ * rounded), 1: fp32 MFMA. A + 1 <= 32; d->T is not used. */
+int ph_mingru_rollout_step(const ph_mingru_dims* d, const float* params, const float* obs, float* state,
+                           float* out, void* stream);
+
 /* The whole minibatch step: V-trace (bootstrapped variant on oldval with boot[B]; logrho may be NULL
  * for ratio 1) -> advantage normalisation -> ph_mingru_ppo_grad -> ph_mingru_muon. G is caller
  * scratch of P floats (holds the clipped gradient afterwards). */
@@ -374,6 +395,18 @@ int ph_ffi_gather_seq_minibatch(const double* obsCol, const double* actCol, cons
                                 const double* termCol, const double* advFlat, const double* valueBuf,
                                 const double* segIdx, const double* mbPrio, size_t T, size_t Bmb,
                                 size_t D, size_t N, double* out);
+/* lean_cuda_sample_actions (puffercuda.cu:1521-1536): Y N*O f64 (A logits, the value at column A),
+ * out[3N] = [act; logp; value]. Same draw as ph_sample_actions on f64 rows. */
+int ph_cuda_sample_actions(const double* Y, size_t N, size_t A, size_t O, uint64_t rng, double* out);
+/* lean_cuda_mingru_step (puffercuda.cu:2190-2265): params (flattenMG, P), obs N*D, state N*L*H
+ * ([n][l][h]); out[N*O + N*L*H] = [logits and value per env (O = A+1); new state]. bf16 selects bf16
+ * MFMA products, else fp32. */
+int ph_cuda_mingru_step(const double* params, const double* obs, const double* state, size_t N, size_t D,
+                        size_t H, size_t L, size_t A, uint8_t bf16, double* out);
+/* lean_cuda_mlp_forward (puffercuda.cu:6038-6060): flattenMLP params, obs N*D; out[N*O] =
+ * relu(obs W1^T + b1) W2^T + b2. bf16 selects bf16 MFMA products, else fp32. */
+int ph_cuda_mlp_forward(const double* params, const double* obs, size_t N, size_t D, size_t H, size_t O,
+                        uint8_t bf16, double* out);
 /* lean_cuda_mingru_muon_resident (puffercuda.cu:5727), host-gradient mode: gClip (nG >= P) is the
  * clipped gradient; Muon on every flattenMG matrix of the handle (fp32-MFMA Newton-Schulz on f64
  * state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the biases, in place. wOut: P. */

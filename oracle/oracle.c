@@ -41,6 +41,10 @@
  *   orc_gather_seq_minibatch     numpy fancy-index construction of the six columns (exact), numpy mean
  *                                and population std; exact mean/std closed form on dyadic inputs
  *   orc_mb_iterate               a dictionary of last assignments per segment (exact)
+ *   orc_sample_actions           numpy softmax + inverse-CDF on the pinned splitmix64 words; uniform-logit
+ *                                closed form a = floor(u*A); draw frequencies against the softmax
+ *   orc_mingru_step              T chained steps from a zero state equal orc_mingru_ppo_grad_seq's
+ *                                new values and new log-probs (a separately pinned function)
  */
 #include "oracle.h"
 #include <math.h>
@@ -815,4 +819,84 @@ void orc_mb_iterate(double* value, double* ratio, const double* logp, const floa
       value[si] = (double)newval[os];
     }
   }
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Rollout policy forward and categorical sampler. */
+
+/* lean_ffi_sample_actions_batch (pufferffi.c:896-918): max-shifted softmax, the first k whose running
+ * probability exceeds u (else the last action), log of the chosen probability, the value column. */
+void orc_sample_actions(const double* Y, size_t N, size_t A, size_t O, uint64_t rng, double* out) {
+  for (size_t n = 0; n < N; n++) {
+    const double* row = Y + n * O;
+    double m = row[0];
+    for (size_t k = 1; k < A; k++)
+      if (row[k] > m) m = row[k];
+    double z = 0.0;
+    for (size_t k = 0; k < A; k++) z += exp(row[k] - m);
+    uint64_t s = rng + (uint64_t)n * 0x9E3779B97F4A7C15ULL;
+    const double u = orc_uniform01(orc_rng_next(&s));
+    double acc = 0.0;
+    size_t a = A - 1;
+    for (size_t k = 0; k < A; k++) {
+      acc += exp(row[k] - m) / z;
+      if (u < acc) {
+        a = k;
+        break;
+      }
+    }
+    out[n] = (double)a;
+    out[N + n] = log(exp(row[a] - m) / z);
+    out[2 * N + n] = row[A];
+  }
+}
+
+/* lean_cuda_mingru_step (puffercuda.cu:2190-2265) in f64: encoder, then per layer the 3H x H product
+ * (hid | gate | proj) and the cell o = (1-z) prev + z gact(hid), h = hg o + (1-hg) h_in; then the
+ * action and value heads. */
+void orc_mingru_step(const double* p, const double* obs, const double* state, size_t N, size_t D,
+                     size_t H, size_t L, size_t A, double* out) {
+  const size_t szE = H * D, szL = 3 * H * H, O = A + 1;
+  const double* wEnc = p; const double* bEnc = p + szE; const double* Wl0 = p + szE + H;
+  const double* wDec = Wl0 + L * szL; const double* bDec = wDec + A * H;
+  const double* wVal = bDec + A; const double* bVal = wVal + H;
+  double* h = (double*)malloc(H * sizeof(double));
+  double* hn = (double*)malloc(H * sizeof(double));
+  double* y = (double*)malloc(3 * H * sizeof(double));
+  double* ns = out + N * O;
+  for (size_t n = 0; n < N; n++) {
+    const double* x = obs + n * D;
+    for (size_t i = 0; i < H; i++) {
+      double acc = 0.0;
+      for (size_t k = 0; k < D; k++) acc += wEnc[i * D + k] * x[k];
+      h[i] = bEnc[i] + acc;
+    }
+    for (size_t l = 0; l < L; l++) {
+      const double* W = Wl0 + l * szL;
+      const double* prev = state + (n * L + l) * H;
+      for (size_t r = 0; r < 3 * H; r++) {
+        double acc = 0.0;
+        for (size_t j = 0; j < H; j++) acc += W[r * H + j] * h[j];
+        y[r] = acc;
+      }
+      for (size_t j = 0; j < H; j++) {
+        const double z = sigm(y[H + j]), gg = gact(y[j]), hg = sigm(y[2 * H + j]);
+        const double o = (1.0 - z) * prev[j] + z * gg;
+        hn[j] = hg * o + (1.0 - hg) * h[j];
+        ns[(n * L + l) * H + j] = o;
+      }
+      memcpy(h, hn, H * sizeof(double));
+    }
+    for (size_t k = 0; k < A; k++) {
+      double acc = 0.0;
+      for (size_t j = 0; j < H; j++) acc += wDec[k * H + j] * h[j];
+      out[n * O + k] = bDec[k] + acc;
+    }
+    double acc = 0.0;
+    for (size_t j = 0; j < H; j++) acc += wVal[j] * h[j];
+    out[n * O + A] = bVal[0] + acc;
+  }
+  free(h);
+  free(hn);
+  free(y);
 }

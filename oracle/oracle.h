@@ -141,6 +141,16 @@ void orc_gather_seq_minibatch(const double* act, const double* logp, const doubl
 void orc_mb_iterate(double* value, double* ratio, const double* logp, const float* newlp,
                     const float* newval, const double* seg, size_t Bmb, size_t T);
 
+/* ---- rollout policy forward and sampler ---- */
+/* lean_ffi_sample_actions_batch (pufferffi.c:896-918): Y is N x O row-major (A logits, then the value
+ * at column A); row n draws the splitmix64 word of rng + (n+1)*GOLD. out = [act(N); logp(N); value(N)]. */
+void orc_sample_actions(const double* Y, size_t N, size_t A, size_t O, uint64_t rng, double* out);
+/* One rollout timestep of the MinGRU policy for N envs (lean_cuda_mingru_step, puffercuda.cu:2190-2265,
+ * the cell of k_mingru_gate 1949-1959): params in flattenMG order, obs N*D, state N*L*H ([n][l][h]).
+ * out = [N*O (A logits, then the value, per env); new state N*L*H]. */
+void orc_mingru_step(const double* p, const double* obs, const double* state, size_t N, size_t D,
+                     size_t H, size_t L, size_t A, double* out);
+
 #ifdef __cplusplus
 }
 #endif

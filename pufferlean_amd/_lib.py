@@ -73,6 +73,8 @@ SIGNATURES: dict[str, list] = {
     "ph_prio_sample": [vp, sz, sz, dbl, dbl, u64, vp, vp, vp],
     "ph_mb_gather": [vp, vp, vp, sz, vp, vp, vp],
     "ph_mb_iterate": [vp, vp, sz, vp, vp, vp],
+    "ph_sample_actions": [i32, vp, sz, sz, sz, i32, u64, vp, vp, vp, vp],
+    "ph_mingru_rollout_step": [vp, vp, vp, vp, vp, vp],
     # host-buffer layer (reference Lean @[extern] GPU symbols)
     "ph_cuda_vtrace": [dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_vtrace_mingru": [dptr, dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
@@ -103,6 +105,9 @@ SIGNATURES: dict[str, list] = {
     "ph_cuda_mg_vtrace": [sz, sz, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_mg_vtrace_prio": [sz, sz, dbl, dbl, dbl, dbl, sz, dbl, dbl, u64, C.POINTER(C.c_uint8)],
     "ph_ffi_prio_sample": [dptr, sz, sz, sz, dbl, dbl, u64, dptr, dptr],
+    "ph_cuda_sample_actions": [dptr, sz, sz, sz, u64, dptr],
+    "ph_cuda_mingru_step": [dptr, dptr, dptr, sz, sz, sz, sz, sz, u8, dptr],
+    "ph_cuda_mlp_forward": [dptr, dptr, sz, sz, sz, sz, u8, dptr],
     "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }

@@ -51,6 +51,8 @@ enum : int {
   kHsPrio = kSlotHost + 12,   // resident sampler draws (segment indices, importance weights)
   kHsPrioHost = kSlotHost + 13,
   kHsGather = kSlotHost + 14,
+  kHsRoll = kSlotHost + 15,   // MinGRU rollout step staging
+  kHsSample = kSlotHost + 16, // sampler staging
 };
 
 // Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
@@ -706,10 +708,10 @@ extern "C" int ph_ffi_dense_forward_bf16(const double* X, const double* W, const
   return down(Y, dY, N * H * 8);
 }
 
-extern "C" int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, size_t D, size_t H,
-                                             size_t O, double* Y) {
-  PH_REQUIRE(N * O == 0 || (p && X && Y), "ph_ffi_mlp_forward_batch_bf16: null buffer");
-  if (N * O == 0) return PH_OK;
+namespace {
+// relu(X W1^T + b1) W2^T + b2 on the MFMA GEMMs, f64 in and out.
+int mlp_forward_host(const double* p, const double* X, size_t N, size_t D, size_t H, size_t O, int math,
+                     double* Y) {
   const size_t P = H * D + H + O * H + O;
   double *dp, *dX, *dY;
   float *pf, *xf, *h1, *of;
@@ -720,16 +722,74 @@ extern "C" int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, s
   PH_TRY(up(dp, p, P * 8)); PH_TRY(up(dX, X, N * D * 8));
   PH_TRY(to_f32(dp, pf, (long)P, nullptr));
   PH_TRY(to_f32(dX, xf, (long)(N * D), nullptr));
-  PhGemmDesc g = f32desc(0, 1, (long)N, (long)H, (long)D, xf, (long)D, pf, (long)D, h1, (long)H, PH_MATH_BF16);
+  PhGemmDesc g = f32desc(0, 1, (long)N, (long)H, (long)D, xf, (long)D, pf, (long)D, h1, (long)H, math);
   g.epi = PH_EPI_BIAS_RELU; g.bias = pf + H * D;
   PH_TRY(gemm(g, nullptr));
-  g = f32desc(0, 1, (long)N, (long)O, (long)H, h1, (long)H, pf + H * D + H, (long)H, of, (long)O, PH_MATH_BF16);
+  g = f32desc(0, 1, (long)N, (long)O, (long)H, h1, (long)H, pf + H * D + H, (long)H, of, (long)O, math);
   g.epi = PH_EPI_BIAS; g.bias = pf + H * D + H + O * H;
   PH_TRY(gemm(g, nullptr));
   k_f32_f64<<<ceil_div(N * O, kT), kT>>>(of, dY, (long)(N * O), 1.0);
   PH_LAUNCH_CHECK();
   PH_TRY(finish());
   return down(Y, dY, N * O * 8);
+}
+}  // namespace
+
+extern "C" int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, size_t D, size_t H,
+                                             size_t O, double* Y) {
+  PH_REQUIRE(N * O == 0 || (p && X && Y), "ph_ffi_mlp_forward_batch_bf16: null buffer");
+  if (N * O == 0) return PH_OK;
+  return mlp_forward_host(p, X, N, D, H, O, PH_MATH_BF16, Y);
+}
+
+// lean_cuda_mlp_forward (puffercuda.cu:6038-6060): the same forward with the reference's gemm32
+// precision switch (bf16 products, or fp32).
+extern "C" int ph_cuda_mlp_forward(const double* params, const double* obs, size_t N, size_t D, size_t H,
+                                   size_t O, uint8_t bf16, double* out) {
+  PH_REQUIRE(N * O == 0 || (params && obs && out), "ph_cuda_mlp_forward: null buffer");
+  if (N * O == 0) return PH_OK;
+  return mlp_forward_host(params, obs, N, D, H, O, bf16 ? PH_MATH_BF16 : PH_MATH_F32, out);
+}
+
+// lean_cuda_sample_actions (puffercuda.cu:1521-1536): f64 logits rows in, [act; logp; value] out.
+extern "C" int ph_cuda_sample_actions(const double* Y, size_t N, size_t A, size_t O, uint64_t rng, double* out) {
+  PH_REQUIRE(A >= 1 && O >= A + 1, "ph_cuda_sample_actions: A=%zu O=%zu (the value column is A)", A, O);
+  PH_REQUIRE(N <= 0x7fffffffUL, "ph_cuda_sample_actions: N=%zu", N);
+  if (N == 0) return PH_OK;
+  PH_REQUIRE(Y && out, "ph_cuda_sample_actions: null buffer");
+  double *dY, *dO;
+  PH_TRY(carve(kHsSample, [&](Carve& c) { dY = c.take<double>(N * O); dO = c.take<double>(3 * N); }));
+  PH_TRY(up(dY, Y, N * O * 8));
+  PH_TRY(sample_actions(PH_F64, dY, O, N, A, 1, rng, nullptr, nullptr, nullptr, dO, nullptr));
+  PH_TRY(finish());
+  return down(out, dO, 3 * N * 8);
+}
+
+// lean_cuda_mingru_step (puffercuda.cu:2190-2265): one rollout timestep over N envs, state in and out
+// as f64 [n][l][h].
+extern "C" int ph_cuda_mingru_step(const double* params, const double* obs, const double* state, size_t N,
+                                   size_t D, size_t H, size_t L, size_t A, uint8_t bf16, double* out) {
+  PH_REQUIRE(N > 0 && D > 0 && H > 0 && L > 0 && A > 0 && A + 1 <= 32 && N <= 0x7fffffffUL,
+             "ph_cuda_mingru_step: N=%zu D=%zu H=%zu L=%zu A=%zu (A + 1 <= 32)", N, D, H, L, A);
+  PH_REQUIRE(params && obs && state && out, "ph_cuda_mingru_step: null buffer");
+  const size_t O = A + 1, P = H * D + H + L * 3 * H * H + A * H + A + H + 1, ns = N * L * H;
+  double *dp, *dx, *ds, *dout;
+  float *pf, *xf, *sf, *of;
+  PH_TRY(carve(kHsRoll, [&](Carve& c) {
+    dp = c.take<double>(P); dx = c.take<double>(N * D); ds = c.take<double>(ns); dout = c.take<double>(N * O + ns);
+    pf = c.take<float>(P); xf = c.take<float>(N * D); sf = c.take<float>(ns); of = c.take<float>(N * O);
+  }));
+  PH_TRY(up(dp, params, P * 8)); PH_TRY(up(dx, obs, N * D * 8)); PH_TRY(up(ds, state, ns * 8));
+  PH_TRY(to_f32(dp, pf, (long)P, nullptr));
+  PH_TRY(to_f32(dx, xf, (long)(N * D), nullptr));
+  PH_TRY(to_f32(ds, sf, (long)ns, nullptr));
+  ph_mingru_dims d{(int)N, 1, (int)D, (int)H, (int)L, (int)A, bf16 ? 0 : 1};
+  PH_TRY(mingru_rollout_step(d, pf, xf, sf, of, nullptr));
+  k_f32_f64<<<ceil_div(N * O, kT), kT>>>(of, dout, (long)(N * O), 1.0);
+  k_f32_f64<<<ceil_div(ns, kT), kT>>>(sf, dout + N * O, (long)ns, 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(out, dout, (N * O + ns) * 8);
 }
 
 // Device-resident bf16 dense-layer throughput in GFLOP/s (2*N*D*H per rep); -1 without a device.

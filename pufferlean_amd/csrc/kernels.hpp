@@ -24,6 +24,7 @@ enum : int {
   kSlotMuonExact = 16,
   kSlotMuonFastU = 17,
   kSlotGclip = 18,
+  kSlotRollout = 19,  // rollout step: layer inputs, layer products, padded head
   kSlotMgBufs = 20,
   kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
   kSlotHost = 48,     // 48..127: host-buffer entry points
@@ -134,5 +135,11 @@ int mb_gather(const ph_replay_cols& c, const int* seg, const double* mp, size_t 
               hipStream_t st);
 int mb_iterate(const ph_replay_cols& c, const int* seg, size_t B, const float* newlp, const float* newval,
                hipStream_t st);
+
+// Rollout forward and sampler (rollout.hip). out3 (may be NULL): [act; logp; value] as f64 [3N].
+int sample_actions(int dtype, const void* Y, size_t ldy, size_t N, size_t A, int has_value, uint64_t rng, int* act,
+                   void* logp, void* val, double* out3, hipStream_t st);
+int mingru_rollout_step(const ph_mingru_dims& d, const float* params, const float* obs, float* state, float* out,
+                        hipStream_t st);
 
 }  // namespace ph

@@ -49,6 +49,8 @@ _SIG = {
     "orc_prio_sample": ([vp, sz, sz, d, d, C.c_uint64, vp, vp, vp, vp], None),
     "orc_gather_seq_minibatch": ([vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, vp], None),
     "orc_mb_iterate": ([vp, vp, vp, vp, vp, vp, sz, sz], None),
+    "orc_sample_actions": ([vp, sz, sz, sz, C.c_uint64, vp], None),
+    "orc_mingru_step": ([vp, vp, vp, sz, sz, sz, sz, sz, vp], None),
 }
 
 _lib = None
@@ -193,3 +195,19 @@ def mb_iterate(value, ratio, logp, newlp, newval, seg, T):
     lib().orc_mb_iterate(P(value), P(ratio), P(f64(logp)), P(f32(newlp)), P(f32(newval)), P(seg),
                          seg.size, T)
     return value, ratio
+
+
+def sample_actions(Y, A, rng_state):
+    """(act, logp, value) of the CPU twin of the categorical sampler; Y is N x O (O >= A + 1)."""
+    Y = f64(Y)
+    N, O = Y.shape
+    out = np.zeros(3 * N)
+    lib().orc_sample_actions(P(Y), N, A, O, rng_state & 0xFFFFFFFFFFFFFFFF, P(out))
+    return out[:N], out[N:2 * N], out[2 * N:]
+
+
+def mingru_step(params, obs, state, N, D, H, L, A):
+    """(out [N, A+1], new_state [N, L, H]) of the f64 single-step MinGRU forward."""
+    out = np.zeros(N * (A + 1) + N * L * H)
+    lib().orc_mingru_step(P(f64(params)), P(f64(obs)), P(f64(state)), N, D, H, L, A, P(out))
+    return out[:N * (A + 1)].reshape(N, A + 1), out[N * (A + 1):].reshape(N, L, H)
