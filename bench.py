@@ -14,6 +14,8 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
   gemm    policy GEMMs M=16384, K=N=512 in the three forms (forward X.W^T, dgrad dY.W, wgrad dY^T.X)
   ns      Newton-Schulz batch: 4 x (512x512) + 2 x (512x1024), 5 steps, constant coefficients
   vtrace  V-trace, fp32 time-major, 4096 segments x 64, replicated 64x in one launch (403 MB)
+  rollout one rollout timestep of the headline policy over 4096 envs (MinGRU step + categorical
+          draw), bf16 and fp32 MFMA products
   replay  prioritised replay between V-trace and the BPTT on 4096 segments x 64 with 4096 draws:
           segment |adv| sums, sampler, minibatch gather (+ normalisation), value/ratio iterate, in
           the fp32 time-major layout and in the reference's f64 segment-major layout
@@ -324,6 +326,34 @@ def bench_replay(steps, warmup):
     return out
 
 
+def bench_rollout(steps, warmup):
+    import numpy as np
+    import torch
+    from pufferlean_amd import device as D
+    from pufferlean_amd import rng
+
+    N = B5
+    params, _ = mingru_inputs(B5, 1, D5, H5, L5, A5)
+    p = _t(params)
+    obs = _t(rng.normal(rng.seed_for(7, 0), N * D5)).view(N, D5)
+    state = torch.zeros(N, L5, H5, device="cuda")
+    out = torch.empty(N, A5 + 1, device="cuda")
+    act = torch.empty(N, device="cuda", dtype=torch.int32)
+    lp = torch.empty(N, device="cuda")
+    val = torch.empty(N, device="cuda")
+    flops = 2.0 * N * (D5 * H5 + L5 * 3 * H5 * H5 + (A5 + 1) * H5)
+    r = {"envs": N, "flops": flops}
+    for name, prec, peak in (("bf16", 0, BF16_PEAK_TFLOPS), ("f32", 1, F32_PEAK_TFLOPS)):
+        def fn():
+            D.mingru_rollout_step(p, obs, state, out, D=D5, H=H5, L_layers=L5, A=A5, precision=prec)
+            D.sample_actions(out, A5, rng_state=0x5EED, act=act, logp=lp, value=val)
+        ms = time_graph(fn, steps, warmup)
+        tf = flops / (ms * 1e-3) / 1e12
+        r[name] = {"us": round(ms * 1e3, 2), "env_steps_per_s": round(N / (ms * 1e-3), 1),
+                   "tflops": round(tf, 1), "frac": round(tf / peak, 4)}
+    return r
+
+
 def traffic_kernels():
     """Launches for the two HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
     the dominant kernel (layer-forward GEMM) 3 times, then a plain 512 MiB device copy 3 times, whose
@@ -423,6 +453,9 @@ def main():
     if args.only in ("all", "vtrace"):
         comps["vtrace"] = bench_vtrace(args.steps, args.warmup)
         print("# vtrace done", file=sys.stderr, flush=True)
+    if args.only in ("all", "rollout"):
+        comps["rollout"] = bench_rollout(args.steps, args.warmup)
+        print("# rollout done", file=sys.stderr, flush=True)
     if args.only in ("all", "replay"):
         comps["replay"] = bench_replay(args.steps, args.warmup)
         print("# replay done", file=sys.stderr, flush=True)

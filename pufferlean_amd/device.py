@@ -318,3 +318,28 @@ def mb_iterate(cols, seg, newlp, newval):
     if newlp.dtype != torch.float32 or newval.dtype != torch.float32 or seg.dtype != torch.int32:
         raise TypeError("newlp/newval must be float32 and seg int32")
     L.call("ph_mb_iterate", cols.ref(), _p(seg), seg.numel(), _p(newlp), _p(newval), _stream())
+
+
+# ---- rollout forward and sampler -------------------------------------------------------------------
+def sample_actions(logits, A, *, rng_state, has_value=True, act=None, logp=None, value=None):
+    """Categorical draw per row of logits [N, >= A (+1)] (float32/float64, row stride honoured):
+    returns (act int32 [N], logp [N], value [N] or None)."""
+    _dev(logits)
+    N = logits.shape[0]
+    act = act if act is not None else torch.empty(N, device=logits.device, dtype=torch.int32)
+    logp = logp if logp is not None else torch.empty(N, device=logits.device, dtype=logits.dtype)
+    if has_value and value is None:
+        value = torch.empty(N, device=logits.device, dtype=logits.dtype)
+    L.call("ph_sample_actions", _DT[logits.dtype], _p(logits), logits.stride(0), N, A, int(has_value),
+           rng_state & 0xFFFFFFFFFFFFFFFF, _p(act), _p(logp), _p(value if has_value else None), _stream())
+    return act, logp, (value if has_value else None)
+
+
+def mingru_rollout_step(params, obs, state, out, *, D, H, L_layers, A, precision=0):
+    """One rollout timestep over N envs: obs [N, D] fp32, state [N, L, H] fp32 (in place),
+    out [N, A+1] fp32 (logits, then the value)."""
+    _dev(params, obs, state, out)
+    N = obs.shape[0]
+    dims = L.MinGRUDims(N, 1, D, H, L_layers, A, precision)
+    L.call("ph_mingru_rollout_step", C.byref(dims), _p(params), _p(obs), _p(state), _p(out), _stream())
+    return out
