@@ -349,7 +349,9 @@ double ph_ffi_bench_bf16_resident(size_t N, size_t D, size_t H, size_t reps);
 /* lean_ffi_cuda_available (pufferblas.c:1348-1352). */
 uint8_t ph_ffi_cuda_available(void);
 /* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, P), obs (nobs >= T*B*D, host,
- * time-major), K = 1. Two modes, chosen as the reference chooses them:
+ * time-major; or nobs = 0 in the device-column mode, which gathers the minibatch from the resident obs
+ * trajectory of ph_cuda_mg_obs_traj by the drawn segments, as the reference gathers its rollout's),
+ * K = 1. Two scalar sources, chosen as the reference chooses them:
  *   device-column mode: (nseg > 0 and nprio > 0: host segIdx[B] as doubles and mbPrio[B]) or (both 0
  *     and a fresh sampler result of B draws from ph_cuda_mg_vtrace_prio, consumed here), with the
  *     resident columns of ph_cuda_mg_prep for this T: the 6 scalars are gathered on the device
@@ -373,6 +375,11 @@ int ph_cuda_mg_prep(const double* rew, const double* term, const double* act, co
 /* lean_cuda_mg_cols_ready (puffercuda.cu:305-309): *ready = 1 when a rollout stamped the resident
  * columns for (N, T). This library has no rollout, so it is always 0 and ph_cuda_mg_prep is needed. */
 int ph_cuda_mg_cols_ready(size_t N, size_t T, uint8_t* ready);
+/* No counterpart in the reference: its rollout entries store the obs trajectory the device-column
+ * gradient reads (g_dMGObsTraj, puffercuda.cu:2136, written at 4116-4403 and 4598-4843) while they step
+ * the env plugins, which this library does not run. A caller whose rollout runs elsewhere stores it
+ * here: obs N*T*D f64, row e*T+t (segment-major), kept as f32 on the current device. */
+int ph_cuda_mg_obs_traj(const double* obs, size_t N, size_t T, size_t D);
 /* lean_cuda_mg_vtrace (puffercuda.cu:386-399): bootstrapped V-trace on the resident columns (ratio,
  * value) into the resident advantages, and L1out[N] = sum_t |adv| per segment. */
 int ph_cuda_mg_vtrace(size_t N, size_t T, double gamma, double lam, double rhoClip, double cClip,

@@ -102,6 +102,7 @@ SIGNATURES: dict[str, list] = {
                                 dptr, sz, dptr, sz, dptr],
     "ph_cuda_mg_prep": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz],
     "ph_cuda_mg_cols_ready": [sz, sz, C.POINTER(C.c_uint8)],
+    "ph_cuda_mg_obs_traj": [dptr, sz, sz, sz],
     "ph_cuda_mg_vtrace": [sz, sz, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_mg_vtrace_prio": [sz, sz, dbl, dbl, dbl, dbl, sz, dbl, dbl, u64, C.POINTER(C.c_uint8)],
     "ph_ffi_prio_sample": [dptr, sz, sz, sz, dbl, dbl, u64, dptr, dptr],

@@ -53,6 +53,7 @@ enum : int {
   kHsGather = kSlotHost + 14,
   kHsRoll = kSlotHost + 15,   // MinGRU rollout step staging
   kHsSample = kSlotHost + 16, // sampler staging
+  kHsObsTraj = kSlotHost + 17,  // resident obs trajectory of the MinGRU chain (f32)
 };
 
 // Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
@@ -850,6 +851,26 @@ struct DcState {
 };
 DcState g_dc;
 
+// The resident obs trajectory [N*T][D] f32, row e*T+t (the reference's g_dMGObsTraj,
+// puffercuda.cu:2136), bound to the device current when it was stored.
+struct ObsTraj {
+  bool valid = false;
+  int dev = -1;
+  long N = 0, T = 0, D = 0;
+  float* obs = nullptr;
+};
+ObsTraj g_traj;
+
+// Minibatch obs, time-major: x[(t*B + bi)*D + j] = traj[(seg[bi]*T + t)*D + j] (k_gather_mg_obs,
+// puffercuda.cu:2146-2150).
+__global__ void k_gather_obs_traj(const float* __restrict__ traj, const int* __restrict__ seg, long B, long T,
+                                  long D, float* __restrict__ x) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * B * D) return;
+  const long j = i % D, r = i / D, t = r / B, bi = r - t * B;
+  x[i] = traj[((long)seg[bi] * T + t) * D + j];
+}
+
 __global__ void k_fill_f64(double* __restrict__ x, long n, double v) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) x[i] = v;
@@ -918,6 +939,23 @@ extern "C" int ph_cuda_mg_cols_ready(size_t N, size_t T, uint8_t* ready) {
   (void)T;
   PH_REQUIRE(ready, "ph_cuda_mg_cols_ready: null output");
   *ready = 0;
+  return PH_OK;
+}
+
+extern "C" int ph_cuda_mg_obs_traj(const double* obs, size_t N, size_t T, size_t D) {
+  g_traj.valid = false;
+  PH_REQUIRE(N > 0 && T > 0 && D > 0 && N <= 0x7fffffffUL, "ph_cuda_mg_obs_traj: N=%zu T=%zu D=%zu", N, T, D);
+  PH_REQUIRE(obs, "ph_cuda_mg_obs_traj: null buffer");
+  const size_t n = N * T * D;
+  double* d64;
+  float* f;
+  PH_TRY(carve(kHsObsTraj, [&](Carve& c) { d64 = c.take<double>(n); f = c.take<float>(n); }));
+  PH_TRY(up(d64, obs, n * 8));
+  PH_TRY(to_f32(d64, f, (long)n, nullptr));
+  PH_TRY(finish());
+  PH_CHECK_HIP(hipGetDevice(&g_traj.dev));
+  g_traj.N = (long)N; g_traj.T = (long)T; g_traj.D = (long)D; g_traj.obs = f;
+  g_traj.valid = true;
   return PH_OK;
 }
 
@@ -1036,8 +1074,15 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
              "ph_cuda_mingru_ppo_grad: no scalar source: scal holds %zu of %zu values and the device-column "
              "mode is off (needs segIdx+mbPrio or a fresh ph_cuda_mg_vtrace_prio draw, and resident columns "
              "for T=%zu)", nscal, 6 * TB, T);
-  PH_REQUIRE(nobs >= TB * D, "ph_cuda_mingru_ppo_grad: obs holds %zu of %zu values", nobs, TB * D);
-  PH_REQUIRE(params && obs && out && (devCol || scal), "ph_cuda_mingru_ppo_grad: null buffer");
+  // empty obs: gather the minibatch from the resident obs trajectory by the drawn segments
+  // (puffercuda.cu:5226-5230, 5362-5363), which needs segment indices and a trajectory of these shapes
+  const bool useTraj = nobs == 0 && devCol && g_traj.valid && g_traj.dev == dev && g_traj.N == g_dc.N &&
+                       g_traj.T == (long)T && g_traj.D == (long)D;
+  PH_REQUIRE(useTraj || nobs >= TB * D,
+             "ph_cuda_mingru_ppo_grad: obs holds %zu of %zu values and no resident obs trajectory matches "
+             "(the device-column mode with a ph_cuda_mg_obs_traj trajectory of N=%ld segments, T=%zu, D=%zu)",
+             nobs, TB * D, g_dc.N, T, D);
+  PH_REQUIRE(params && (useTraj || obs) && out && (devCol || scal), "ph_cuda_mingru_ppo_grad: null buffer");
   if (devCol && !prioRes) {
     PH_REQUIRE(nseg >= B && nprio >= B && segIdx && mbPrio,
                "ph_cuda_mingru_ppo_grad: segIdx/mbPrio hold %zu/%zu of %zu draws", nseg, nprio, B);
@@ -1056,7 +1101,8 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
     sf = cv.take<float>(6 * TB); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
     act = cv.take<int>(TB); segd = cv.take<double>(B); mpd = cv.take<double>(B); segi = cv.take<int>(B);
   }));
-  PH_TRY(up(dp, params, P * 8)); PH_TRY(up(dx, obs, TB * D * 8));
+  PH_TRY(up(dp, params, P * 8));
+  if (!useTraj) PH_TRY(up(dx, obs, TB * D * 8));
   const int* seg = nullptr;
   if (devCol) {
     const double* mp = nullptr;
@@ -1076,7 +1122,12 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
     PH_TRY(up(ds, scal, 6 * TB * 8));
   }
   PH_TRY(to_f32(dp, pf, P, nullptr));
-  PH_TRY(to_f32(dx, xf, (long)(TB * D), nullptr));
+  if (useTraj) {
+    k_gather_obs_traj<<<ceil_div(TB * D, kT), kT>>>(g_traj.obs, seg, (long)B, (long)T, (long)D, xf);
+    PH_LAUNCH_CHECK();
+  } else {
+    PH_TRY(to_f32(dx, xf, (long)(TB * D), nullptr));
+  }
   PH_TRY(to_f32(ds, sf, (long)(6 * TB), nullptr));
   k_f64_i32<<<ceil_div(TB, kT), kT>>>(ds, act, (long)TB);
   PH_LAUNCH_CHECK();
