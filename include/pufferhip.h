@@ -93,6 +93,41 @@ int ph_ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv
                 float* dlogits, size_t ldd, float* dvalues, size_t lddv, float* newlp,
                 float* newval, double* losses, void* stream);
 
+/* Multi-discrete heads (k_ppo_dout_md, puffercuda.cu:702-727): K categorical heads of head_sizes[K]
+ * actions (host array, K <= 32); row n holds the heads' logits back to back, then the value at
+ * column W = sum of sizes (stride ldl >= W + 1). act int32 [N][K]. One clipped surrogate on the joint
+ * ratio exp(sum_h log softmax_h[a_h] - old); each head's logits get dPol (onehot - p) plus the entropy
+ * gradient; dvalue as ph_ppo_grad. Writes dlogits rows (W + 1 columns, stride ldd) and optional
+ * newlp (joint) / newval. Log-sum-exp is max-shifted (the reference's is not; equal to rounding).
+ * A row with an action outside [0, head_sizes[h]) gets NaN logit gradients and NaN newlp (its value
+ * gradient stands); no logit outside the row is read. losses (device doubles, may be NULL): the 7
+ * dashboard losses as ph_ppo_grad, the entropy summed over the heads (ff_surface_losses mode 1,
+ * puffercuda.cu:1798-1870). */
+int ph_ppo_grad_md(const float* logits, size_t ldl, const int* act, const float* adv, const float* ret,
+                   const float* old, const float* ov, size_t N, const int* head_sizes, size_t K,
+                   float vfCoef, float entCoef, float clipEps, float vfClip, float* dlogits, size_t ldd,
+                   float* newlp, float* newval, double* losses, void* stream);
+/* Diagonal Gaussian head (k_ppo_dout_cont, puffercuda.cu:1767-1790; CPU twin pufferffi.c:223-330): row n
+ * holds d means, d raw log-stds (clamped to [ls_lo, ls_hi]; the reference's GPU path uses [-20, 2], its
+ * CPU twin [-5, 2]), the value at 2d. act f32 [N][d]. z = (a - mu) exp(-ls), logp = sum(-z^2/2 - ls -
+ * log(2 pi)/2); dmu = dPol z exp(-ls), dls = dPol (z^2 - 1) + ent inside the clamp range, else 0.
+ * losses (device doubles, may be NULL): the 7 dashboard losses, entropy sum(ls + (1 + log(2 pi))/2)
+ * (ff_surface_losses mode 2, puffercuda.cu:1798-1870). */
+int ph_ppo_grad_cont(const float* out, size_t ldo, const float* act, const float* adv, const float* ret,
+                     const float* old, const float* ov, size_t N, size_t d, float vfCoef, float entCoef,
+                     float clipEps, float vfClip, float ls_lo, float ls_hi, float* dout, size_t ldd,
+                     float* newlp, float* newval, double* losses, void* stream);
+/* Multi-discrete draw (k_sample_md, puffercuda.cu:1538-1551): head h of row n draws the splitmix64 word of
+ * rng + (n+1)*GOLD + (h+1)*0xD1B54A32D192ED03. out (device f64, (K+2)*N) = [actions (head h at
+ * h*N + n); joint logp; value]. Y: PH_F32 or PH_F64 rows as for ph_ppo_grad_md. */
+int ph_sample_actions_md(int dtype, const void* Y, size_t ldy, size_t N, const int* head_sizes, size_t K,
+                         uint64_t rng, double* out, void* stream);
+/* Gaussian draw (k_sample_cont, puffercuda.cu:1652-1668): Box-Muller from the words of rng + (n+1)*GOLD +
+ * (2i+1)*G2 and (2i+2)*G2 (u1 floored at 1e-7); a = mu + exp(ls) z. out (device f64, (d+2)*N) =
+ * [actions (dim i at i*N + n); logp; value]. */
+int ph_sample_actions_cont(int dtype, const void* Y, size_t ldy, size_t N, size_t d, uint64_t rng,
+                           double ls_lo, double ls_hi, double* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- */
 /* GEMM on MFMA. C[MxN] = op(A)[MxK] op(B)[KxN] with a fused epilogue, row-major. Replaces gemm32
  * (cublasGemmEx, puffercuda.cu:661-667) and the cuBLASLt dense layers (pufferblas.c:302-365).
@@ -306,6 +341,20 @@ int ph_cuda_train_update_resident(size_t policyH, const double* obs, const doubl
                                   size_t H, size_t A, size_t epochs, size_t numMB, double lr, double wd,
                                   double mu, double eps, double vfCoef, double entCoef, double clipEps,
                                   double vfClip, double maxGradNorm, uint8_t bf16, double* out1);
+/* lean_cuda_train_update_wide_resident (puffercuda.cu:1307-1411): the whole resident update for
+ * multi-discrete (mode 1: Wdim heads of sizes hs[0..Wdim), O = sum + 1) and Gaussian (mode 2: Wdim
+ * dims, O = 2 Wdim + 1) policies. acts: NT x Wdim row-major. hs/hsN: the head sizes as doubles (read
+ * in mode 1 only). Otherwise as ph_cuda_train_update_resident, except that Newton-Schulz is always
+ * the exact f64 one, as in the reference. Every perm entry must lie in [0, NT) (all whole-update
+ * entries check this on the host; the reference would read out of bounds). out1: params[0]. */
+int ph_cuda_train_update_wide_resident(size_t policyH, const double* obs, const double* acts,
+                                       const double* adv, const double* ret, const double* olp,
+                                       const double* ov, size_t ovN, const double* perm, const double* hs,
+                                       size_t hsN, size_t NT, size_t D, size_t H, size_t O, size_t Wdim,
+                                       uint32_t mode, size_t epochs, size_t numMB, double lr, double wd,
+                                       double mu, double eps, double vfCoef, double entCoef,
+                                       double clipEps, double vfClip, double maxGradNorm, uint8_t bf16,
+                                       double* out1);
 /* lean_cuda_muon_stepmat (puffercuda.cu:557-631): exact f64 Muon of one matrix. out: [newW; newMom]. */
 int ph_cuda_muon_stepmat(const double* W, const double* G, const double* M, size_t rows, size_t cols,
                          double lr, double wd, double mu, double eps, double* out);
@@ -414,6 +463,24 @@ int ph_cuda_mingru_step(const double* params, const double* obs, const double* s
  * relu(obs W1^T + b1) W2^T + b2. bf16 selects bf16 MFMA products, else fp32. */
 int ph_cuda_mlp_forward(const double* params, const double* obs, size_t N, size_t D, size_t H, size_t O,
                         uint8_t bf16, double* out);
+/* lean_cuda_sample_actions_md (puffercuda.cu:1553-1568): Y N*O f64, hs K head sizes as doubles;
+ * out[(K+2)*N] = [actions (head-major); joint logp; value]. */
+int ph_cuda_sample_actions_md(const double* Y, const double* hs, size_t N, size_t K, size_t O, uint64_t rng,
+                              double* out);
+/* lean_cuda_sample_actions_cont (puffercuda.cu:1670-1684): Y N*O f64 (O = 2d+1), log-std clamp [-20, 2];
+ * out[(d+2)*N] = [actions (dim-major); logp; value]. */
+int ph_cuda_sample_actions_cont(const double* Y, size_t N, size_t d, size_t O, uint64_t rng, double* out);
+/* lean_cuda_mlp_ppo_grad_md (puffercuda.cu:1570-1650): flattenMLP with O = sum(hs) + 1 outputs, acts N*K,
+ * the multi-discrete head loss; g: P summed gradient. */
+int ph_cuda_mlp_ppo_grad_md(const double* params, const double* obs, const double* acts, const double* advs,
+                            const double* rets, const double* oldlps, const double* hs, size_t N, size_t H,
+                            size_t D, size_t K, double vfCoef, double entCoef, double clipEps, uint8_t bf16,
+                            double* g);
+/* lean_cuda_mlp_ppo_grad_cont (puffercuda.cu:1873-1940): flattenMLP with O = 2d+1 outputs, acts N*d,
+ * the Gaussian head loss (log-std clamp [-20, 2]); g: P summed gradient. */
+int ph_cuda_mlp_ppo_grad_cont(const double* params, const double* obs, const double* acts, const double* advs,
+                              const double* rets, const double* oldlps, size_t N, size_t H, size_t D, size_t d,
+                              double vfCoef, double entCoef, double clipEps, uint8_t bf16, double* g);
 /* lean_cuda_mingru_muon_resident (puffercuda.cu:5727), host-gradient mode: gClip (nG >= P) is the
  * clipped gradient; Muon on every flattenMG matrix of the handle (fp32-MFMA Newton-Schulz on f64
  * state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the biases, in place. wOut: P. */

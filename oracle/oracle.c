@@ -45,11 +45,21 @@
  *                                closed form a = floor(u*A); draw frequencies against the softmax
  *   orc_mingru_step              T chained steps from a zero state equal orc_mingru_ppo_grad_seq's
  *                                new values and new log-probs (a separately pinned function)
+ *   orc_ppo_grad_md / _cont      central finite differences of independently written numpy objectives
+ *                                (joint clipped surrogate, value loss, entropy); K = 1 equals
+ *                                orc_ppo_grad; the clamp mask zeroes saturated log-stds
+ *   orc_sample_md / _cont        numpy inverse-CDF / Box-Muller on the pinned splitmix64 words; Gaussian
+ *                                draw moments; K = 1 logp equals log softmax
+ *   orc_wide_losses              mode 1 with K = 1 equals orc_ppo_losses; two heads equal one head over
+ *                                the product space; mode 2 logp and entropy against scipy's normal
+ *                                logpdf / entropy; special cases (adv 0, ratio 1, no value clip)
  */
 #include "oracle.h"
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+
+#define M_PI_ORACLE 3.14159265358979323846
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -899,4 +909,225 @@ void orc_mingru_step(const double* p, const double* obs, const double* state, si
   free(h);
   free(hn);
   free(y);
+}
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Multi-discrete and continuous heads. */
+
+static double vloss_grad_d(double v, double ret, const double* ov, size_t n, double vfClip) {
+  if (vfClip <= 0.0 || !ov) return v - ret;
+  const double dd = v - ov[n];
+  const double vc = ov[n] + (dd < -vfClip ? -vfClip : (dd > vfClip ? vfClip : dd));
+  if ((v - ret) * (v - ret) >= (vc - ret) * (vc - ret)) return v - ret;
+  if (dd > -vfClip && dd < vfClip) return v - ret;
+  return 0.0;
+}
+
+static double dpol_of(double ratio, double adv, double clip) {
+  const double lo = 1.0 - clip, hi = 1.0 + clip;
+  const double rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+  if (adv * ratio <= adv * rc) return adv * ratio;
+  return (lo < ratio && ratio < hi) ? adv * ratio : 0.0;
+}
+
+/* k_ppo_dout_md (puffercuda.cu:702-727): joint log-prob over the heads, one clip, per-head softmax and
+ * entropy gradients. A row with an action outside [0, size) of its head gets NaN logit gradients and
+ * NaN log-prob (its value gradient stands). */
+void orc_ppo_grad_md(const double* out, size_t ldo, const double* act, const double* adv, const double* ret,
+                     const double* old, const double* ov, size_t N, const int* sizes, size_t K, double vf,
+                     double ent, double clip, double vfClip, double* dout, size_t ldd, double* newlp,
+                     double* newval) {
+  size_t W = 0;
+  for (size_t h = 0; h < K; h++) W += (size_t)sizes[h];
+  for (size_t n = 0; n < N; n++) {
+    const double* o = out + n * ldo;
+    double* d = dout + n * ldd;
+    double joint = 0.0;
+    int inRange = 1;
+    size_t off = 0;
+    for (size_t h = 0; h < K; h++) {
+      const double ah = act[n * K + h];
+      double se = 0.0;
+      for (int k = 0; k < sizes[h]; k++) se += exp(o[off + k]);
+      if (ah >= 0.0 && ah < (double)sizes[h]) joint += o[off + (size_t)ah] - log(se);
+      else inRange = 0;
+      off += (size_t)sizes[h];
+    }
+    if (!inRange) joint = NAN;
+    const double dPol = inRange ? dpol_of(exp(joint - old[n]), adv[n], clip) : NAN;
+    off = 0;
+    for (size_t h = 0; h < K; h++) {
+      const int a = (int)act[n * K + h];
+      double se = 0.0;
+      for (int k = 0; k < sizes[h]; k++) se += exp(o[off + k]);
+      const double lse = log(se);
+      double pout = 0.0;
+      for (int k = 0; k < sizes[h]; k++) pout += exp(o[off + k] - lse) * o[off + k];
+      for (int k = 0; k < sizes[h]; k++) {
+        const double p = exp(o[off + k] - lse);
+        d[off + k] = dPol * ((k == a ? 1.0 : 0.0) - p) + ent * p * (pout - o[off + k]);
+      }
+      off += (size_t)sizes[h];
+    }
+    d[W] = -vf * vloss_grad_d(o[W], ret[n], ov, n, vfClip);
+    if (newlp) newlp[n] = joint;
+    if (newval) newval[n] = o[W];
+  }
+}
+
+/* k_ppo_dout_cont (puffercuda.cu:1767-1790); the CPU twin pufferffi.c:264-307 is this with a [-5, 2]
+ * clamp and no value clip. */
+void orc_ppo_grad_cont(const double* out, size_t ldo, const double* act, const double* adv, const double* ret,
+                       const double* old, const double* ov, size_t N, size_t d, double vf, double ent,
+                       double clip, double vfClip, double lslo, double lshi, double* dout, size_t ldd,
+                       double* newlp, double* newval) {
+  const double hl = 0.5 * log(2.0 * M_PI_ORACLE);
+  for (size_t n = 0; n < N; n++) {
+    const double* o = out + n * ldo;
+    double* g = dout + n * ldd;
+    const double* a = act + n * d;
+    double logp = 0.0;
+    for (size_t i = 0; i < d; i++) {
+      const double lsr = o[d + i], ls = lsr < lslo ? lslo : (lsr > lshi ? lshi : lsr);
+      const double z = (a[i] - o[i]) * exp(-ls);
+      logp += -0.5 * z * z - ls - hl;
+    }
+    const double dPol = dpol_of(exp(logp - old[n]), adv[n], clip);
+    for (size_t i = 0; i < d; i++) {
+      const double lsr = o[d + i], ls = lsr < lslo ? lslo : (lsr > lshi ? lshi : lsr);
+      const double inv = exp(-ls), z = (a[i] - o[i]) * inv;
+      g[i] = dPol * z * inv;
+      g[d + i] = (lslo < lsr && lsr < lshi) ? dPol * (z * z - 1.0) + ent : 0.0;
+    }
+    g[2 * d] = -vf * vloss_grad_d(o[2 * d], ret[n], ov, n, vfClip);
+    if (newlp) newlp[n] = logp;
+    if (newval) newval[n] = o[2 * d];
+  }
+}
+
+static const uint64_t ORC_GOLD2 = 0xD1B54A32D192ED03ULL;
+static double orc_word_unit(uint64_t state) {
+  uint64_t s = state - 0x9E3779B97F4A7C15ULL; /* orc_rng_next advances before mixing */
+  return orc_uniform01(orc_rng_next(&s));
+}
+
+/* ff_surface_losses modes 1 and 2 (puffercuda.cu:1798-1870): the 7 dashboard losses [pg, v, ent, total,
+ * old_kl, kl, clipfrac] as means over N rows of head outputs. mode 1: K categorical heads of sizes[K]
+ * (max-shifted log-sum-exp per head, entropy summed over the heads); mode 2: d Gaussian dims with the
+ * log-std clamped to [lslo, lshi], entropy sum(ls + (1 + log 2 pi)/2). The value is at column ldo-wide
+ * row index W (sum of sizes, or 2d). ov NULL or vfClip <= 0: unclipped value loss. */
+void orc_wide_losses(int mode, const double* out, size_t ldo, const double* act, const double* adv,
+                     const double* ret, const double* old, const double* ov, size_t N, const int* sizes, size_t K,
+                     size_t d, double vfCoef, double entCoef, double clipEps, double vfClip, double lslo,
+                     double lshi, double* L) {
+  const double lo = 1.0 - clipEps, hi = 1.0 + clipEps, hl = 0.5 * log(2.0 * M_PI_ORACLE);
+  const int clipV = ov != NULL && vfClip > 0.0;
+  double sPg = 0, sV = 0, sEnt = 0, sKL = 0, sOld = 0;
+  size_t nclip = 0;
+  for (size_t n = 0; n < N; n++) {
+    const double* o = out + n * ldo;
+    double newlp = 0.0, ent = 0.0, newval;
+    if (mode == 2) {
+      for (size_t i = 0; i < d; i++) {
+        const double lsr = o[d + i], ls = lsr < lslo ? lslo : (lsr > lshi ? lshi : lsr);
+        const double z = (act[n * d + i] - o[i]) * exp(-ls);
+        newlp += -0.5 * z * z - ls - hl;
+        ent += ls + (0.5 + hl);
+      }
+      newval = o[2 * d];
+    } else {
+      size_t off = 0;
+      for (size_t h = 0; h < K; h++) {
+        const int sz = sizes[h];
+        const size_t a = (size_t)act[n * K + h];
+        double mx = o[off];
+        for (int k = 1; k < sz; k++) if (o[off + k] > mx) mx = o[off + k];
+        double se = 0.0;
+        for (int k = 0; k < sz; k++) se += exp(o[off + k] - mx);
+        const double lse = mx + log(se);
+        newlp += o[off + a] - lse;
+        for (int k = 0; k < sz; k++) { const double lp = o[off + k] - lse; ent -= exp(lp) * lp; }
+        off += (size_t)sz;
+      }
+      newval = o[off];
+    }
+    sEnt += ent;
+    const double lr = newlp - old[n], ratio = exp(lr);
+    const double rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+    const double p1 = -adv[n] * ratio, p2 = -adv[n] * rc;
+    sPg += p1 > p2 ? p1 : p2;
+    if (ratio < lo || ratio > hi) nclip++;
+    sKL += (ratio - 1.0) - lr;
+    sOld += -lr;
+    const double du = (newval - ret[n]) * (newval - ret[n]);
+    double vl = du;
+    if (clipV) {
+      const double dd = newval - ov[n];
+      const double vc = ov[n] + (dd < -vfClip ? -vfClip : (dd > vfClip ? vfClip : dd));
+      const double cc = (vc - ret[n]) * (vc - ret[n]);
+      if (cc > du) vl = cc;
+    }
+    sV += 0.5 * vl;
+  }
+  const double dn = (double)N;
+  L[0] = sPg / dn; L[1] = sV / dn; L[2] = sEnt / dn;
+  L[3] = L[0] + vfCoef * L[1] - entCoef * L[2];
+  L[4] = sOld / dn; L[5] = sKL / dn; L[6] = (double)nclip / dn;
+}
+
+/* k_sample_md (puffercuda.cu:1538-1551). */
+void orc_sample_md(const double* Y, size_t ldy, size_t N, const int* sizes, size_t K, uint64_t rng,
+                   double* out) {
+  size_t W = 0;
+  for (size_t h = 0; h < K; h++) W += (size_t)sizes[h];
+  for (size_t n = 0; n < N; n++) {
+    const double* row = Y + n * ldy;
+    double joint = 0.0;
+    size_t off = 0;
+    for (size_t h = 0; h < K; h++) {
+      const int sz = sizes[h];
+      double m = row[off];
+      for (int k = 1; k < sz; k++)
+        if (row[off + k] > m) m = row[off + k];
+      double z = 0.0;
+      for (int k = 0; k < sz; k++) z += exp(row[off + k] - m);
+      const double u = orc_word_unit(rng + (uint64_t)(n + 1) * 0x9E3779B97F4A7C15ULL + (uint64_t)(h + 1) * ORC_GOLD2);
+      double acc = 0.0;
+      int a = sz - 1;
+      for (int k = 0; k < sz; k++) {
+        acc += exp(row[off + k] - m) / z;
+        if (u < acc) {
+          a = k;
+          break;
+        }
+      }
+      out[h * N + n] = (double)a;
+      joint += log(exp(row[off + a] - m) / z);
+      off += (size_t)sz;
+    }
+    out[K * N + n] = joint;
+    out[(K + 1) * N + n] = row[W];
+  }
+}
+
+/* k_sample_cont (puffercuda.cu:1652-1668). */
+void orc_sample_cont(const double* Y, size_t ldy, size_t N, size_t d, uint64_t rng, double lslo, double lshi,
+                     double* out) {
+  const double hl = 0.5 * log(2.0 * M_PI_ORACLE);
+  for (size_t n = 0; n < N; n++) {
+    const double* row = Y + n * ldy;
+    double logp = 0.0;
+    for (size_t i = 0; i < d; i++) {
+      const double lsr = row[d + i], ls = lsr < lslo ? lslo : (lsr > lshi ? lshi : lsr);
+      const uint64_t base = rng + (uint64_t)(n + 1) * 0x9E3779B97F4A7C15ULL;
+      double u1 = orc_word_unit(base + (uint64_t)(2 * i + 1) * ORC_GOLD2);
+      if (u1 < 1.0e-7) u1 = 1.0e-7;
+      const double u2 = orc_word_unit(base + (uint64_t)(2 * i + 2) * ORC_GOLD2);
+      const double z = sqrt(-2.0 * log(u1)) * cos(2.0 * M_PI_ORACLE * u2);
+      out[i * N + n] = row[i] + exp(ls) * z;
+      logp += -0.5 * z * z - ls - hl;
+    }
+    out[d * N + n] = logp;
+    out[(d + 1) * N + n] = row[2 * d];
+  }
 }

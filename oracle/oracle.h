@@ -151,6 +151,32 @@ void orc_sample_actions(const double* Y, size_t N, size_t A, size_t O, uint64_t 
 void orc_mingru_step(const double* p, const double* obs, const double* state, size_t N, size_t D,
                      size_t H, size_t L, size_t A, double* out);
 
+/* ---- multi-discrete and continuous heads ---- */
+/* k_ppo_dout_md (puffercuda.cu:702-727) in f64: row n of out (stride ldo) holds the K heads' logits
+ * (sizes[h] each, W in all) then the value at W; act N x K. Writes dout (W+1 per row, stride ldd),
+ * newlp (joint log-prob) and newval (may be NULL). Ascent sign. */
+void orc_ppo_grad_md(const double* out, size_t ldo, const double* act, const double* adv, const double* ret,
+                     const double* old, const double* ov, size_t N, const int* sizes, size_t K, double vf,
+                     double ent, double clip, double vfClip, double* dout, size_t ldd, double* newlp,
+                     double* newval);
+/* k_ppo_dout_cont (puffercuda.cu:1767-1790; pufferffi.c:223-330) in f64: row n holds d means, d raw
+ * log-stds (clamped to [lslo, lshi]) and the value at 2d; act N x d. */
+void orc_ppo_grad_cont(const double* out, size_t ldo, const double* act, const double* adv, const double* ret,
+                       const double* old, const double* ov, size_t N, size_t d, double vf, double ent,
+                       double clip, double vfClip, double lslo, double lshi, double* dout, size_t ldd,
+                       double* newlp, double* newval);
+/* k_sample_md (puffercuda.cu:1538-1551): out[(K+2)N] = [actions (head-major); joint logp; value]. */
+/* Dashboard losses of multi-discrete (mode 1) / Gaussian (mode 2) heads (ff_surface_losses). */
+void orc_wide_losses(int mode, const double* out, size_t ldo, const double* act, const double* adv,
+                     const double* ret, const double* old, const double* ov, size_t N, const int* sizes, size_t K,
+                     size_t d, double vfCoef, double entCoef, double clipEps, double vfClip, double lslo,
+                     double lshi, double* L);
+void orc_sample_md(const double* Y, size_t ldy, size_t N, const int* sizes, size_t K, uint64_t rng,
+                   double* out);
+/* k_sample_cont (puffercuda.cu:1652-1668): out[(d+2)N] = [actions (dim-major); logp; value]. */
+void orc_sample_cont(const double* Y, size_t ldy, size_t N, size_t d, uint64_t rng, double lslo, double lshi,
+                     double* out);
+
 #ifdef __cplusplus
 }
 #endif

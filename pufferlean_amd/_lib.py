@@ -19,6 +19,7 @@ PH_EPI_NONE, PH_EPI_BIAS, PH_EPI_BIAS_RELU, PH_EPI_RELU_MASK, PH_EPI_AXPBY = 0, 
 vp, sz, dbl, flt, i32, i64, u8, u64 = (C.c_void_p, C.c_size_t, C.c_double, C.c_float, C.c_int,
                                        C.c_long, C.c_uint8, C.c_uint64)
 dptr = C.POINTER(C.c_double)
+u32 = C.c_uint32
 fptr = C.POINTER(C.c_float)
 szptr = C.POINTER(C.c_size_t)
 
@@ -74,6 +75,10 @@ SIGNATURES: dict[str, list] = {
     "ph_mb_gather": [vp, vp, vp, sz, vp, vp, vp],
     "ph_mb_iterate": [vp, vp, sz, vp, vp, vp],
     "ph_sample_actions": [i32, vp, sz, sz, sz, i32, u64, vp, vp, vp, vp],
+    "ph_ppo_grad_md": [vp, sz, vp, vp, vp, vp, vp, sz, vp, sz, flt, flt, flt, flt, vp, sz, vp, vp, vp, vp],
+    "ph_ppo_grad_cont": [vp, sz, vp, vp, vp, vp, vp, sz, sz, flt, flt, flt, flt, flt, flt, vp, sz, vp, vp, vp, vp],
+    "ph_sample_actions_md": [i32, vp, sz, sz, vp, sz, u64, vp, vp],
+    "ph_sample_actions_cont": [i32, vp, sz, sz, sz, u64, dbl, dbl, vp, vp],
     "ph_mingru_rollout_step": [vp, vp, vp, vp, vp, vp],
     # host-buffer layer (reference Lean @[extern] GPU symbols)
     "ph_cuda_vtrace": [dptr, dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
@@ -86,6 +91,9 @@ SIGNATURES: dict[str, list] = {
                              dbl, dbl, dbl, dbl, u8, dptr],
     "ph_cuda_train_update_resident": [sz, dptr, dptr, dptr, dptr, dptr, dptr, sz, dptr, sz, sz, sz, sz, sz,
                                       sz, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, u8, dptr],
+    "ph_cuda_train_update_wide_resident": [sz, dptr, dptr, dptr, dptr, dptr, dptr, sz, dptr, dptr, sz, sz, sz,
+                                           sz, sz, sz, u32, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl,
+                                           u8, dptr],
     "ph_cuda_muon_stepmat": [dptr, dptr, dptr, sz, sz, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_muon_step_mlp_resident": [sz, dptr, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dptr],
     "ph_cuda_policy_load": [dptr, sz, szptr],
@@ -109,6 +117,10 @@ SIGNATURES: dict[str, list] = {
     "ph_cuda_sample_actions": [dptr, sz, sz, sz, u64, dptr],
     "ph_cuda_mingru_step": [dptr, dptr, dptr, sz, sz, sz, sz, sz, u8, dptr],
     "ph_cuda_mlp_forward": [dptr, dptr, sz, sz, sz, sz, u8, dptr],
+    "ph_cuda_sample_actions_md": [dptr, dptr, sz, sz, sz, u64, dptr],
+    "ph_cuda_sample_actions_cont": [dptr, sz, sz, sz, u64, dptr],
+    "ph_cuda_mlp_ppo_grad_md": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, u8, dptr],
+    "ph_cuda_mlp_ppo_grad_cont": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, u8, dptr],
     "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }

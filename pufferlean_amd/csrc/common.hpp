@@ -77,4 +77,17 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
 }
 __device__ __forceinline__ uint16_t bf16_rne(float a) { return (uint16_t)(bf16x2_rne(a, 0.f) & 0xffffu); }
 
+// Gradient of the (optionally clipped) value loss 0.5 (v - ret)^2 with respect to v: with vfClip > 0
+// and an old value, the loss is max((v - ret)^2, (clip(v - vold) + vold - ret)^2) / 2
+// (d_vloss_grad, puffercuda.cu:692-700).
+__device__ inline float vloss_grad(float vnew, float ret, float vold, bool has_old, float vfClip) {
+  if (vfClip <= 0.f || !has_old) return vnew - ret;
+  const float dd = vnew - vold;
+  const float vc = vold + (dd < -vfClip ? -vfClip : (dd > vfClip ? vfClip : dd));
+  const float du = (vnew - ret) * (vnew - ret), cc = (vc - ret) * (vc - ret);
+  if (du >= cc) return vnew - ret;
+  if (dd > -vfClip && dd < vfClip) return vnew - ret;
+  return 0.f;
+}
+
 }  // namespace ph

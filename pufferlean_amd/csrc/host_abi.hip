@@ -54,6 +54,7 @@ enum : int {
   kHsRoll = kSlotHost + 15,   // MinGRU rollout step staging
   kHsSample = kSlotHost + 16, // sampler staging
   kHsObsTraj = kSlotHost + 17,  // resident obs trajectory of the MinGRU chain (f32)
+  kHsHeads = kSlotHost + 18,    // multi-discrete / continuous head staging
 };
 
 // Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
@@ -124,11 +125,24 @@ __global__ void k_gather_cols(const double* __restrict__ idx, long n, const doub
   const long k = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= n) return;
   const long r = idx ? (long)(int)idx[k] : k;
-  gact[k] = (int)act[r];
+  if (gact) gact[k] = (int)act[r];
   gadv[k] = adv[r];
   gret[k] = (float)ret[r];
   gold[k] = (float)old[r];
   if (ov) gov[k] = (float)ov[r];
+}
+// Wide action rows: the Wd f64 action columns of row idx[k] (row k without idx) as int32
+// (multi-discrete heads) into gi, or as f32 (Gaussian dims) into gf.
+__global__ void k_gather_wide(const double* __restrict__ idx, long n, int Wd, const double* __restrict__ act,
+                              int* __restrict__ gi, float* __restrict__ gf) {
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * Wd) return;
+  const long k = t / Wd;
+  const int j = (int)(t % Wd);
+  const long r = idx ? (long)(int)idx[k] : k;
+  const double v = act[r * Wd + j];
+  if (gi) gi[t] = (int)v;
+  else gf[t] = (float)v;
 }
 __global__ void k_bias_relu_f64(double* __restrict__ Y, const double* __restrict__ b, long N, int H,
                                 int relu) {
@@ -277,26 +291,23 @@ PhGemmDesc f32desc(int ta, int tb, long M, long N, long K, const float* A, long 
 // dOut by the fused PPO loss (no max shift, as k_ppo_dout); gb2 = colsum dOut; gW2 = dOut^T H1;
 // dZ = (dOut W2) masked by H1 > 0; gb1 = colsum dZ; gW1 = dZ^T X. `bf`: bf16 MFMA on the fp32
 // operands (the reference's FAST_16BF), else fp32 MFMA.
-int mlp_grad_dev(const MlpShape& s, long N, const MlpWork& w, int bf, double vf, double ent, double clip,
-                 double vfClip, bool use_ov, double* losses, hipStream_t st) {
+// MLP forward (relu hidden, linear head) -> head(): the loss gradient of Out into dOut -> backward into
+// the f32 gradient gf. head() may use dZ's first N floats as staging: dZ is written only by the dgrad
+// GEMM that follows it.
+template <typename HeadFn>
+int mlp_grad_head(const MlpShape& s, long N, const MlpWork& w, int bf, HeadFn&& head, hipStream_t st) {
   const int math = bf ? PH_MATH_BF16 : PH_MATH_F32;
   const float* W1 = w.Wf + s.oW1;
   const float* b1 = w.Wf + s.ob1;
   const float* W2 = w.Wf + s.oW2;
   const float* b2 = w.Wf + s.ob2;
-  // advantages as the f32 the loss computes in, staged in dZ's first N floats (dZ is written only
-  // by the dgrad GEMM, after the loss kernel has read them)
-  float* advf = w.dZ;
-  PH_TRY(to_f32(w.advn, advf, N, st));
   PhGemmDesc g = f32desc(0, 1, N, s.H, s.D, w.X, s.D, W1, s.D, w.H1, s.H, math);
   g.epi = PH_EPI_BIAS_RELU; g.bias = b1;
   PH_TRY(gemm(g, st));
   g = f32desc(0, 1, N, s.O, s.H, w.H1, s.H, W2, s.H, w.Out, s.O, math);
   g.epi = PH_EPI_BIAS; g.bias = b2;
   PH_TRY(gemm(g, st));
-  PH_TRY(ppo_grad(w.Out, s.O, w.Out + s.A, s.O, w.act, advf, w.ret, w.old, use_ov ? w.ov : nullptr, N,
-                  s.A, (float)vf, (float)ent, (float)clip, (float)vfClip, 0, w.dOut, s.O, w.dOut + s.A,
-                  s.O, nullptr, nullptr, losses, st));
+  PH_TRY(head());
   PH_TRY(colsum_f32(w.dOut, N, s.O, s.O, w.gf + s.ob2, 1.f, 0, st));
   PH_TRY(gemm(f32desc(1, 0, s.O, s.H, N, w.dOut, s.O, w.H1, s.H, w.gf + s.oW2, s.H, math), st));
   g = f32desc(0, 0, N, s.H, s.O, w.dOut, s.O, W2, s.H, w.dZ, s.H, math);
@@ -305,6 +316,18 @@ int mlp_grad_dev(const MlpShape& s, long N, const MlpWork& w, int bf, double vf,
   PH_TRY(colsum_f32(w.dZ, N, s.H, s.H, w.gf + s.ob1, 1.f, 0, st));
   PH_TRY(gemm(f32desc(1, 0, s.H, s.D, N, w.dZ, s.H, w.X, s.D, w.gf + s.oW1, s.D, math), st));
   return PH_OK;
+}
+
+int mlp_grad_dev(const MlpShape& s, long N, const MlpWork& w, int bf, double vf, double ent, double clip,
+                 double vfClip, bool use_ov, double* losses, hipStream_t st) {
+  return mlp_grad_head(s, N, w, bf, [&]() {
+    // advantages as the f32 the loss computes in, staged in dZ
+    float* advf = w.dZ;
+    PH_TRY(to_f32(w.advn, advf, N, st));
+    return ppo_grad(w.Out, s.O, w.Out + s.A, s.O, w.act, advf, w.ret, w.old, use_ov ? w.ov : nullptr, N, s.A,
+                    (float)vf, (float)ent, (float)clip, (float)vfClip, 0, w.dOut, s.O, w.dOut + s.A, s.O, nullptr,
+                    nullptr, losses, st);
+  }, st);
 }
 
 // Muon on an f64 [rows x cols] matrix in place: exact tier (f64 Newton-Schulz, the reference's op
@@ -370,25 +393,55 @@ int state_bufs(long P, State& t) {
 // of the columns), normalise the advantages, gradient, mean (and optional clip), Muon in place.
 struct Cols {
   float* obs;  // [NT][D]
-  const double *act, *adv, *ret, *old, *ov;
+  const double *act, *adv, *ret, *old, *ov;  // act: [NT][Wd] (Wd = 1 for the categorical head)
 };
-int mlp_minibatch(const MlpShape& s, const Cols& cols, const double* idx, long Nmb, MlpWork& w,
-                  double* par, double* mom, double* G, int bf, bool mixed, double lr, double wd, double mu,
-                  double eps, double vf, double ent, double clip, double vfClip, double maxGradNorm,
+// The action head of an update: one categorical head over the O - 1 logits (mode 0), K categorical
+// heads of the given sizes (mode 1), or a Gaussian of Wd dims (mode 2). actI / actF hold the gathered
+// minibatch actions of modes 1 and 2.
+struct HeadSpec {
+  int mode = 0;
+  int Wd = 1;
+  int sizes[kMaxHeads] = {};
+  int* actI = nullptr;
+  float* actF = nullptr;
+};
+constexpr double kContLsLo = -20.0, kContLsHi = 2.0;  // the reference's GPU clamp (puffercuda.cu:1646-1647)
+int mlp_minibatch(const MlpShape& s, const HeadSpec& head, const Cols& cols, const double* idx, long Nmb,
+                  MlpWork& w, double* par, double* mom, double* G, int bf, bool mixed, double lr, double wd,
+                  double mu, double eps, double vf, double ent, double clip, double vfClip, double maxGradNorm,
                   bool want_losses, hipStream_t st) {
   const bool use_ov = cols.ov != nullptr && vfClip > 0.0;
+  const bool cat = head.mode == 0;
   if (idx) {
     k_gather_rows<<<ceil_div(Nmb * s.D, kT), kT, 0, st>>>(cols.obs, idx, w.X, Nmb, s.D);
   } else {
     PH_CHECK_HIP(hipMemcpyAsync(w.X, cols.obs, (size_t)Nmb * s.D * 4, hipMemcpyDeviceToDevice, st));
   }
-  k_gather_cols<<<ceil_div(Nmb, kT), kT, 0, st>>>(idx, Nmb, cols.act, cols.adv, cols.ret, cols.old,
-                                                 use_ov ? cols.ov : nullptr, w.act, w.adv, w.ret, w.old,
-                                                 w.ov);
+  k_gather_cols<<<ceil_div(Nmb, kT), kT, 0, st>>>(idx, Nmb, cat ? cols.act : nullptr, cols.adv, cols.ret, cols.old,
+                                                 use_ov ? cols.ov : nullptr, cat ? w.act : nullptr, w.adv, w.ret,
+                                                 w.old, w.ov);
   PH_LAUNCH_CHECK();
+  if (!cat) {
+    k_gather_wide<<<ceil_div(Nmb * head.Wd, kT), kT, 0, st>>>(idx, Nmb, head.Wd, cols.act, head.actI, head.actF);
+    PH_LAUNCH_CHECK();
+  }
   PH_TRY(moments_normalize(PH_F64, w.adv, Nmb, w.advn, w.stats, st));
   PH_TRY(to_f32(par, w.Wf, s.P, st));
-  PH_TRY(mlp_grad_dev(s, Nmb, w, bf, vf, ent, clip, vfClip, use_ov, want_losses ? w.losses : nullptr, st));
+  double* losses = want_losses ? w.losses : nullptr;
+  if (cat) {
+    PH_TRY(mlp_grad_dev(s, Nmb, w, bf, vf, ent, clip, vfClip, use_ov, losses, st));
+  } else {
+    PH_TRY(mlp_grad_head(s, Nmb, w, bf, [&]() {
+      PH_TRY(to_f32(w.advn, w.dZ, Nmb, st));  // advantages as the f32 the loss computes in, staged in dZ
+      const float* ov = use_ov ? w.ov : nullptr;
+      if (head.mode == 1)
+        return ppo_grad_md(w.Out, s.O, head.actI, w.dZ, w.ret, w.old, ov, Nmb, head.sizes, head.Wd, (float)vf,
+                           (float)ent, (float)clip, (float)vfClip, w.dOut, s.O, nullptr, nullptr, losses, st);
+      return ppo_grad_cont(w.Out, s.O, head.actF, w.dZ, w.ret, w.old, ov, Nmb, head.Wd, (float)vf, (float)ent,
+                           (float)clip, (float)vfClip, (float)kContLsLo, (float)kContLsHi, w.dOut, s.O, nullptr,
+                           nullptr, losses, st);
+    }, st));
+  }
   k_f32_f64<<<ceil_div(s.P, kT), kT, 0, st>>>(w.gf, G, s.P, 1.0);
   PH_LAUNCH_CHECK();
   double gscale = 1.0 / (double)Nmb;
@@ -492,6 +545,122 @@ extern "C" int ph_cuda_mlp_ppo_grad(const double* params, const double* obs, con
   return down(g, dg, s.P * 8);
 }
 
+namespace {
+// Shared set-up of the multi-discrete / continuous MLP gradients: params, obs, adv, ret, old on the
+// device in the f32/f64 forms mlp_grad_head's head kernel reads.
+int mlp_head_inputs(const MlpShape& s, const double* params, const double* obs, const double* advs,
+                    const double* rets, const double* oldlps, MlpWork& w, double*& dg) {
+  PH_TRY(mlp_work(s, s.N, w));
+  double *dp, *dx, *dc;
+  PH_TRY(carve(kHsCols, [&](Carve& c) {
+    dp = c.take<double>(s.P); dx = c.take<double>((size_t)s.N * s.D); dc = c.take<double>(3 * s.N);
+    dg = c.take<double>(s.P);
+  }));
+  PH_TRY(up(dp, params, s.P * 8)); PH_TRY(up(dx, obs, (size_t)s.N * s.D * 8));
+  PH_TRY(up(w.advn, advs, s.N * 8)); PH_TRY(up(dc, rets, s.N * 8)); PH_TRY(up(dc + s.N, oldlps, s.N * 8));
+  PH_TRY(to_f32(dp, w.Wf, s.P, nullptr));
+  PH_TRY(to_f32(dx, w.X, s.N * s.D, nullptr));
+  PH_TRY(to_f32(dc, w.ret, s.N, nullptr));
+  PH_TRY(to_f32(dc + s.N, w.old, s.N, nullptr));
+  return PH_OK;
+}
+int mlp_head_finish(const MlpShape& s, const MlpWork& w, double* dg, double* g) {
+  k_f32_f64<<<ceil_div(s.P, kT), kT>>>(w.gf, dg, s.P, 1.0);
+  PH_LAUNCH_CHECK();
+  PH_TRY(finish());
+  return down(g, dg, s.P * 8);
+}
+int sizes_from(const double* hs, size_t K, int* sizes, size_t& W, const char* who) {
+  PH_REQUIRE(hs && K >= 1 && K <= (size_t)kMaxHeads, "%s: K=%zu heads (1..%d)", who, K, kMaxHeads);
+  W = 0;
+  for (size_t h = 0; h < K; h++) {
+    PH_REQUIRE(hs[h] >= 1.0 && hs[h] <= 4096.0, "%s: head %zu size %g", who, h, hs[h]);
+    sizes[h] = (int)hs[h];
+    W += (size_t)sizes[h];
+  }
+  return PH_OK;
+}
+}  // namespace
+
+extern "C" int ph_cuda_mlp_ppo_grad_md(const double* params, const double* obs, const double* acts,
+                                       const double* advs, const double* rets, const double* oldlps,
+                                       const double* hs, size_t N, size_t H, size_t D, size_t K, double vfCoef,
+                                       double entCoef, double clipEps, uint8_t bf16, double* g) {
+  int sizes[kMaxHeads];
+  size_t W = 0;
+  PH_TRY(sizes_from(hs, K, sizes, W, "ph_cuda_mlp_ppo_grad_md"));
+  PH_REQUIRE(N > 0 && H > 0 && D > 0 && N <= 0x7fffffffUL, "ph_cuda_mlp_ppo_grad_md: bad shape");
+  PH_REQUIRE(params && obs && acts && advs && rets && oldlps && g, "ph_cuda_mlp_ppo_grad_md: null buffer");
+  const MlpShape s = mlp_shape(N, H, D, W);
+  MlpWork w;
+  double* dg;
+  PH_TRY(mlp_head_inputs(s, params, obs, advs, rets, oldlps, w, dg));
+  double* da;
+  int* ai;
+  PH_TRY(carve(kHsHeads, [&](Carve& c) { da = c.take<double>(N * K); ai = c.take<int>(N * K); }));
+  PH_TRY(up(da, acts, N * K * 8));
+  k_f64_i32<<<ceil_div(N * K, kT), kT>>>(da, ai, (long)(N * K));
+  PH_LAUNCH_CHECK();
+  PH_TRY(mlp_grad_head(s, s.N, w, bf16, [&]() {
+    PH_TRY(to_f32(w.advn, w.dZ, s.N, nullptr));
+    return ppo_grad_md(w.Out, s.O, ai, w.dZ, w.ret, w.old, nullptr, N, sizes, K, (float)vfCoef, (float)entCoef,
+                       (float)clipEps, 0.f, w.dOut, s.O, nullptr, nullptr, nullptr, nullptr);
+  }, nullptr));
+  return mlp_head_finish(s, w, dg, g);
+}
+
+extern "C" int ph_cuda_mlp_ppo_grad_cont(const double* params, const double* obs, const double* acts,
+                                         const double* advs, const double* rets, const double* oldlps, size_t N,
+                                         size_t H, size_t D, size_t d, double vfCoef, double entCoef, double clipEps,
+                                         uint8_t bf16, double* g) {
+  PH_REQUIRE(N > 0 && H > 0 && D > 0 && d >= 1 && N <= 0x7fffffffUL, "ph_cuda_mlp_ppo_grad_cont: bad shape");
+  PH_REQUIRE(params && obs && acts && advs && rets && oldlps && g, "ph_cuda_mlp_ppo_grad_cont: null buffer");
+  const MlpShape s = mlp_shape(N, H, D, 2 * d);
+  MlpWork w;
+  double* dg;
+  PH_TRY(mlp_head_inputs(s, params, obs, advs, rets, oldlps, w, dg));
+  double* da;
+  float* af;
+  PH_TRY(carve(kHsHeads, [&](Carve& c) { da = c.take<double>(N * d); af = c.take<float>(N * d); }));
+  PH_TRY(up(da, acts, N * d * 8));
+  PH_TRY(to_f32(da, af, (long)(N * d), nullptr));
+  PH_TRY(mlp_grad_head(s, s.N, w, bf16, [&]() {
+    PH_TRY(to_f32(w.advn, w.dZ, s.N, nullptr));
+    return ppo_grad_cont(w.Out, s.O, af, w.dZ, w.ret, w.old, nullptr, N, d, (float)vfCoef, (float)entCoef,
+                         (float)clipEps, 0.f, (float)kContLsLo, (float)kContLsHi, w.dOut, s.O, nullptr, nullptr,
+                         nullptr, nullptr);
+  }, nullptr));
+  return mlp_head_finish(s, w, dg, g);
+}
+
+extern "C" int ph_cuda_sample_actions_md(const double* Y, const double* hs, size_t N, size_t K, size_t O,
+                                         uint64_t rng, double* out) {
+  int sizes[kMaxHeads];
+  size_t W = 0;
+  PH_TRY(sizes_from(hs, K, sizes, W, "ph_cuda_sample_actions_md"));
+  PH_REQUIRE(O >= W + 1 && N <= 0x7fffffffUL, "ph_cuda_sample_actions_md: O=%zu below %zu", O, W + 1);
+  if (N == 0) return PH_OK;
+  PH_REQUIRE(Y && out, "ph_cuda_sample_actions_md: null buffer");
+  double *dY, *dO;
+  PH_TRY(carve(kHsSample, [&](Carve& c) { dY = c.take<double>(N * O); dO = c.take<double>((K + 2) * N); }));
+  PH_TRY(up(dY, Y, N * O * 8));
+  PH_TRY(sample_actions_md(PH_F64, dY, O, N, sizes, K, rng, dO, nullptr));
+  PH_TRY(finish());
+  return down(out, dO, (K + 2) * N * 8);
+}
+
+extern "C" int ph_cuda_sample_actions_cont(const double* Y, size_t N, size_t d, size_t O, uint64_t rng, double* out) {
+  PH_REQUIRE(d >= 1 && O >= 2 * d + 1 && N <= 0x7fffffffUL, "ph_cuda_sample_actions_cont: d=%zu O=%zu", d, O);
+  if (N == 0) return PH_OK;
+  PH_REQUIRE(Y && out, "ph_cuda_sample_actions_cont: null buffer");
+  double *dY, *dO;
+  PH_TRY(carve(kHsSample, [&](Carve& c) { dY = c.take<double>(N * O); dO = c.take<double>((d + 2) * N); }));
+  PH_TRY(up(dY, Y, N * O * 8));
+  PH_TRY(sample_actions_cont(PH_F64, dY, O, N, d, rng, kContLsLo, kContLsHi, dO, nullptr));
+  PH_TRY(finish());
+  return down(out, dO, (d + 2) * N * 8);
+}
+
 extern "C" int ph_cuda_train_step(const double* pm, const double* obs, const double* acts,
                                   const double* advRaw, const double* rets, const double* oldlps, size_t N,
                                   size_t H, size_t D, size_t A, double lr, double wd, double mu, double eps,
@@ -515,36 +684,45 @@ extern "C" int ph_cuda_train_step(const double* pm, const double* obs, const dou
   const Cols cols{obsf, dc, dc + N, dc + 2 * N, dc + 3 * N, nullptr};
   // bf16 tier: bf16-MFMA gradient GEMMs and fp32-MFMA Newton-Schulz (the reference's bf16 Muon runs
   // fp32 Sgemm, puffercuda.cu:937-941); fp32 tier: fp32 GEMMs and the exact f64 Newton-Schulz.
-  PH_TRY(mlp_minibatch(s, cols, nullptr, s.N, w, t.par, t.mom, t.G, bf16, bf16 != 0, lr, wd, mu, eps, vfCoef,
-                       entCoef, clipEps, 0.0, 0.0, false, nullptr));
+  PH_TRY(mlp_minibatch(s, HeadSpec{}, cols, nullptr, s.N, w, t.par, t.mom, t.G, bf16, bf16 != 0, lr, wd, mu, eps,
+                       vfCoef, entCoef, clipEps, 0.0, 0.0, false, nullptr));
   PH_TRY(finish());
   return down(out, t.par, 2 * s.P * 8);
 }
 
 namespace {
 // Shared body of the whole-update entries: columns uploaded once, epochs x minibatches on device.
-int train_update_impl(double* par, double* mom, const double* obs, const double* acts, const double* adv,
-                      const double* ret, const double* olp, const double* ov, const double* perm, size_t NT,
-                      size_t D, size_t H, size_t A, size_t epochs, size_t numMB, double lr, double wd,
+// acts holds head.Wd f64 columns per row. Every shuffle index must lie in [0, NT): the gathers read
+// the row it names.
+int train_update_impl(double* par, double* mom, const HeadSpec& head0, const double* obs, const double* acts,
+                      const double* adv, const double* ret, const double* olp, const double* ov, const double* perm,
+                      size_t NT, size_t D, size_t H, size_t O, size_t epochs, size_t numMB, double lr, double wd,
                       double mu, double eps, double vfCoef, double entCoef, double clipEps, double vfClip,
-                      double maxGradNorm, int bf, bool mixed, bool losses) {
-  const MlpShape s = mlp_shape(NT, H, D, A);
+                      double maxGradNorm, int bf, bool mixed, bool losses, const char* who) {
+  for (size_t i = 0; i < epochs * NT; i++)
+    PH_REQUIRE(perm[i] >= 0.0 && perm[i] < (double)NT, "%s: shuffle index %g at %zu outside [0, %zu)", who, perm[i], i,
+               NT);
+  const MlpShape s = mlp_shape(NT, H, D, O - 1);
   const size_t mbSize = numMB > 0 && NT / numMB > 0 ? NT / numMB : 1;
+  const size_t Wd = (size_t)head0.Wd;
+  HeadSpec head = head0;
   MlpWork w;
   PH_TRY(mlp_work(s, s.N, w));
-  double *dx, *dc, *dperm, *G;
+  double *dx, *dact, *dc, *dperm, *G;
   float* obsf;
   PH_TRY(carve(kHsCols, [&](Carve& c) {
-    dx = c.take<double>(NT * D); dc = c.take<double>(5 * NT); dperm = c.take<double>(epochs * NT);
-    obsf = c.take<float>(NT * D); G = c.take<double>(s.P);
+    dx = c.take<double>(NT * D); dact = c.take<double>(NT * Wd); dc = c.take<double>(4 * NT);
+    dperm = c.take<double>(epochs * NT); obsf = c.take<float>(NT * D); G = c.take<double>(s.P);
+    head.actI = head.mode == 1 ? c.take<int>(NT * Wd) : nullptr;
+    head.actF = head.mode == 2 ? c.take<float>(NT * Wd) : nullptr;
   }));
   PH_TRY(up(dx, obs, NT * D * 8));
-  PH_TRY(up(dc, acts, NT * 8)); PH_TRY(up(dc + NT, adv, NT * 8));
-  PH_TRY(up(dc + 2 * NT, ret, NT * 8)); PH_TRY(up(dc + 3 * NT, olp, NT * 8));
-  if (ov) PH_TRY(up(dc + 4 * NT, ov, NT * 8));
+  PH_TRY(up(dact, acts, NT * Wd * 8)); PH_TRY(up(dc, adv, NT * 8));
+  PH_TRY(up(dc + NT, ret, NT * 8)); PH_TRY(up(dc + 2 * NT, olp, NT * 8));
+  if (ov) PH_TRY(up(dc + 3 * NT, ov, NT * 8));
   PH_TRY(up(dperm, perm, epochs * NT * 8));
   PH_TRY(to_f32(dx, obsf, (long)(NT * D), nullptr));
-  const Cols cols{obsf, dc, dc + NT, dc + 2 * NT, dc + 3 * NT, ov ? dc + 4 * NT : nullptr};
+  const Cols cols{obsf, dact, dc, dc + NT, dc + 2 * NT, ov ? dc + 3 * NT : nullptr};
   for (size_t e = 0; e < epochs; e++)
     for (size_t m = 0; m < numMB; m++) {
       const size_t lo = m * mbSize;
@@ -552,7 +730,7 @@ int train_update_impl(double* par, double* mom, const double* obs, const double*
       if (hi > NT) hi = NT;
       if (hi <= lo) continue;
       const bool last = losses && e + 1 == epochs && m + 1 == numMB;
-      PH_TRY(mlp_minibatch(s, cols, dperm + e * NT + lo, (long)(hi - lo), w, par, mom, G, bf, mixed, lr, wd,
+      PH_TRY(mlp_minibatch(s, head, cols, dperm + e * NT + lo, (long)(hi - lo), w, par, mom, G, bf, mixed, lr, wd,
                            mu, eps, vfCoef, entCoef, clipEps, vfClip, maxGradNorm, last, nullptr));
     }
   return PH_OK;
@@ -571,8 +749,9 @@ extern "C" int ph_cuda_train_update(const double* pm, const double* obs, const d
   PH_TRY(state_bufs(s.P, t));
   PH_TRY(up(t.par, pm, 2 * s.P * 8));
   // the whole-update twin always orthogonalises in exact f64 (puffercuda.cu:1168-1171)
-  PH_TRY(train_update_impl(t.par, t.mom, obs, acts, adv, ret, olp, nullptr, perm, NT, D, H, A, epochs, numMB,
-                           lr, wd, mu, eps, vfCoef, entCoef, clipEps, 0.0, 0.0, bf16, false, false));
+  PH_TRY(train_update_impl(t.par, t.mom, HeadSpec{}, obs, acts, adv, ret, olp, nullptr, perm, NT, D, H, A + 1,
+                           epochs, numMB, lr, wd, mu, eps, vfCoef, entCoef, clipEps, 0.0, 0.0, bf16, false, false,
+                           "ph_cuda_train_update"));
   PH_TRY(finish());
   return down(out, t.par, 2 * s.P * 8);
 }
@@ -591,9 +770,44 @@ extern "C" int ph_cuda_train_update_resident(size_t policyH, const double* obs, 
   const MlpShape s = mlp_shape(NT, H, D, A);
   double* par = (double*)policyH;
   const bool vclip = vfClip > 0.0 && ov && ovN >= NT;  // an empty old-value column turns the clip off
-  PH_TRY(train_update_impl(par, par + s.P, obs, acts, adv, ret, olp, vclip ? ov : nullptr, perm, NT, D, H, A,
+  PH_TRY(train_update_impl(par, par + s.P, HeadSpec{}, obs, acts, adv, ret, olp, vclip ? ov : nullptr, perm, NT, D,
+                           H, A + 1, epochs, numMB, lr, wd, mu, eps, vfCoef, entCoef, clipEps, vclip ? vfClip : 0.0,
+                           maxGradNorm, bf16, bf16 != 0, g_mgLossOn != 0, "ph_cuda_train_update_resident"));
+  PH_TRY(finish());
+  return down(out1, par, 8);  // params[0], the caller's divergence guard
+}
+
+extern "C" int ph_cuda_train_update_wide_resident(size_t policyH, const double* obs, const double* acts,
+                                                  const double* adv, const double* ret, const double* olp,
+                                                  const double* ov, size_t ovN, const double* perm, const double* hs,
+                                                  size_t hsN, size_t NT, size_t D, size_t H, size_t O, size_t Wdim,
+                                                  uint32_t mode, size_t epochs, size_t numMB, double lr, double wd,
+                                                  double mu, double eps, double vfCoef, double entCoef,
+                                                  double clipEps, double vfClip, double maxGradNorm, uint8_t bf16,
+                                                  double* out1) {
+  const char* who = "ph_cuda_train_update_wide_resident";
+  PH_REQUIRE(policyH != 0, "%s: no policy handle", who);
+  PH_REQUIRE(mode == 1 || mode == 2, "%s: mode %u (1 multi-discrete, 2 Gaussian)", who, mode);
+  PH_REQUIRE(NT > 0 && H > 0 && D > 0 && Wdim >= 1 && numMB > 0 && NT <= 0x7fffffffUL, "%s: bad shape", who);
+  PH_REQUIRE(obs && acts && adv && ret && olp && perm && out1, "%s: null buffer", who);
+  HeadSpec head;
+  head.mode = (int)mode;
+  head.Wd = (int)Wdim;
+  if (mode == 1) {
+    PH_REQUIRE(hs && hsN >= Wdim, "%s: %zu head sizes for %zu heads", who, hsN, Wdim);
+    size_t W = 0;
+    PH_TRY(sizes_from(hs, Wdim, head.sizes, W, who));
+    PH_REQUIRE(O == W + 1, "%s: O=%zu but the head sizes sum to %zu", who, O, W);
+  } else {
+    PH_REQUIRE(O == 2 * Wdim + 1, "%s: O=%zu for %zu Gaussian dims (2d+1)", who, O, Wdim);
+  }
+  const MlpShape s = mlp_shape(NT, H, D, O - 1);
+  double* par = (double*)policyH;
+  const bool vclip = vfClip > 0.0 && ov && ovN >= NT;  // an empty old-value column turns the clip off
+  // the wide update orthogonalises in exact f64 whatever the GEMM precision (puffercuda.cu:1397-1400)
+  PH_TRY(train_update_impl(par, par + s.P, head, obs, acts, adv, ret, olp, vclip ? ov : nullptr, perm, NT, D, H, O,
                            epochs, numMB, lr, wd, mu, eps, vfCoef, entCoef, clipEps, vclip ? vfClip : 0.0,
-                           maxGradNorm, bf16, bf16 != 0, g_mgLossOn != 0));
+                           maxGradNorm, bf16, false, g_mgLossOn != 0, who));
   PH_TRY(finish());
   return down(out1, par, 8);  // params[0], the caller's divergence guard
 }

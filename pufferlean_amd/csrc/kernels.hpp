@@ -26,6 +26,8 @@ enum : int {
   kSlotGclip = 18,
   kSlotRollout = 19,  // rollout step: layer inputs, layer products, padded head
   kSlotMgBufs = 20,
+  kSlotHeadsPart = 21,     // multi-discrete / Gaussian heads: dashboard-loss block partials
+  kSlotHeadsCounter = 22,  // multi-discrete / Gaussian heads: arrival counter (256 bytes)
   kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
   kSlotHost = 48,     // 48..127: host-buffer entry points
 };
@@ -135,6 +137,24 @@ int mb_gather(const ph_replay_cols& c, const int* seg, const double* mp, size_t 
               hipStream_t st);
 int mb_iterate(const ph_replay_cols& c, const int* seg, size_t B, const float* newlp, const float* newval,
                hipStream_t st);
+
+// Multi-discrete and continuous heads (heads.hip). Head sizes travel by value in the kernel arguments.
+constexpr int kMaxHeads = 32;
+struct HeadSizes {
+  int K;
+  int n[kMaxHeads];
+};
+int ppo_grad_md(const float* out, size_t ldo, const int* act, const float* adv, const float* ret, const float* old,
+                const float* ov, size_t N, const int* sizes, size_t K, float vf, float ent, float clip, float vfClip,
+                float* dout, size_t ldd, float* newlp, float* newval, double* losses, hipStream_t st);
+int ppo_grad_cont(const float* out, size_t ldo, const float* act, const float* adv, const float* ret,
+                  const float* old, const float* ov, size_t N, size_t d, float vf, float ent, float clip, float vfClip,
+                  float lslo, float lshi, float* dout, size_t ldd, float* newlp, float* newval, double* losses,
+                  hipStream_t st);
+int sample_actions_md(int dtype, const void* Y, size_t ldy, size_t N, const int* sizes, size_t K, uint64_t rng,
+                      double* out, hipStream_t st);
+int sample_actions_cont(int dtype, const void* Y, size_t ldy, size_t N, size_t d, uint64_t rng, double lslo,
+                        double lshi, double* out, hipStream_t st);
 
 // Rollout forward and sampler (rollout.hip). out3 (may be NULL): [act; logp; value] as f64 [3N].
 int sample_actions(int dtype, const void* Y, size_t ldy, size_t N, size_t A, int has_value, uint64_t rng, int* act,

@@ -7,21 +7,12 @@
 // (per-block partials in f64, the last block folds them in block order).
 #include "common.hpp"
 #include "kernels.hpp"
+#include "losses.hpp"
 
 namespace ph {
 namespace {
 
 constexpr int kMaxA = 64;
-
-__device__ inline float vloss_grad(float vnew, float ret, float vold, bool has_old, float vfClip) {
-  if (vfClip <= 0.f || !has_old) return vnew - ret;
-  const float dd = vnew - vold;
-  const float vc = vold + (dd < -vfClip ? -vfClip : (dd > vfClip ? vfClip : dd));
-  const float du = (vnew - ret) * (vnew - ret), cc = (vc - ret) * (vc - ret);
-  if (du >= cc) return vnew - ret;
-  if (dd > -vfClip && dd < vfClip) return vnew - ret;
-  return 0.f;
-}
 
 // VEC: logit and gradient rows are 16-byte aligned with a pitch that covers A rounded up to 4, so each
 // row moves as float4s (a quarter of the memory instructions of the scalar form; same arithmetic).
@@ -112,83 +103,17 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
     if (newlp) newlp[n] = logpA;
     if (newval) newval[n] = vnew;
     if (losses) {
-      const double lr = (double)logpA - (double)ol;
-      const double r = exp(lr);
-      const double dlo = 1.0 - (double)clipEps, dhi = 1.0 + (double)clipEps;
-      const double rcd = r < dlo ? dlo : (r > dhi ? dhi : r);
-      const double p1 = -(double)av * r, p2 = -(double)av * rcd;
-      lsum[0] = p1 > p2 ? p1 : p2;
-      const double du = ((double)vnew - rv) * ((double)vnew - rv);
-      double vl = du;
-      if (vfClip > 0.f && ov) {
-        const double dd = (double)vnew - vold;
-        const double vc = vold + (dd < -vfClip ? -(double)vfClip : (dd > vfClip ? (double)vfClip : dd));
-        const double cc = (vc - rv) * (vc - rv);
-        if (cc > du) vl = cc;
-      }
-      lsum[1] = 0.5 * vl;
-      // entropy from the fp32 probabilities of the gradient path (one fp64 exp per row above is
-      // for the ratio terms; 16 more per row made this kernel fp64-bound)
+      // entropy from the fp32 probabilities of the gradient path (one fp64 exp per row in row_losses
+      // is for the ratio terms; 16 more per row made this kernel fp64-bound)
       float ent = 0.f;
 #pragma unroll
       for (int k = 0; k < AMAX; k++)
         if (k < A) ent -= pk[k] * (x[k] - lse);
-      lsum[2] = (double)ent;
-      lsum[3] = -lr;
-      lsum[4] = (r - 1.0) - lr;
-      lsum[5] = (r < dlo || r > dhi) ? 1.0 : 0.0;
+      row_losses(logpA, ol, av, vnew, rv, vold, vfClip > 0.f && ov, vfClip, clipEps, ent, lsum);
     }
   }
   if (!losses) return;
-  // Deterministic block reduction of the 6 sums, then last-block fold over blocks in order.
-  __shared__ double sh[6][256];
-  __shared__ bool last;
-#pragma unroll
-  for (int q = 0; q < 6; q++) sh[q][threadIdx.x] = lsum[q];
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s)
-#pragma unroll
-      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int q = 0; q < 6; q++) part[(size_t)blockIdx.x * 6 + q] = sh[q][0];
-    __threadfence();
-    last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // Fold the block partials in a fixed order: thread t adds blocks t, t+256, ... in sequence, then
-  // the same tree as above combines the 256 thread sums.
-#pragma unroll
-  for (int q = 0; q < 6; q++) {
-    double s = 0.0;
-    for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x)
-      s += __hip_atomic_load(&part[(size_t)b * 6 + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh[q][threadIdx.x] = s;
-  }
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s)
-#pragma unroll
-      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    const double dn = (double)(N > 0 ? N : 1);
-    const double pg = sh[0][0] / dn, vl = sh[1][0] / dn, en = sh[2][0] / dn;
-    losses[0] = pg;
-    losses[1] = vl;
-    losses[2] = en;
-    losses[3] = pg + (double)vfCoef * vl - (double)entCoef * en;
-    losses[4] = sh[3][0] / dn;
-    losses[5] = sh[4][0] / dn;
-    losses[6] = sh[5][0] / dn;
-    *counter = 0u;
-  }
+  fold_losses(lsum, part, counter, losses, N, vfCoef, entCoef);
 }
 
 }  // namespace

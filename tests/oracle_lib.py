@@ -51,6 +51,11 @@ _SIG = {
     "orc_mb_iterate": ([vp, vp, vp, vp, vp, vp, sz, sz], None),
     "orc_sample_actions": ([vp, sz, sz, sz, C.c_uint64, vp], None),
     "orc_mingru_step": ([vp, vp, vp, sz, sz, sz, sz, sz, vp], None),
+    "orc_ppo_grad_md": ([vp, sz, vp, vp, vp, vp, vp, sz, vp, sz, d, d, d, d, vp, sz, vp, vp], None),
+    "orc_ppo_grad_cont": ([vp, sz, vp, vp, vp, vp, vp, sz, sz, d, d, d, d, d, d, vp, sz, vp, vp], None),
+    "orc_sample_md": ([vp, sz, sz, vp, sz, C.c_uint64, vp], None),
+    "orc_sample_cont": ([vp, sz, sz, sz, C.c_uint64, d, d, vp], None),
+    "orc_wide_losses": ([i, vp, sz, vp, vp, vp, vp, vp, sz, vp, sz, sz, d, d, d, d, d, d, vp], None),
 }
 
 _lib = None
@@ -63,8 +68,7 @@ def build() -> None:
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        if not ORACLE_SO.exists():
-            build()
+        build()  # make rebuilds only when oracle.c or oracle.h is newer than the library
         h = C.CDLL(str(ORACLE_SO))
         for name, (args, res) in _SIG.items():
             f = getattr(h, name)
@@ -211,3 +215,62 @@ def mingru_step(params, obs, state, N, D, H, L, A):
     out = np.zeros(N * (A + 1) + N * L * H)
     lib().orc_mingru_step(P(f64(params)), P(f64(obs)), P(f64(state)), N, D, H, L, A, P(out))
     return out[:N * (A + 1)].reshape(N, A + 1), out[N * (A + 1):].reshape(N, L, H)
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def ppo_grad_md(out, act, adv, ret, old, ov, sizes, *, vf=0.5, ent=0.01, clip=0.2, vfclip=0.0):
+    out = f64(out)
+    N, O = out.shape
+    K = len(sizes)
+    sz = _i32(sizes)
+    d = np.zeros((N, O))
+    nlp, nv = np.zeros(N), np.zeros(N)
+    lib().orc_ppo_grad_md(P(out), O, P(f64(act)), P(f64(adv)), P(f64(ret)), P(f64(old)),
+                          P(None if ov is None else f64(ov)), N, P(sz), K, vf, ent, clip, vfclip, P(d), O, P(nlp),
+                          P(nv))
+    return d, nlp, nv
+
+
+def ppo_grad_cont(out, act, adv, ret, old, ov, dim, *, vf=0.5, ent=0.01, clip=0.2, vfclip=0.0, lslo=-20.0,
+                  lshi=2.0):
+    out = f64(out)
+    N, O = out.shape
+    d = np.zeros((N, O))
+    nlp, nv = np.zeros(N), np.zeros(N)
+    lib().orc_ppo_grad_cont(P(out), O, P(f64(act)), P(f64(adv)), P(f64(ret)), P(f64(old)),
+                            P(None if ov is None else f64(ov)), N, dim, vf, ent, clip, vfclip, lslo, lshi, P(d), O,
+                            P(nlp), P(nv))
+    return d, nlp, nv
+
+
+def wide_losses(mode, out, act, adv, ret, old, ov, *, sizes=None, dim=0, vf=0.5, ent=0.01, clip=0.2, vfclip=0.0,
+                lslo=-20.0, lshi=2.0):
+    """The 7 dashboard losses of multi-discrete (mode 1, head sizes) or Gaussian (mode 2, dim) rows."""
+    out = f64(out)
+    N, O = out.shape
+    K = len(sizes) if sizes is not None else 0
+    L = np.zeros(7)
+    lib().orc_wide_losses(mode, P(out), O, P(f64(act)), P(f64(adv)), P(f64(ret)), P(f64(old)),
+                          P(None if ov is None else f64(ov)), N, P(_i32(sizes) if sizes is not None else None), K,
+                          dim, vf, ent, clip, vfclip, lslo, lshi, P(L))
+    return L
+
+
+def sample_md(Y, sizes, rng_state):
+    Y = f64(Y)
+    N, O = Y.shape
+    K = len(sizes)
+    out = np.zeros((K + 2) * N)
+    lib().orc_sample_md(P(Y), O, N, P(_i32(sizes)), K, rng_state & 0xFFFFFFFFFFFFFFFF, P(out))
+    return out
+
+
+def sample_cont(Y, dim, rng_state, lslo=-20.0, lshi=2.0):
+    Y = f64(Y)
+    N, O = Y.shape
+    out = np.zeros((dim + 2) * N)
+    lib().orc_sample_cont(P(Y), O, N, dim, rng_state & 0xFFFFFFFFFFFFFFFF, lslo, lshi, P(out))
+    return out

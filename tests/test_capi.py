@@ -69,6 +69,27 @@ def test_host_entries_reject_bad_arguments_without_device():
     assert lib.ph_cuda_policy_download(0, 4, None) == L.PH_ERR_ARG
 
 
+def test_wide_update_rejects_bad_arguments_without_device():
+    # the handle is never dereferenced: every check below returns before any device work
+    import numpy as np
+    NT, D, H = 4, 3, 5
+    z = np.zeros(64)
+    p = z.ctypes.data_as(L.dptr)
+    hs = np.array([2.0, 3.0]).ctypes.data_as(L.dptr)
+    bad_perm = np.array([0.0, 1.0, 4.0, 2.0]).ctypes.data_as(L.dptr)  # 4 is outside [0, NT)
+
+    def call(mode, O, W, perm=p, hsp=hs, hsN=2):
+        return L.lib().ph_cuda_train_update_wide_resident(1, p, p, p, p, p, None, 0, perm, hsp, hsN, NT, D, H, O, W,
+                                                          mode, 1, 1, 0.02, 0.0, 0.95, 1e-7, 0.5, 0.01, 0.2, 0.0,
+                                                          0.0, 0, p)
+    lib = L.lib()
+    assert call(3, 6, 2) == L.PH_ERR_ARG and b"mode" in lib.ph_last_error()
+    assert call(1, 7, 2) == L.PH_ERR_ARG and b"sum" in lib.ph_last_error()   # sizes sum to 5: O must be 6
+    assert call(1, 6, 2, hsN=1) == L.PH_ERR_ARG
+    assert call(2, 6, 2) == L.PH_ERR_ARG and b"2d+1" in lib.ph_last_error()  # 2 dims: O must be 5
+    assert call(1, 6, 2, perm=bad_perm) == L.PH_ERR_ARG and b"shuffle index" in lib.ph_last_error()
+
+
 def test_no_device_calls_fail_cleanly():
     lib = L.lib()
     assert lib.ph_version() == 100

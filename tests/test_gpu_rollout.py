@@ -114,8 +114,9 @@ def test_rollout_step_matches_oracle_over_three_steps(gpu, prec, tol):
     ref_state = np.zeros((N, Lr, H))
     for t in range(3):
         obs = rng.normal(0x712 + t, N * Dm).reshape(N, Dm)
+        gobs = cu(obs, torch.float32)  # held until after the synchronize: the kernel reads it
         L.call("ph_mingru_rollout_step", C.byref(dims), C.c_void_p(gp.data_ptr()),
-               C.c_void_p(cu(obs, torch.float32).data_ptr()), C.c_void_p(state.data_ptr()),
+               C.c_void_p(gobs.data_ptr()), C.c_void_p(state.data_ptr()),
                C.c_void_p(out.data_ptr()), C.c_void_p(torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         ref_out, ref_state = O.mingru_step(params.astype(np.float32).astype(np.float64),
