@@ -19,6 +19,10 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
   replay  prioritised replay between V-trace and the BPTT on 4096 segments x 64 with 4096 draws:
           segment |adv| sums, sampler, minibatch gather (+ normalisation), value/ratio iterate, in
           the fp32 time-major layout and in the reference's f64 segment-major layout
+  heads   multi-discrete (heads 9 and 5, 262,144 rows) and Gaussian (4 dims, 131,072 rows) loss
+          gradients with their dashboard losses, the two samplers over one step of 4096 / 2048
+          agents, and the whole wide update (4 epochs, hidden 128) through its host-buffer entry
+          (wall time, PCIe upload of the f64 columns included)
 Component times are HIP-event times of a HIP graph holding `steps` launches (device time per launch,
 no host launch path; "us_eager" is the same loop launched from Python). Events are recorded on the
 stream the kernels run on.
@@ -354,6 +358,97 @@ def bench_rollout(steps, warmup):
     return r
 
 
+# multi-discrete heads: the reference's `target` env (config/target.ini, ocean/target/adapter.c: 4096
+# agents, obs 28, heads {9, 5}, minibatch 32768); Gaussian: its `drone` env (config/drone.ini,
+# ocean/drone: 2048 agents, obs 21, 4 dims, minibatch 16384); default horizon 64, hidden 128, 4 epochs
+MD_AGENTS, MD_OBS, MD_HEADS, MD_MB = 4096, 28, (9, 5), 32768
+CT_AGENTS, CT_OBS, CT_DIM, CT_MB = 2048, 21, 4, 16384
+HD_T, HD_H, HD_EPOCHS = 64, 128, 4
+
+
+def bench_heads(steps, warmup):
+    import ctypes as C
+    import numpy as np
+    import torch
+    from pufferlean_amd import _lib as L
+    from pufferlean_amd import device as D
+    from pufferlean_amd import rng
+
+    out = {}
+    K = len(MD_HEADS)
+    # loss gradients over a whole rollout of rows, dashboard losses folded in the same launch
+    for name, N, O, Wd in (("md_grad", MD_AGENTS * HD_T, sum(MD_HEADS) + 1, K),
+                           ("cont_grad", CT_AGENTS * HD_T, 2 * CT_DIM + 1, CT_DIM)):
+        y = _t(rng.normal(rng.seed_for(8, 0), N * O)).view(N, O)
+        if name == "md_grad":
+            act = torch.stack([_t(rng.randint(rng.seed_for(8, 1 + h), N, s), np.int32) for h, s in enumerate(MD_HEADS)],
+                              1).contiguous()
+        else:
+            act = _t(rng.normal(rng.seed_for(8, 1), N * Wd)).view(N, Wd)
+        adv, ret = _t(rng.normal(rng.seed_for(8, 8), N)), _t(rng.normal(rng.seed_for(8, 9), N))
+        old, ov = _t(rng.normal(rng.seed_for(8, 10), N) - 3.0), _t(rng.normal(rng.seed_for(8, 11), N))
+        dout = torch.empty_like(y)
+        losses = torch.zeros(7, device="cuda", dtype=torch.float64)
+        if name == "md_grad":
+            fn = lambda: D.ppo_grad_md(y, act, adv, ret, old, ov, head_sizes=MD_HEADS, vf_clip=0.2, dout=dout,
+                                       losses=losses)
+        else:
+            fn = lambda: D.ppo_grad_cont(y, act, adv, ret, old, ov, dim=CT_DIM, vf_clip=0.2, dout=dout, losses=losses)
+        us = time_graph(fn, steps, warmup) * 1e3
+        # per row: the O head outputs read and their O gradients written, Wd actions, adv/ret/old/ov
+        nbytes = N * (2 * O * 4 + Wd * 4 + 4 * 4)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"rows": N, "us": round(us, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # samplers over one rollout step of the env's agents
+    Ym = _t(rng.normal(rng.seed_for(8, 20), MD_AGENTS * (sum(MD_HEADS) + 1))).view(MD_AGENTS, -1)
+    om = torch.empty((K + 2) * MD_AGENTS, device="cuda", dtype=torch.float64)
+    out["md_sample_us"] = round(time_graph(lambda: D.sample_actions_md(Ym, MD_HEADS, rng_state=0x5EED, out=om),
+                                           steps, warmup) * 1e3, 2)
+    Yc = _t(rng.normal(rng.seed_for(8, 21), CT_AGENTS * (2 * CT_DIM + 1))).view(CT_AGENTS, -1)
+    oc = torch.empty((CT_DIM + 2) * CT_AGENTS, device="cuda", dtype=torch.float64)
+    out["cont_sample_us"] = round(time_graph(lambda: D.sample_actions_cont(Yc, CT_DIM, rng_state=0x5EED, out=oc),
+                                             steps, warmup) * 1e3, 2)
+    # the whole wide update through its host-buffer entry: f64 columns uploaded once, 4 epochs of
+    # minibatches on the device, exact f64 Muon; wall time per call, PCIe upload included
+    dp = lambda a: np.ascontiguousarray(a, np.float64).ctypes.data_as(L.dptr)
+    for name, mode, agents, Dm, O, Wd, mb in (("md_update", 1, MD_AGENTS, MD_OBS, sum(MD_HEADS) + 1, K, MD_MB),
+                                              ("cont_update", 2, CT_AGENTS, CT_OBS, 2 * CT_DIM + 1, CT_DIM, CT_MB)):
+        NT = agents * HD_T
+        P = HD_H * Dm + HD_H + O * HD_H + O
+        pm = np.concatenate([rng.normal(rng.seed_for(8, 30), P) * 0.1, np.zeros(P)])
+        obs = rng.normal(rng.seed_for(8, 31), NT * Dm)
+        if mode == 1:
+            acts = np.stack([rng.randint(rng.seed_for(8, 32 + h), NT, s) for h, s in enumerate(MD_HEADS)],
+                            1).astype(np.float64)
+        else:
+            acts = rng.normal(rng.seed_for(8, 32), NT * Wd)
+        adv, ret = rng.normal(rng.seed_for(8, 40), NT), rng.normal(rng.seed_for(8, 41), NT)
+        olp, ov = rng.normal(rng.seed_for(8, 42), NT) - 3.0, rng.normal(rng.seed_for(8, 43), NT)
+        perm = np.concatenate([np.random.default_rng(e).permutation(NT) for e in range(HD_EPOCHS)]).astype(np.float64)
+        hs = np.array(MD_HEADS, np.float64)
+        h = C.c_size_t(0)
+        L.call("ph_cuda_policy_load", dp(pm), P, C.byref(h))
+        peek = np.zeros(1)
+        args = [dp(obs), dp(acts), dp(adv), dp(ret), dp(olp), dp(ov), NT, dp(perm), dp(hs), len(hs), NT, Dm, HD_H, O,
+                Wd, mode, HD_EPOCHS, NT // mb, 0.015, 0.0, 0.95, 1e-12, 2.0, 0.001, 0.2, 0.2, 1.5, 1, dp(peek)]
+        try:
+            n_calls = max(2, min(steps, 5))
+            L.call("ph_cuda_train_update_wide_resident", h.value, *args)
+            t0 = time.perf_counter()
+            for _ in range(n_calls):
+                L.call("ph_cuda_train_update_wide_resident", h.value, *args)
+            ms = (time.perf_counter() - t0) / n_calls * 1e3
+        finally:
+            L.call("ph_cuda_policy_free", h.value)
+        out[name] = {"rows": NT, "obs": Dm, "hidden": HD_H, "out": O, "epochs": HD_EPOCHS, "minibatch": mb,
+                     "ms": round(ms, 2), "rows_per_s": round(NT / (ms * 1e-3), 1),
+                     "upload_bytes": 8 * (NT * (Dm + Wd + 4) + HD_EPOCHS * NT)}
+    out["heads"] = list(MD_HEADS)
+    out["cont_dims"] = CT_DIM
+    return out
+
+
 def traffic_kernels():
     """Launches for the two HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
     the dominant kernel (layer-forward GEMM) 3 times, then a plain 512 MiB device copy 3 times, whose
@@ -459,6 +554,9 @@ def main():
     if args.only in ("all", "replay"):
         comps["replay"] = bench_replay(args.steps, args.warmup)
         print("# replay done", file=sys.stderr, flush=True)
+    if args.only in ("all", "heads"):
+        comps["heads"] = bench_heads(args.steps, args.warmup)
+        print("# heads done", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": head["samples_per_s"] if head else None,

@@ -1135,9 +1135,67 @@ int gemm_scalar(const GemmArgs& g, const PhGemmDesc& d, hipStream_t st) {
   return PH_OK;
 }
 
+// dst [rows_p][cols_p] = src [rows][cols] (row stride ld) with zeros beyond it.
+template <typename T>
+__global__ void __launch_bounds__(256) k_pad2d(const T* __restrict__ src, long rows, long cols, long ld,
+                                              T* __restrict__ dst, long rows_p, long cols_p) {
+  const long n = rows_p * cols_p;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / cols_p, c = i % cols_p;
+    dst[i] = (r < rows && c < cols) ? src[r * ld + c] : T(0);
+  }
+}
+
+int pad2d(int dtype, const void* src, long rows, long cols, long ld, int slot, long rows_p, long cols_p, const void*& out,
+          hipStream_t st) {
+  const size_t esz = dtype == PH_BF16 ? 2 : 4;
+  void* dst = scratch(slot, (size_t)rows_p * cols_p * esz);
+  if (!dst) return PH_ERR_NOMEM;
+  long blocks = (rows_p * cols_p + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (esz == 2)
+    k_pad2d<uint16_t><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)src, rows, cols, ld, (uint16_t*)dst, rows_p,
+                                                        cols_p);
+  else
+    k_pad2d<float><<<(unsigned)blocks, 256, 0, st>>>((const float*)src, rows, cols, ld, (float*)dst, rows_p, cols_p);
+  PH_LAUNCH_CHECK();
+  out = dst;
+  return PH_OK;
+}
+
+// Zero-padded copies of the operands whose contiguous extent, leading dimension, K or base address
+// miss the MFMA kernels' vector preconditions: the contiguous extent and K round up to `vec`. K is
+// padded in both operands (the zeros add nothing to the products); padded rows of A or columns of B
+// feed only output rows and columns that are never stored.
+int pad_operands(PhGemmDesc& d, int vec, hipStream_t st) {
+  auto up = [vec](long x) { return (x + vec - 1) / vec * vec; };
+  const long K8 = up(d.K);
+  const bool padK = K8 != d.K;
+  const long a_contig = d.trans_a ? d.M : d.K, b_contig = d.trans_b ? d.K : d.N;
+  const bool padA = padK || a_contig % vec || d.lda % vec || ((uintptr_t)d.A % 16);
+  const bool padB = padK || b_contig % vec || d.ldb % vec || ((uintptr_t)d.B % 16);
+  if (padA) {
+    // stored [M][K] (or [K][M] transposed)
+    const long rows = d.trans_a ? d.K : d.M, cols = d.trans_a ? d.M : d.K;
+    const long rows_p = d.trans_a ? K8 : d.M, cols_p = d.trans_a ? up(d.M) : K8;
+    PH_TRY(pad2d(d.a_dtype, d.A, rows, cols, d.lda, kSlotGemmPadA, rows_p, cols_p, d.A, st));
+    d.lda = cols_p;
+  }
+  if (padB) {
+    // stored [K][N] (or [N][K] transposed)
+    const long rows = d.trans_b ? d.N : d.K, cols = d.trans_b ? d.K : d.N;
+    const long rows_p = d.trans_b ? d.N : K8, cols_p = d.trans_b ? K8 : up(d.N);
+    PH_TRY(pad2d(d.b_dtype, d.B, rows, cols, d.ldb, kSlotGemmPadB, rows_p, cols_p, d.B, st));
+    d.ldb = cols_p;
+  }
+  d.K = (int)K8;
+  return PH_OK;
+}
+
 }  // namespace
 
-int gemm(const PhGemmDesc& d, hipStream_t st) {
+int gemm(const PhGemmDesc& d_in, hipStream_t st) {
+  PhGemmDesc d = d_in;
   PH_REQUIRE(d.M >= 0 && d.N >= 0 && d.K >= 0, "gemm: negative extent");
   if (d.M == 0 || d.N == 0) return PH_OK;
   PH_REQUIRE(d.a_dtype == PH_F32 || d.a_dtype == PH_BF16, "gemm: A dtype must be F32 or BF16");
@@ -1153,6 +1211,21 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   PH_REQUIRE(!(d.epi == PH_EPI_BIAS || d.epi == PH_EPI_BIAS_RELU) || d.bias, "gemm: bias missing");
   PH_REQUIRE(d.epi != PH_EPI_RELU_MASK || d.aux, "gemm: mask tensor missing");
 
+  // Vector-load preconditions of the MFMA kernels: every 8 (bf16 math) or 4 (fp32 math) consecutive
+  // elements along each operand's contiguous dimension, and along K, start on a multiple of that
+  // count. Shapes that miss them (a 28-wide observation, a 15-wide head) run on zero-padded copies
+  // of the operands. A call with its own workspace slot (a concurrent update lane) takes the scalar
+  // kernel instead, as the padded copies live in buffers shared by the calls of the default slot.
+  const int vec = d.math == PH_MATH_F32 ? 4 : 8;
+  const long a_contig = d.trans_a ? d.M : d.K, b_contig = d.trans_b ? d.K : d.N;
+  bool aligned = a_contig % vec == 0 && d.lda % vec == 0 && b_contig % vec == 0 && d.ldb % vec == 0 &&
+                 d.K % vec == 0 && ((uintptr_t)d.A % 16) == 0 && ((uintptr_t)d.B % 16) == 0;
+  if (!aligned && d.ws_slot <= 0 && d.K > 0) {
+    // the padded copies' rows (and K) are whole multiples of vec, whatever the logical M and N
+    PH_TRY(pad_operands(d, vec, st));
+    aligned = true;
+  }
+
   GemmArgs g{};
   g.M = d.M; g.N = d.N; g.K = d.K;
   g.A = d.A; g.lda = d.lda; g.B = d.B; g.ldb = d.ldb;
@@ -1162,14 +1235,6 @@ int gemm(const PhGemmDesc& d, hipStream_t st) {
   g.C2 = (uint16_t*)d.C2; g.ldc2 = d.ldc2; g.c2_trans = d.c2_trans;
   g.remap = 1;
 
-  // Vector-load preconditions of the MFMA kernels: every 8 (bf16 math) or 4 (fp32 math) consecutive
-  // elements along each operand's contiguous dimension, and along K, start on a multiple of that
-  // count. Shapes that miss them (e.g. a 4-wide observation layer) take the scalar kernel.
-  const int vec = d.math == PH_MATH_F32 ? 4 : 8;
-  const long a_contig = d.trans_a ? d.M : d.K, b_contig = d.trans_b ? d.K : d.N;
-  const bool aligned = a_contig % vec == 0 && d.lda % vec == 0 && b_contig % vec == 0 &&
-                       d.ldb % vec == 0 && d.K % vec == 0 && ((uintptr_t)d.A % 16) == 0 &&
-                       ((uintptr_t)d.B % 16) == 0;
   if (!aligned) return gemm_scalar(g, d, st);
 
   // Tile choice (measured on the policy shapes). bf16 x bf16 with >= 512 tiles of 256x128: the

@@ -13,6 +13,7 @@ enum : int {
   kSlotPpoPart = 4,
   kSlotPpoCounter = 5,
   kSlotGemmWs = 6,
+  kSlotGemmPadA = 7,  // zero-padded copy of a GEMM's A operand (unaligned shapes)
   kSlotNs = 8,        // Newton-Schulz buffers of the stand-alone entry points
   kSlotNsCtl = 9,     // work-item counters of the fused Newton-Schulz launch (256 bytes)
   kSlotMuonU = 10,    // Nesterov updates of a batched Muon step
@@ -28,6 +29,7 @@ enum : int {
   kSlotMgBufs = 20,
   kSlotHeadsPart = 21,     // multi-discrete / Gaussian heads: dashboard-loss block partials
   kSlotHeadsCounter = 22,  // multi-discrete / Gaussian heads: arrival counter (256 bytes)
+  kSlotGemmPadB = 23,      // zero-padded copy of a GEMM's B operand (unaligned shapes)
   kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
   kSlotHost = 48,     // 48..127: host-buffer entry points
 };

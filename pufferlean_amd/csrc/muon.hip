@@ -219,6 +219,94 @@ __global__ void k_gclip_scale(float* __restrict__ g, long n, const float* __rest
 
 constexpr unsigned kB = 256;
 
+// The whole exact-tier step of one small matrix in one workgroup: X, P and the Gram matrix A live in
+// LDS (2 n + min(rows, cols)^2 doubles), so the Newton-Schulz steps need no launches between them.
+// Every value is computed with the chain's operations in the chain's order (ascending sums, no
+// contraction), so the result is bit-identical to the multi-launch form. The Q = A P (or P A)
+// product is consumed where it is made: the thread computing Q(i, j) updates X(i, j) in place, as
+// that phase reads only A and P. W/nW and M/nM may alias (each element is read and written by one
+// thread).
+constexpr int kExactFusedMaxSteps = 8;
+constexpr long kExactFusedLds = 8192;  // doubles: 64 KB
+struct ExactCoeffs {
+  double v[3 * kExactFusedMaxSteps];
+};
+
+__global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, const double* __restrict__ G,
+                                                           const double* M, double* nW, double* nM, int rows,
+                                                           int cols, double gscale, double mu, double eps,
+                                                           ExactCoeffs cf, int nsteps, double c1, double c2) {
+#pragma clang fp contract(off)
+  extern __shared__ double lds[];
+  const int n = rows * cols, T = blockDim.x, tid = threadIdx.x;
+  const bool wide = rows <= cols;
+  const int mn = wide ? rows : cols;
+  double* X = lds;
+  double* P = lds + n;
+  double* A = lds + 2 * n;
+  __shared__ double inv;
+  // Nesterov: U (kept in X) and the new momentum
+  for (int i = tid; i < n; i += T) {
+    const double gi = G[i] * gscale;
+    const double m = mu * M[i] + gi;
+    nM[i] = m;
+    X[i] = gi + mu * m;
+  }
+  __syncthreads();
+  // Frobenius norm: row sums of squares in ascending column order, then the rows in order
+  for (int r = tid; r < rows; r += T) {
+    double sq = 0.0;
+    for (int j = 0; j < cols; j++) {
+      const double v = X[r * cols + j];
+      sq = sq + v * v;
+    }
+    P[r] = sq;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double sq = 0.0;
+    for (int r = 0; r < rows; r++) sq = sq + P[r];
+    inv = 1.0 / (sqrt(sq) + eps);
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += T) X[i] = inv * X[i];
+  __syncthreads();
+  for (int it = 0; it < nsteps; it++) {
+    const double a = cf.v[3 * it], b = cf.v[3 * it + 1], c = cf.v[3 * it + 2];
+    for (int e = tid; e < mn * mn; e += T) {  // A = X X^T (wide) or X^T X (tall)
+      const int i = e / mn, j = e % mn;
+      double t = 0.0;
+      if (wide)
+        for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * X[j * cols + l];
+      else
+        for (int l = 0; l < rows; l++) t = t + X[l * cols + i] * X[l * cols + j];
+      A[e] = t;
+    }
+    __syncthreads();
+    for (int e = tid; e < n; e += T) {  // P = A X (wide) or X A (tall)
+      const int i = e / cols, j = e % cols;
+      double t = 0.0;
+      if (wide)
+        for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * X[l * cols + j];
+      else
+        for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * A[l * cols + j];
+      P[e] = t;
+    }
+    __syncthreads();
+    for (int e = tid; e < n; e += T) {  // Q = A P (wide) or P A (tall); X = a X + b P + c Q
+      const int i = e / cols, j = e % cols;
+      double t = 0.0;
+      if (wide)
+        for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * P[l * cols + j];
+      else
+        for (int l = 0; l < cols; l++) t = t + P[i * cols + l] * A[l * cols + j];
+      X[e] = a * X[e] + b * P[e] + c * t;
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < n; i += T) nW[i] = c1 * W[i] + c2 * X[i];
+}
+
 }  // namespace
 
 // ---- exact tier host driver: one matrix, device f64 buffers ------------------------------------
@@ -228,6 +316,15 @@ int muon_mat_exact(int rows, int cols, const double* W, const double* G, const d
   const long n = (long)rows * cols;
   if (n == 0) return PH_OK;
   const int mn = rows < cols ? rows : cols;
+  const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
+  if (2 * n + (long)mn * mn <= kExactFusedLds && nsteps <= kExactFusedMaxSteps) {
+    ExactCoeffs cf{};
+    for (int i = 0; i < 3 * nsteps; i++) cf.v[i] = coeffs[i];
+    k_muon_exact_fused<<<1, 1024, (size_t)(2 * n + (long)mn * mn) * 8, st>>>(
+        W, G, M, nW, nM, rows, cols, gscale, mu, eps, cf, nsteps, 1.0 - lr * wd, lr * scale);
+    PH_LAUNCH_CHECK();
+    return PH_OK;
+  }
   double* ws = (double*)scratch(kSlotMuonExact, (size_t)(6 * n + (long)mn * mn + rows + 8) * 8);
   if (!ws) return PH_ERR_NOMEM;
   double *U = ws, *X = U + n, *Xt = X + n, *P = Xt + n, *Q = P + n, *A = Q + n, *rs = A + (long)mn * mn,
@@ -251,7 +348,6 @@ int muon_mat_exact(int rows, int cols, const double* W, const double* G, const d
     }
     k_lincomb3_f64<<<gN, kB, 0, st>>>(X, a, P, b, Q, c, n);
   }
-  const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
   k_finalize_f64<<<gN, kB, 0, st>>>(W, X, nW, 1.0 - lr * wd, lr * scale, n);
   PH_LAUNCH_CHECK();
   return PH_OK;

@@ -343,3 +343,58 @@ def mingru_rollout_step(params, obs, state, out, *, D, H, L_layers, A, precision
     dims = L.MinGRUDims(N, 1, D, H, L_layers, A, precision)
     L.call("ph_mingru_rollout_step", C.byref(dims), _p(params), _p(obs), _p(state), _p(out), _stream())
     return out
+
+
+# ---- multi-discrete and Gaussian heads -------------------------------------------------------------
+def _sizes(head_sizes):
+    return (C.c_int * len(head_sizes))(*[int(s) for s in head_sizes])
+
+
+def ppo_grad_md(out, act, adv, ret, old, ov=None, *, head_sizes, vf_coef=0.5, ent_coef=0.01, clip_eps=0.2,
+                vf_clip=0.0, dout=None, newlp=None, newval=None, losses=None):
+    """Loss gradient of K categorical heads: out [N, sum(sizes)+1] fp32 (heads' logits, then the value),
+    act int32 [N, K]; adv/ret/old (and ov) fp32 [N]. Returns dout [N, sum(sizes)+1]."""
+    _dev(out, act, adv, ret, old)
+    N = out.shape[0]
+    if act.dtype != torch.int32 or out.dtype != torch.float32:
+        raise TypeError("out must be float32 and act int32")
+    dout = dout if dout is not None else torch.empty_like(out)
+    L.call("ph_ppo_grad_md", _p(out), out.stride(0), _p(act), _p(adv), _p(ret), _p(old), _p(ov), N,
+           _sizes(head_sizes), len(head_sizes), vf_coef, ent_coef, clip_eps, vf_clip, _p(dout), dout.stride(0),
+           _p(newlp), _p(newval), _p(losses), _stream())
+    return dout
+
+
+def ppo_grad_cont(out, act, adv, ret, old, ov=None, *, dim, vf_coef=0.5, ent_coef=0.01, clip_eps=0.2, vf_clip=0.0,
+                  ls_lo=-20.0, ls_hi=2.0, dout=None, newlp=None, newval=None, losses=None):
+    """Loss gradient of a d-dim diagonal Gaussian: out [N, 2d+1] fp32 (means, raw log-stds, value),
+    act fp32 [N, d]. Returns dout [N, 2d+1]."""
+    _dev(out, act, adv, ret, old)
+    N = out.shape[0]
+    dout = dout if dout is not None else torch.empty_like(out)
+    L.call("ph_ppo_grad_cont", _p(out), out.stride(0), _p(act), _p(adv), _p(ret), _p(old), _p(ov), N, dim, vf_coef,
+           ent_coef, clip_eps, vf_clip, ls_lo, ls_hi, _p(dout), dout.stride(0), _p(newlp), _p(newval), _p(losses),
+           _stream())
+    return dout
+
+
+def sample_actions_md(logits, head_sizes, *, rng_state, out=None):
+    """Draw every head of every row of logits [N, sum(sizes)+1] (float32/float64). Returns f64
+    [(K+2) * N]: actions (head h at h*N + n), joint log-prob, value."""
+    _dev(logits)
+    N, K = logits.shape[0], len(head_sizes)
+    out = out if out is not None else torch.empty((K + 2) * N, device=logits.device, dtype=torch.float64)
+    L.call("ph_sample_actions_md", _DT[logits.dtype], _p(logits), logits.stride(0), N, _sizes(head_sizes), K,
+           rng_state & 0xFFFFFFFFFFFFFFFF, _p(out), _stream())
+    return out
+
+
+def sample_actions_cont(y, dim, *, rng_state, ls_lo=-20.0, ls_hi=2.0, out=None):
+    """Gaussian draw per row of y [N, 2d+1] (float32/float64). Returns f64 [(d+2) * N]: actions (dim i
+    at i*N + n), log-prob, value."""
+    _dev(y)
+    N = y.shape[0]
+    out = out if out is not None else torch.empty((dim + 2) * N, device=y.device, dtype=torch.float64)
+    L.call("ph_sample_actions_cont", _DT[y.dtype], _p(y), y.stride(0), N, dim, rng_state & 0xFFFFFFFFFFFFFFFF,
+           ls_lo, ls_hi, _p(out), _stream())
+    return out

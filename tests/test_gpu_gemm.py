@@ -114,13 +114,47 @@ def test_gemm_epilogues(gpu):
 
 
 @pytest.mark.parametrize("M,N,K", [(65536, 128, 4), (65536, 3, 128), (128, 4, 16384), (3, 128, 16384)])
-def test_gemm_small_dims_scalar_path(gpu, M, N, K):
-    # the CartPole policy's 4-wide input layer and 3-wide head take the scalar kernel
+def test_gemm_small_dims_padded_path(gpu, M, N, K):
+    # the CartPole policy's 4-wide input layer and 3-wide head: operands staged zero-padded
     for ta, tb in FORMS:
         a, b = operands(M, N, K, ta, tb, 13 + ta * 2 + tb)
         ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
         c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), math="f32").cpu().numpy()
         assert rel(c, oracle(a, b, ta, tb, M, N, K)) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(32768, 128, 28), (32768, 28, 128), (128, 28, 32768), (32768, 15, 128),
+                                   (15, 128, 32768), (32768, 128, 15), (300, 9, 21), (9, 300, 4097)])
+@pytest.mark.parametrize("math_", ["bf16", "f32"])
+def test_gemm_unaligned_env_shapes(gpu, M, N, K, math_):
+    """The target/drone MLP products (obs 28 / 21, heads 15 / 9 wide): zero-padded staging, all forms."""
+    print(f"gemm unaligned M={M} N={N} K={K} {math_}", flush=True)
+    for ta, tb in FORMS:
+        a, b = operands(M, N, K, ta, tb, 17 + M + N + K + 2 * ta + tb)
+        ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        c = D.gemm(ga, gb, trans_a=bool(ta), trans_b=bool(tb), math=math_).cpu().numpy()
+        if math_ == "f32":
+            assert rel(c, oracle(a, b, ta, tb, M, N, K)) < 1e-5, (ta, tb)
+        else:
+            assert rel(c, oracle(bf16_round(a), bf16_round(b), ta, tb, M, N, K)) < 1e-5, (ta, tb)
+
+
+def test_gemm_unaligned_strided_bf16_storage_and_epilogue(gpu):
+    """Unaligned leading dimensions (column views of wider rows), bf16-stored operands and the bias
+    epilogue through the padded staging."""
+    M, N, K = 4000, 15, 28
+    a = rng.normal(21, M * 31).reshape(M, 31).astype(np.float32)
+    b = (rng.normal(22, N * 29).reshape(N, 29) / np.sqrt(K)).astype(np.float32)
+    ga = torch.from_numpy(a).cuda()[:, 1:1 + K]     # lda 31, base offset by one element
+    gb = torch.from_numpy(b).cuda()[:, :K]          # ldb 29
+    bias = torch.from_numpy(rng.normal(23, N).astype(np.float32)).cuda()
+    ref = oracle(np.ascontiguousarray(a[:, 1:1 + K]), np.ascontiguousarray(b[:, :K]), 0, 1, M, N, K)
+    c = D.gemm(ga, gb, trans_b=True, math="f32", epilogue=L.PH_EPI_BIAS, bias=bias).cpu().numpy()
+    assert rel(c, ref + bias.cpu().numpy()) < 1e-5
+    abf, bbf = ga.to(torch.bfloat16), gb.to(torch.bfloat16)  # contiguous bf16 copies, K = 28
+    c = D.gemm(abf, bbf, trans_b=True, math="bf16").cpu().numpy()
+    ref_r = oracle(abf.float().cpu().numpy(), bbf.float().cpu().numpy(), 0, 1, M, N, K)
+    assert rel(c, ref_r) < 1e-5
 
 
 def _bf(x):

@@ -19,7 +19,10 @@ def rel(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
 
 
-@pytest.mark.parametrize("shape", [(16, 24), (24, 16), (20, 20), (128, 128), (6, 128)])
+# (128, 28), (15, 128), (48, 48) ... run in one workgroup (2 n + min^2 <= 8192 doubles of LDS);
+# (128, 128), (64, 64), (90, 40) run as the launch chain
+@pytest.mark.parametrize("shape", [(16, 24), (24, 16), (20, 20), (128, 128), (6, 128), (128, 28), (28, 128),
+                                   (15, 128), (128, 15), (48, 48), (64, 64), (90, 40), (1, 1)])
 def test_exact_tier_bit_exact(gpu, shape):
     # verify-muon-gpu draw order: per element w U[-.5,.5), g U[-.3,.3), m U[-.2,.2) (Exe/Puffer.lean:1134-1138)
     rows, cols = shape
