@@ -276,30 +276,33 @@ __global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, cons
     for (int e = tid; e < mn * mn; e += T) {  // A = X X^T (wide) or X^T X (tall)
       const int i = e / mn, j = e % mn;
       double t = 0.0;
-      if (wide)
+      if (wide) {
         for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * X[j * cols + l];
-      else
+      } else {
         for (int l = 0; l < rows; l++) t = t + X[l * cols + i] * X[l * cols + j];
+      }
       A[e] = t;
     }
     __syncthreads();
     for (int e = tid; e < n; e += T) {  // P = A X (wide) or X A (tall)
       const int i = e / cols, j = e % cols;
       double t = 0.0;
-      if (wide)
+      if (wide) {
         for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * X[l * cols + j];
-      else
+      } else {
         for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * A[l * cols + j];
+      }
       P[e] = t;
     }
     __syncthreads();
     for (int e = tid; e < n; e += T) {  // Q = A P (wide) or P A (tall); X = a X + b P + c Q
       const int i = e / cols, j = e % cols;
       double t = 0.0;
-      if (wide)
+      if (wide) {
         for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * P[l * cols + j];
-      else
+      } else {
         for (int l = 0; l < cols; l++) t = t + P[i * cols + l] * A[l * cols + j];
+      }
       X[e] = a * X[e] + b * P[e] + c * t;
     }
     __syncthreads();

@@ -123,19 +123,25 @@ __global__ void __launch_bounds__(256) k_colsum_part(const T* __restrict__ X, lo
   }
 }
 
+// out[c] (+)= scale * sum of the G partials of column c: 16 lanes per column each add every 16th
+// partial in order, then a fixed tree combines the 16 lane sums.
 __global__ void __launch_bounds__(256) k_colsum_finish(const float* __restrict__ part, int G, int J,
                                                        float* __restrict__ out, float scale,
                                                        int accumulate) {
-  __shared__ float sh[4][64];
-  const int lc = threadIdx.x & 63, ln = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lc;
+  __shared__ float sh[16][17];
+  const int lc = threadIdx.x & 15, ln = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + lc;
   float s = 0.f;
   if (c < J)
-    for (int g = ln; g < G; g += 4) s += part[(long)g * J + c];
+    for (int g = ln; g < G; g += 16) s += part[(long)g * J + c];
   sh[ln][lc] = s;
   __syncthreads();
+  for (int w = 8; w > 0; w >>= 1) {
+    if (ln < w) sh[ln][lc] += sh[ln + w][lc];
+    __syncthreads();
+  }
   if (ln == 0 && c < J) {
-    const float t = (((sh[0][lc] + sh[1][lc]) + sh[2][lc]) + sh[3][lc]) * scale;
+    const float t = sh[0][lc] * scale;
     out[c] = accumulate ? out[c] + t : t;
   }
 }
@@ -150,19 +156,19 @@ int colsum_t(const T* X, long N, int J, long ld, float* out, float scale, int ac
   int ct = 64;
   while (ct > 1 && ct / 2 >= groups) ct /= 2;   // narrow matrices: more row lanes per block
   const unsigned gx = (unsigned)((groups + ct - 1) / ct);
-  long rows_per = 2048;
-  long G = (N + rows_per - 1) / rows_per;
-  if (G > 1024 / (long)gx) {
-    G = 1024 / (long)gx > 0 ? 1024 / (long)gx : 1;
-    rows_per = (N + G - 1) / G;
-  }
+  // row slices of >= 128 rows, as many as keep the grid within about 1024 workgroups (a minibatch of
+  // 32768 rows then spreads over 256 workgroups instead of 16); the slicing depends only on N and J
+  long G = (N + 127) / 128;
+  const long gmax = 1024 / (long)gx > 0 ? 1024 / (long)gx : 1;
+  if (G > gmax) G = gmax;
   if (G < 1) G = 1;
+  const long rows_per = (N + G - 1) / G;
   float* part = (float*)scratch(kSlotColsumPart, (size_t)G * J * 4);
   if (!part) return PH_ERR_NOMEM;
   dim3 grid(gx, (unsigned)G);
   if (vec) k_colsum_part<T, 4><<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, ct, part);
   else k_colsum_part<T, 1><<<grid, 256, 0, st>>>(X, N, J, ld, rows_per, ct, part);
-  k_colsum_finish<<<ceil_div(J, 64), 256, 0, st>>>(part, (int)G, J, out, scale, accumulate);
+  k_colsum_finish<<<ceil_div(J, 16), 256, 0, st>>>(part, (int)G, J, out, scale, accumulate);
   PH_LAUNCH_CHECK();
   return PH_OK;
 }
