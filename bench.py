@@ -395,11 +395,16 @@ def bench_heads(steps, warmup):
         else:
             fn = lambda: D.ppo_grad_cont(y, act, adv, ret, old, ov, dim=CT_DIM, vf_clip=0.2, dout=dout, losses=losses)
         us = time_graph(fn, steps, warmup) * 1e3
+        if name == "md_grad":
+            fn0 = lambda: D.ppo_grad_md(y, act, adv, ret, old, ov, head_sizes=MD_HEADS, vf_clip=0.2, dout=dout)
+        else:
+            fn0 = lambda: D.ppo_grad_cont(y, act, adv, ret, old, ov, dim=CT_DIM, vf_clip=0.2, dout=dout)
+        us0 = time_graph(fn0, steps, warmup) * 1e3
         # per row: the O head outputs read and their O gradients written, Wd actions, adv/ret/old/ov
         nbytes = N * (2 * O * 4 + Wd * 4 + 4 * 4)
         gbs = nbytes / (us * 1e-6) / 1e9
-        out[name] = {"rows": N, "us": round(us, 2), "bytes": nbytes, "gbs": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        out[name] = {"rows": N, "us": round(us, 2), "us_no_losses": round(us0, 2), "bytes": nbytes,
+                     "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     # samplers over one rollout step of the env's agents
     Ym = _t(rng.normal(rng.seed_for(8, 20), MD_AGENTS * (sum(MD_HEADS) + 1))).view(MD_AGENTS, -1)
     om = torch.empty((K + 2) * MD_AGENTS, device="cuda", dtype=torch.float64)

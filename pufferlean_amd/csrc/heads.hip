@@ -46,7 +46,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md(const float* __restrict__ o
                                                      float vf, float ent, float clip, float vfClip,
                                                      float* __restrict__ dout, long ldd, float* __restrict__ newlp,
                                                      float* __restrict__ newval, double* __restrict__ part,
-                                                     unsigned* counter, double* __restrict__ losses) {
+                                                     double* __restrict__ losses) {
   const long n = (long)blockIdx.x * blockDim.x + threadIdx.x;
   double lsum[6] = {0, 0, 0, 0, 0, 0};
   if (n < N) {
@@ -96,8 +96,192 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md(const float* __restrict__ o
     if (newval) newval[n] = o[W];
     if (losses) row_losses(joint, old[n], A, o[W], ret[n], vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
   }
-  if (!losses) return;
-  fold_losses(lsum, part, counter, losses, N, vf, ent);
+  if (losses) block_losses(lsum, part);
+}
+
+// ---- LDS-staged forms for rows up to kTileW wide ---------------------------------------------------
+// A workgroup's 256 rows of head outputs arrive through LDS with coalesced loads (columns past the
+// row width, if the stride has any, are skipped), each lane then holds its row in
+// registers, and the gradient rows leave through the same tile with coalesced stores. The pitch is
+// odd, so the lanes reading one column of their rows hit distinct banks. Head boundaries are the
+// same for every lane, so the per-head loops below branch uniformly.
+constexpr int kTileW = 32;
+constexpr int kTileP = 33;
+
+// Lane t walks the (row, column) pairs t, t + 256, ... of the R x O block in row-major order; the
+// pair advances by 256 / O rows and 256 % O columns with a carry, so no division runs per element.
+__device__ __forceinline__ void tile_load(const float* __restrict__ src, long ld, int O, long n0, int R,
+                                          float* __restrict__ tile) {
+  const int q = (int)blockDim.x / O, rm = (int)blockDim.x % O;
+  int r = (int)threadIdx.x / O, c = (int)threadIdx.x % O;
+  const float* s = src + n0 * ld;
+  while (r < R) {
+    tile[r * kTileP + c] = s[(long)r * ld + c];
+    r += q;
+    c += rm;
+    if (c >= O) {
+      c -= O;
+      r++;
+    }
+  }
+}
+__device__ __forceinline__ void tile_store(float* __restrict__ dst, long ld, int O, long n0, int R,
+                                           const float* __restrict__ tile) {
+  const int q = (int)blockDim.x / O, rm = (int)blockDim.x % O;
+  int r = (int)threadIdx.x / O, c = (int)threadIdx.x % O;
+  float* d = dst + n0 * ld;
+  while (r < R) {
+    d[(long)r * ld + c] = tile[r * kTileP + c];
+    r += q;
+    c += rm;
+    if (c >= O) {
+      c -= O;
+      r++;
+    }
+  }
+}
+
+// k_ppo_grad_md for W + 1 <= kTileW: each probability is computed once and kept with its head's
+// expected logit for the gradient pass.
+__global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restrict__ out, long ldo,
+                                                          const int* __restrict__ act, const float* __restrict__ adv,
+                                                          const float* __restrict__ ret, const float* __restrict__ old,
+                                                          const float* __restrict__ ov, long N, HeadSizes hs, int W,
+                                                          float vf, float ent, float clip, float vfClip,
+                                                          float* __restrict__ dout, long ldd, float* __restrict__ newlp,
+                                                          float* __restrict__ newval, double* __restrict__ part,
+                                                          double* __restrict__ losses) {
+  __shared__ float tile[256 * kTileP];
+  const long n0 = (long)blockIdx.x * 256;
+  const int R = (int)(N - n0 < 256 ? N - n0 : 256);
+  const int t = threadIdx.x, O = W + 1;
+  tile_load(out, ldo, O, n0, R, tile);
+  __syncthreads();
+  double lsum[6] = {0, 0, 0, 0, 0, 0};
+  if (t < R) {
+    const long n = n0 + t;
+    float x[kTileW], p[kTileW], pout[kTileW];
+#pragma unroll
+    for (int k = 0; k < kTileW; k++) x[k] = k < O ? tile[t * kTileP + k] : 0.f;
+    const int* a = act + n * hs.K;
+    float joint = 0.f, entropy = 0.f;
+    unsigned hit = 0u;
+    bool inRange = true;
+    int off = 0;
+    for (int h = 0; h < hs.K; h++) {
+      const int end = off + hs.n[h], ah = a[h];
+      float m = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < kTileW; k++)
+        if (k >= off && k < end) m = fmaxf(m, x[k]);
+      float se = 0.f;
+#pragma unroll
+      for (int k = 0; k < kTileW; k++)
+        if (k >= off && k < end) se += expf(x[k] - m);
+      const float lse = m + logf(se);
+      float po = 0.f, xa = 0.f;
+#pragma unroll
+      for (int k = 0; k < kTileW; k++)
+        if (k >= off && k < end) {
+          p[k] = expf(x[k] - lse);
+          po += p[k] * x[k];
+          entropy -= p[k] * (x[k] - lse);
+          if (k == off + ah) xa = x[k];
+        }
+#pragma unroll
+      for (int k = 0; k < kTileW; k++)
+        if (k >= off && k < end) pout[k] = po;
+      if (ah >= 0 && ah < end - off) {
+        joint += xa - lse;
+        hit |= 1u << (off + ah);
+      } else {
+        inRange = false;
+      }
+      off = end;
+    }
+    if (!inRange) joint = __builtin_nanf("");
+    const float ratio = expf(joint - old[n]), lo = 1.f - clip, hi = 1.f + clip;
+    const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+    const float A = adv[n];
+    const float dPol = !inRange ? __builtin_nanf("")
+                     : (A * ratio <= A * rc) ? A * ratio : ((lo < ratio && ratio < hi) ? A * ratio : 0.f);
+#pragma unroll
+    for (int k = 0; k < kTileW; k++)
+      if (k < W)
+        tile[t * kTileP + k] = dPol * ((float)((hit >> k) & 1u) - p[k]) + ent * p[k] * (pout[k] - x[k]);
+    float vnew = 0.f;
+#pragma unroll
+    for (int k = 0; k < kTileW; k++)
+      if (k == W) vnew = x[k];
+    const float vold = ov ? ov[n] : 0.f;
+    tile[t * kTileP + W] = -vf * vloss_grad(vnew, ret[n], vold, ov != nullptr, vfClip);
+    if (newlp) newlp[n] = joint;
+    if (newval) newval[n] = vnew;
+    if (losses) row_losses(joint, old[n], A, vnew, ret[n], vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
+  }
+  __syncthreads();
+  tile_store(dout, ldd, O, n0, R, tile);
+  if (losses) block_losses(lsum, part);
+}
+
+// k_ppo_grad_cont for 2d + 1 <= kTileW.
+__global__ void __launch_bounds__(256) k_ppo_grad_cont_tile(const float* __restrict__ out, long ldo,
+                                                            const float* __restrict__ act, const float* __restrict__ adv,
+                                                            const float* __restrict__ ret, const float* __restrict__ old,
+                                                            const float* __restrict__ ov, long N, int d, float vf,
+                                                            float ent, float clip, float vfClip, float lslo, float lshi,
+                                                            float* __restrict__ dout, long ldd,
+                                                            float* __restrict__ newlp, float* __restrict__ newval,
+                                                            double* __restrict__ part,
+                                                            double* __restrict__ losses) {
+  __shared__ float tile[256 * kTileP];
+  const long n0 = (long)blockIdx.x * 256;
+  const int R = (int)(N - n0 < 256 ? N - n0 : 256);
+  const int t = threadIdx.x, W = 2 * d, O = W + 1;
+  tile_load(out, ldo, O, n0, R, tile);
+  __syncthreads();
+  double lsum[6] = {0, 0, 0, 0, 0, 0};
+  if (t < R) {
+    const long n = n0 + t;
+    constexpr int DM = kTileW / 2;
+    float mu[DM], lsr[DM], z[DM];
+#pragma unroll
+    for (int i = 0; i < DM; i++) {
+      mu[i] = i < d ? tile[t * kTileP + i] : 0.f;
+      lsr[i] = i < d ? tile[t * kTileP + d + i] : 0.f;
+    }
+    const float vnew = tile[t * kTileP + W];
+    const float* a = act + n * d;
+    const float hl = (float)kHalfLog2Pi;
+    float logp = 0.f, entropy = 0.f;
+#pragma unroll
+    for (int i = 0; i < DM; i++)
+      if (i < d) {
+        const float ls = lsr[i] < lslo ? lslo : (lsr[i] > lshi ? lshi : lsr[i]);
+        z[i] = (a[i] - mu[i]) * expf(-ls);
+        logp += -0.5f * z[i] * z[i] - ls - hl;
+        entropy += ls + (0.5f + hl);
+      }
+    const float ratio = expf(logp - old[n]), lo = 1.f - clip, hi = 1.f + clip;
+    const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+    const float A = adv[n];
+    const float dPol = (A * ratio <= A * rc) ? A * ratio : ((lo < ratio && ratio < hi) ? A * ratio : 0.f);
+#pragma unroll
+    for (int i = 0; i < DM; i++)
+      if (i < d) {
+        const float ls = lsr[i] < lslo ? lslo : (lsr[i] > lshi ? lshi : lsr[i]);
+        tile[t * kTileP + i] = dPol * z[i] * expf(-ls);
+        tile[t * kTileP + d + i] = (lslo < lsr[i] && lsr[i] < lshi) ? dPol * (z[i] * z[i] - 1.f) + ent : 0.f;
+      }
+    const float vold = ov ? ov[n] : 0.f;
+    tile[t * kTileP + W] = -vf * vloss_grad(vnew, ret[n], vold, ov != nullptr, vfClip);
+    if (newlp) newlp[n] = logp;
+    if (newval) newval[n] = vnew;
+    if (losses) row_losses(logp, old[n], A, vnew, ret[n], vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
+  }
+  __syncthreads();
+  tile_store(dout, ldd, O, n0, R, tile);
+  if (losses) block_losses(lsum, part);
 }
 
 // Draws per head: word of rng + (n+1) GOLD + (h+1) GOLD2; out = [actions (head h at h*N + n); joint
@@ -148,7 +332,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_cont(const float* __restrict__
                                                        float clip, float vfClip, float lslo, float lshi,
                                                        float* __restrict__ dout, long ldd, float* __restrict__ newlp,
                                                        float* __restrict__ newval, double* __restrict__ part,
-                                                       unsigned* counter, double* __restrict__ losses) {
+                                                       double* __restrict__ losses) {
   const long n = (long)blockIdx.x * blockDim.x + threadIdx.x;
   double lsum[6] = {0, 0, 0, 0, 0, 0};
   if (n < N) {
@@ -180,8 +364,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_cont(const float* __restrict__
     if (newval) newval[n] = o[W];
     if (losses) row_losses(logp, old[n], A, o[W], ret[n], vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
   }
-  if (!losses) return;
-  fold_losses(lsum, part, counter, losses, N, vf, ent);
+  if (losses) block_losses(lsum, part);
 }
 
 // Box-Muller per dim from two words, rng + (n+1) GOLD + (2i+1) GOLD2 and (2i+2) GOLD2 (u1 floored at
@@ -224,15 +407,19 @@ int head_sizes(const int* sizes, size_t K, HeadSizes& hs, int& W, const char* wh
 
 }  // namespace
 
-// Scratch for the dashboard-loss fold of a grid of `grid` blocks (none without losses).
-static int loss_scratch(double* losses, unsigned grid, double*& part, unsigned*& counter, hipStream_t st) {
+// Block partials of the dashboard losses for a grid of `grid` blocks (none without losses), and their
+// fold after the kernel.
+static int loss_part(double* losses, unsigned grid, double*& part) {
   part = nullptr;
-  counter = nullptr;
   if (!losses) return PH_OK;
   part = (double*)scratch(kSlotHeadsPart, (size_t)grid * 6 * 8);
-  counter = (unsigned*)scratch(kSlotHeadsCounter, 256);
-  if (!part || !counter) return PH_ERR_NOMEM;
-  return ensure_zeroed_counter(counter, st);
+  return part ? PH_OK : PH_ERR_NOMEM;
+}
+static int loss_fold(double* losses, const double* part, unsigned grid, size_t N, float vf, float ent, hipStream_t st) {
+  if (!losses) return PH_OK;
+  k_fold_losses<<<1, 256, 0, st>>>(part, (int)grid, (long)N, vf, ent, losses);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
 }
 
 int ppo_grad_md(const float* out, size_t ldo, const int* act, const float* adv, const float* ret, const float* old,
@@ -245,12 +432,15 @@ int ppo_grad_md(const float* out, size_t ldo, const int* act, const float* adv, 
   if (N == 0) return PH_OK;
   const unsigned grid = ceil_div(N, 256);
   double* part;
-  unsigned* counter;
-  PH_TRY(loss_scratch(losses, grid, part, counter, st));
-  k_ppo_grad_md<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, hs, W, vf, ent, clip, vfClip,
-                                      dout, (long)ldd, newlp, newval, part, counter, losses);
+  PH_TRY(loss_part(losses, grid, part));
+  if (W + 1 <= kTileW)
+    k_ppo_grad_md_tile<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, hs, W, vf, ent, clip,
+                                             vfClip, dout, (long)ldd, newlp, newval, part, losses);
+  else
+    k_ppo_grad_md<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, hs, W, vf, ent, clip, vfClip,
+                                        dout, (long)ldd, newlp, newval, part, losses);
   PH_LAUNCH_CHECK();
-  return PH_OK;
+  return loss_fold(losses, part, grid, N, vf, ent, st);
 }
 
 int ppo_grad_cont(const float* out, size_t ldo, const float* act, const float* adv, const float* ret,
@@ -261,12 +451,15 @@ int ppo_grad_cont(const float* out, size_t ldo, const float* act, const float* a
   if (N == 0) return PH_OK;
   const unsigned grid = ceil_div(N, 256);
   double* part;
-  unsigned* counter;
-  PH_TRY(loss_scratch(losses, grid, part, counter, st));
-  k_ppo_grad_cont<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, (int)d, vf, ent, clip, vfClip,
-                                        lslo, lshi, dout, (long)ldd, newlp, newval, part, counter, losses);
+  PH_TRY(loss_part(losses, grid, part));
+  if (2 * d + 1 <= (size_t)kTileW)
+    k_ppo_grad_cont_tile<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, (int)d, vf, ent, clip,
+                                               vfClip, lslo, lshi, dout, (long)ldd, newlp, newval, part, losses);
+  else
+    k_ppo_grad_cont<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, (int)d, vf, ent, clip,
+                                          vfClip, lslo, lshi, dout, (long)ldd, newlp, newval, part, losses);
   PH_LAUNCH_CHECK();
-  return PH_OK;
+  return loss_fold(losses, part, grid, N, vf, ent, st);
 }
 
 int sample_actions_md(int dtype, const void* Y, size_t ldy, size_t N, const int* sizes, size_t K, uint64_t rng,

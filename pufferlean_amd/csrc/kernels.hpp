@@ -7,11 +7,9 @@ namespace ph {
 // Scratch slot ids (runtime.hip owns the table).
 enum : int {
   kSlotMomentsPart = 0,
-  kSlotMomentsCounter = 1,
   kSlotMomentsStats = 2,
   kSlotColsumPart = 3,
   kSlotPpoPart = 4,
-  kSlotPpoCounter = 5,
   kSlotGemmWs = 6,
   kSlotGemmPadA = 7,  // zero-padded copy of a GEMM's A operand (unaligned shapes)
   kSlotNs = 8,        // Newton-Schulz buffers of the stand-alone entry points
@@ -19,7 +17,6 @@ enum : int {
   kSlotMuonU = 10,    // Nesterov updates of a batched Muon step
   kSlotPrio = 11,     // prioritised sampler: probabilities and (large N) the cumulative table
   kSlotReplayPart = 12,    // minibatch gather: per-block (count, mean, M2)
-  kSlotReplayCtr = 13,     // minibatch gather: arrival counter (256 bytes)
   kSlotReplayStats = 14,   // minibatch gather: [mean, std] when the caller passes none
   kSlotReplayLastw = 15,   // iterate: last-writer table, N ints, zero between calls
   kSlotMuonExact = 16,
@@ -28,7 +25,6 @@ enum : int {
   kSlotRollout = 19,  // rollout step: layer inputs, layer products, padded head
   kSlotMgBufs = 20,
   kSlotHeadsPart = 21,     // multi-discrete / Gaussian heads: dashboard-loss block partials
-  kSlotHeadsCounter = 22,  // multi-discrete / Gaussian heads: arrival counter (256 bytes)
   kSlotGemmPadB = 23,      // zero-padded copy of a GEMM's B operand (unaligned shapes)
   kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
   kSlotHost = 48,     // 48..127: host-buffer entry points
@@ -48,9 +44,8 @@ hipStream_t lane_stream(int lane);
 int fork_lanes(hipStream_t main, int n);  // lanes 0..n-1 wait for work queued so far on main
 int join_lanes(hipStream_t main, int n);  // main waits for everything queued on lanes 0..n-1
 
-// Zero a 256-byte arrival-counter block once per pointer (fill kernel, no memset node).
-int ensure_zeroed_counter(unsigned* counter, hipStream_t st);
-// The same for a block of n words (a fixed-size scratch slot: its pointer never changes).
+// Zero a block of n words once per pointer (fill kernel, no memset node; for a fixed-size scratch
+// slot, whose pointer never changes).
 int ensure_zeroed_words(unsigned* words, int n, hipStream_t st);
 
 struct PhGemmDesc {

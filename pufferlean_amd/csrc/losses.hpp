@@ -1,7 +1,7 @@
 // The 7 dashboard losses of the PPO objective, [pg, v, ent, total, old_kl, kl, clipfrac] as means over
 // the rows (PufferLib's decomposition, puffercuda.cu:1798-1870 for every head kind), reduced
-// deterministically: six f64 sums per row, a fixed tree per block, per-block partials, and the last
-// block to finish folding the partials in block order.
+// deterministically: six f64 sums per row, fixed-order wavefront butterflies per block, per-block
+// partials, and a one-block kernel folding the partials in block order.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -34,56 +34,67 @@ __device__ inline void row_losses(float logp, float old, float adv, float vnew, 
   lsum[5] = (r < dlo || r > dhi) ? 1.0 : 0.0;
 }
 
-// Every thread of a 256-thread block calls this once with its row's sums (zeros for rows past N).
-// part holds 6 doubles per block; counter starts at 0 and is left at 0.
-__device__ inline void fold_losses(const double lsum[6], double* __restrict__ part, unsigned* counter,
-                                   double* __restrict__ losses, long N, float vfCoef, float entCoef) {
-  __shared__ double sh[6][256];
-  __shared__ bool last;
+// Sum over the 64 lanes of a wavefront by an xor butterfly: each step adds the partner's partial, so
+// both partners hold the same value and, after six steps, every lane holds the same total, formed in
+// the same order on every run.
+__device__ inline double wave_sum(double v) {
 #pragma unroll
-  for (int q = 0; q < 6; q++) sh[q][threadIdx.x] = lsum[q];
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Every thread of a 256-thread block calls this once with its row's sums (zeros for rows past N):
+// the block's six sums go to part[6 * blockIdx.x ..]. k_fold_losses, launched after the kernel on
+// the same stream, folds the blocks. (A last-block fold inside the kernel needs a device-scope
+// release per block, which on this part writes back the XCD's L2 mid-kernel; the launch boundary
+// orders the partials at no such cost.)
+__device__ inline void block_losses(const double lsum[6], double* __restrict__ part) {
+  __shared__ double sh[6][4];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double v[6];
+#pragma unroll
+  for (int q = 0; q < 6; q++) v[q] = wave_sum(lsum[q]);
+  if (lane == 0)
+#pragma unroll
+    for (int q = 0; q < 6; q++) sh[q][w] = v[q];
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s)
-#pragma unroll
-      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
-    __syncthreads();
+  if (threadIdx.x < 6) {
+    const int q = threadIdx.x;
+    part[(size_t)blockIdx.x * 6 + q] = ((sh[q][0] + sh[q][1]) + sh[q][2]) + sh[q][3];
   }
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int q = 0; q < 6; q++) part[(size_t)blockIdx.x * 6 + q] = sh[q][0];
-    __threadfence();
-    last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // thread t adds blocks t, t+256, ... in sequence; the same tree then combines the 256 thread sums
+}
+
+// One 256-thread block: thread t adds blocks t, t + 256, ... in sequence, the wavefront butterflies
+// and the wavefront order combine them, and the means over N rows form the 7 losses. (Internal
+// linkage: each source file that launches it has its own copy.)
+static __global__ void __launch_bounds__(256) k_fold_losses(const double* __restrict__ part, int G, long N, float vfCoef,
+                                                     float entCoef, double* __restrict__ losses) {
+  __shared__ double sh[6][4];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double v[6];
 #pragma unroll
   for (int q = 0; q < 6; q++) {
-    double s = 0.0;
-    for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x)
-      s += __hip_atomic_load(&part[(size_t)b * 6 + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh[q][threadIdx.x] = s;
+    double acc = 0.0;
+    for (int b = threadIdx.x; b < G; b += blockDim.x) acc += part[(size_t)b * 6 + q];
+    v[q] = wave_sum(acc);
   }
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s)
+  if (lane == 0)
 #pragma unroll
-      for (int q = 0; q < 6; q++) sh[q][threadIdx.x] += sh[q][threadIdx.x + s];
-    __syncthreads();
-  }
+    for (int q = 0; q < 6; q++) sh[q][w] = v[q];
+  __syncthreads();
   if (threadIdx.x == 0) {
+    double tot[6];
+#pragma unroll
+    for (int q = 0; q < 6; q++) tot[q] = ((sh[q][0] + sh[q][1]) + sh[q][2]) + sh[q][3];
     const double dn = (double)(N > 0 ? N : 1);
-    const double pg = sh[0][0] / dn, vl = sh[1][0] / dn, en = sh[2][0] / dn;
+    const double pg = tot[0] / dn, vl = tot[1] / dn, en = tot[2] / dn;
     losses[0] = pg;
     losses[1] = vl;
     losses[2] = en;
     losses[3] = pg + (double)vfCoef * vl - (double)entCoef * en;
-    losses[4] = sh[3][0] / dn;
-    losses[5] = sh[4][0] / dn;
-    losses[6] = sh[5][0] / dn;
-    *counter = 0u;
+    losses[4] = tot[3] / dn;
+    losses[5] = tot[4] / dn;
+    losses[6] = tot[5] / dn;
   }
 }
 

@@ -4,7 +4,7 @@
 // importance ratio against the behaviour log-prob, the clipped-surrogate subgradient, the entropy
 // gradient, and PufferLib's clipped value-loss gradient; ascent sign (puffercuda.cu:692-744,
 // 4910-4930; pufferblas.c:726-736). Optionally the 7 dashboard losses are reduced deterministically
-// (per-block partials in f64, the last block folds them in block order).
+// (per-block partials in f64, folded in block order by a one-block kernel).
 #include "common.hpp"
 #include "kernels.hpp"
 #include "losses.hpp"
@@ -23,7 +23,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
     const float* __restrict__ old, const float* __restrict__ ov, int N, int A, float vfCoef,
     float entCoef, float clipEps, float vfClip, int max_shift, float* __restrict__ dlogits, int ldd,
     float* __restrict__ dvalues, int lddv, float* __restrict__ newlp, float* __restrict__ newval,
-    double* __restrict__ part, unsigned* counter, double* __restrict__ losses) {
+    double* __restrict__ part, double* __restrict__ losses) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   double lsum[6] = {0, 0, 0, 0, 0, 0};  // pg, v, ent, old_kl, kl, nclip
   if (n < N) {
@@ -112,8 +112,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad(
       row_losses(logpA, ol, av, vnew, rv, vold, vfClip > 0.f && ov, vfClip, clipEps, ent, lsum);
     }
   }
-  if (!losses) return;
-  fold_losses(lsum, part, counter, losses, N, vfCoef, entCoef);
+  if (losses) block_losses(lsum, part);
 }
 
 }  // namespace
@@ -127,12 +126,9 @@ int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, c
   PH_REQUIRE(A >= 1 && A <= (size_t)kMaxA, "ppo_grad: action count %zu outside [1,%d]", A, kMaxA);
   const unsigned grid = ceil_div(N, 256);
   double* part = nullptr;
-  unsigned* counter = nullptr;
   if (losses) {
     part = (double*)scratch(kSlotPpoPart, (size_t)grid * 6 * 8);
-    counter = (unsigned*)scratch(kSlotPpoCounter, 256);
-    if (!part || !counter) return PH_ERR_NOMEM;
-    PH_TRY(ensure_zeroed_counter(counter, st));
+    if (!part) return PH_ERR_NOMEM;
   }
   const size_t A4 = (A + 3) / 4 * 4;
   const bool vec = ldl % 4 == 0 && ldl >= A4 && ((uintptr_t)logits & 15) == 0 && ldd % 4 == 0 &&
@@ -143,13 +139,12 @@ int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, c
       k_ppo_grad<AM, true><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv, ret, \
                                                  old, ov, (int)N, (int)A, vfCoef, entCoef, clipEps, \
                                                  vfClip, max_shift, dlogits, (int)ldd, dvalues,     \
-                                                 (int)lddv, newlp, newval, part, counter, losses);  \
+                                                 (int)lddv, newlp, newval, part, losses);           \
     else                                                                                            \
       k_ppo_grad<AM, false><<<grid, 256, 0, st>>>(logits, (int)ldl, values, (int)ldv, act, adv,    \
                                                   ret, old, ov, (int)N, (int)A, vfCoef, entCoef,   \
                                                   clipEps, vfClip, max_shift, dlogits, (int)ldd,   \
-                                                  dvalues, (int)lddv, newlp, newval, part, counter, \
-                                                  losses);                                          \
+                                                  dvalues, (int)lddv, newlp, newval, part, losses); \
   } while (0)
   if (A <= 2) PH_PPO(2);
   else if (A <= 4) PH_PPO(4);
@@ -159,6 +154,10 @@ int ppo_grad(const float* logits, size_t ldl, const float* values, size_t ldv, c
   else PH_PPO(64);
 #undef PH_PPO
   PH_LAUNCH_CHECK();
+  if (losses) {
+    k_fold_losses<<<1, 256, 0, st>>>(part, (int)grid, (long)N, vfCoef, entCoef, losses);
+    PH_LAUNCH_CHECK();
+  }
   return PH_OK;
 }
 

@@ -21,18 +21,33 @@ __device__ inline R block_sum_256(R v, R* sh) {
 
 namespace {
 
-// Stage of a two-pass mean/std over x[0..n): each block sums a contiguous chunk (mode 0: x, mode 1:
-// (x-mean)^2); the last block to finish reduces the per-block partials in index order and writes
-// stats[mode] (mode 0: mean, mode 1: sqrt(var)+eps). The arrival counter is reset by that block.
+// Two-pass mean/std over x[0..n) in fixed 4096-element chunks. Pass 0 stores each chunk's sum of x in
+// part0, pass 1 each chunk's sum of (x - mean)^2 in part1. The passes and the normalisation form the
+// mean and the std from the partials themselves (every block the same way: a strided sum per lane and
+// the fixed tree), so no block waits on another inside a kernel; block 0 of pass 1 stores
+// stats[0] = mean and block 0 of the normalisation (or of k_moments_std) stats[1] = sqrt(var) + eps.
+template <typename R>
+__device__ inline R fold_parts(const R* __restrict__ part, unsigned G, R* sh) {
+  R a2 = 0;
+  for (unsigned i = threadIdx.x; i < G; i += 256) a2 += part[i];
+  const R tot = block_sum_256(a2, sh);
+  __syncthreads();  // sh is reused by the caller
+  return tot;
+}
+
 template <typename R>
 __global__ void __launch_bounds__(256) k_moments(const R* __restrict__ x, size_t n, size_t chunk,
-                                                 R* __restrict__ part, unsigned* counter,
-                                                 R* __restrict__ stats, int mode, R eps) {
+                                                 const R* __restrict__ part0, R* __restrict__ part,
+                                                 R* __restrict__ stats, int mode) {
   __shared__ R sh[256];
-  __shared__ bool last;
   const size_t lo = (size_t)blockIdx.x * chunk;
   const size_t hi = lo + chunk < n ? lo + chunk : n;
-  const R mean = mode ? stats[0] : R(0);
+  const R dn = (R)(n > 0 ? n : 1);
+  R mean = R(0);
+  if (mode) {
+    mean = fold_parts(part0, gridDim.x, sh) / dn;
+    if (blockIdx.x == 0 && threadIdx.x == 0) stats[0] = mean;
+  }
   R acc = 0;
   for (size_t i = lo + threadIdx.x; i < hi; i += 256) {
     R v = x[i];
@@ -44,32 +59,29 @@ __global__ void __launch_bounds__(256) k_moments(const R* __restrict__ x, size_t
     }
   }
   R s = block_sum_256(acc, sh);
-  if (threadIdx.x == 0) {
-    part[blockIdx.x] = s;
-    __threadfence();
-    unsigned prev = atomicAdd(counter, 1u);
-    last = (prev == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  R a2 = 0;
-  for (unsigned i = threadIdx.x; i < gridDim.x; i += 256)
-    a2 += __hip_atomic_load(&part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  R tot = block_sum_256(a2, sh);
-  if (threadIdx.x == 0) {
-    const R dn = (R)(n > 0 ? n : 1);
-    if (mode == 0) stats[0] = tot / dn;
-    else stats[1] = sqrt(tot / dn) + eps;
-    *counter = 0u;
-  }
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 
 template <typename R>
-__global__ void k_normalize(const R* __restrict__ x, R* __restrict__ y, size_t n,
-                            const R* __restrict__ stats) {
+__global__ void __launch_bounds__(256) k_normalize(const R* __restrict__ x, R* __restrict__ y, size_t n,
+                                                   const R* __restrict__ part0, const R* __restrict__ part1,
+                                                   unsigned G, R* __restrict__ stats, R eps) {
+  __shared__ R sh[256];
+  const R dn = (R)(n > 0 ? n : 1);
+  const R mean = fold_parts(part0, G, sh) / dn;
+  const R sd = sqrt(fold_parts(part1, G, sh) / dn) + eps;
+  if (blockIdx.x == 0 && threadIdx.x == 0) stats[1] = sd;
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = (x[i] - stats[0]) / stats[1];
+  if (i < n) y[i] = (x[i] - mean) / sd;
+}
+
+template <typename R>
+__global__ void __launch_bounds__(256) k_moments_std(size_t n, const R* __restrict__ part1, unsigned G,
+                                                     R* __restrict__ stats, R eps) {
+  __shared__ R sh[256];
+  const R dn = (R)(n > 0 ? n : 1);
+  const R sd = sqrt(fold_parts(part1, G, sh) / dn) + eps;
+  if (threadIdx.x == 0) stats[1] = sd;
 }
 
 // Column sums of a row-major [N x J] matrix (fp32 or bf16 elements), deterministic.
@@ -216,23 +228,27 @@ int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, 
   const size_t chunk = 4096;
   size_t G = (n + chunk - 1) / chunk;
   const size_t es = dtype == PH_F64 ? 8 : 4;
-  void* part = scratch(kSlotMomentsPart, G * es);
-  unsigned* counter = (unsigned*)scratch(kSlotMomentsCounter, 256);
-  if (!part || !counter) return PH_ERR_NOMEM;
+  uint8_t* part = (uint8_t*)scratch(kSlotMomentsPart, 2 * G * es);
+  if (!part) return PH_ERR_NOMEM;
   if (!stats) {
     stats = scratch(kSlotMomentsStats, 16);
     if (!stats) return PH_ERR_NOMEM;
   }
-  PH_TRY(ensure_zeroed_counter(counter, st));  // every launch leaves it at zero afterwards
   const unsigned g = (unsigned)G;
   if (dtype == PH_F64) {
-    k_moments<double><<<g, 256, 0, st>>>((const double*)x, n, chunk, (double*)part, counter, (double*)stats, 0, 1e-8);
-    k_moments<double><<<g, 256, 0, st>>>((const double*)x, n, chunk, (double*)part, counter, (double*)stats, 1, 1e-8);
-    if (y) k_normalize<double><<<ceil_div(n, 256), 256, 0, st>>>((const double*)x, (double*)y, n, (const double*)stats);
+    using R = double;
+    R *p0 = (R*)part, *p1 = p0 + G;
+    k_moments<R><<<g, 256, 0, st>>>((const R*)x, n, chunk, nullptr, p0, (R*)stats, 0);
+    k_moments<R><<<g, 256, 0, st>>>((const R*)x, n, chunk, p0, p1, (R*)stats, 1);
+    if (y) k_normalize<R><<<ceil_div(n, 256), 256, 0, st>>>((const R*)x, (R*)y, n, p0, p1, g, (R*)stats, 1e-8);
+    else k_moments_std<R><<<1, 256, 0, st>>>(n, p1, g, (R*)stats, 1e-8);
   } else {
-    k_moments<float><<<g, 256, 0, st>>>((const float*)x, n, chunk, (float*)part, counter, (float*)stats, 0, 1e-8f);
-    k_moments<float><<<g, 256, 0, st>>>((const float*)x, n, chunk, (float*)part, counter, (float*)stats, 1, 1e-8f);
-    if (y) k_normalize<float><<<ceil_div(n, 256), 256, 0, st>>>((const float*)x, (float*)y, n, (const float*)stats);
+    using R = float;
+    R *p0 = (R*)part, *p1 = p0 + G;
+    k_moments<R><<<g, 256, 0, st>>>((const R*)x, n, chunk, nullptr, p0, (R*)stats, 0);
+    k_moments<R><<<g, 256, 0, st>>>((const R*)x, n, chunk, p0, p1, (R*)stats, 1);
+    if (y) k_normalize<R><<<ceil_div(n, 256), 256, 0, st>>>((const R*)x, (R*)y, n, p0, p1, g, (R*)stats, 1e-8f);
+    else k_moments_std<R><<<1, 256, 0, st>>>(n, p1, g, (R*)stats, 1e-8f);
   }
   PH_LAUNCH_CHECK();
   return PH_OK;

@@ -150,16 +150,14 @@ __device__ inline void chan_merge(double& n, double& m, double& M2, double nb, d
 //   act (K wide, truncated to an integer) | adv (raw here) | ret = adv + value | old = logp |
 //   term = term > 0.5 ? 1 : 0 | ov = value
 // An index outside [0, N) yields NaN columns for that row (the sampler never produces one).
-// Each block also reduces its raw adv values to (count, mean, M2); the last block to arrive merges
-// all blocks in index order into stats = [mean, std] (population std) and re-arms the counter.
+// Each block also reduces its raw adv values to (count, mean, M2) in part; k_mb_stats merges the
+// blocks in index order into stats = [mean, std] (population std).
 template <typename R, bool TM>
 __global__ void __launch_bounds__(kGaThreads) k_mb_gather(
     const R* __restrict__ adv, const R* __restrict__ value, const R* __restrict__ act,
     const R* __restrict__ logp, const R* __restrict__ term, long N, int T, int K,
-    const int* __restrict__ seg, long B, R* __restrict__ out, double* __restrict__ part,
-    unsigned* counter, double* __restrict__ stats) {
+    const int* __restrict__ seg, long B, R* __restrict__ out, double* __restrict__ part) {
   __shared__ double sh[3][kGaThreads];
-  __shared__ bool last;
   const long n = B * T;
   const int tid = threadIdx.x;
   R* oact = out;
@@ -235,19 +233,17 @@ __global__ void __launch_bounds__(kGaThreads) k_mb_gather(
     part[3 * lb] = bn;
     part[3 * lb + 1] = bm;
     part[3 * lb + 2] = sh[2][0];
-    __threadfence();
-    const unsigned prev = atomicAdd(counter, 1u);
-    last = (prev == gridDim.x - 1);
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // merge: thread i folds blocks i, i+256, ... in order, then a fixed tree over the threads
+}
+
+// One block: thread i folds the gather blocks i, i+256, ... in order, then a fixed tree over the
+// threads; stats = [mean, std]. Launched after the gather, whose partials the launch boundary orders.
+__global__ void __launch_bounds__(kGaThreads) k_mb_stats(const double* __restrict__ part, unsigned G,
+                                                         double* __restrict__ stats) {
+  __shared__ double sh[3][kGaThreads];
+  const int tid = threadIdx.x;
   double mn = 0.0, mm = 0.0, mq = 0.0;
-  for (unsigned b = tid; b < gridDim.x; b += kGaThreads)
-    chan_merge(mn, mm, mq, __hip_atomic_load(&part[3 * b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-               __hip_atomic_load(&part[3 * b + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-               __hip_atomic_load(&part[3 * b + 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  for (unsigned b = tid; b < G; b += kGaThreads) chan_merge(mn, mm, mq, part[3 * b], part[3 * b + 1], part[3 * b + 2]);
   sh[0][tid] = mn;
   sh[1][tid] = mm;
   sh[2][tid] = mq;
@@ -266,7 +262,6 @@ __global__ void __launch_bounds__(kGaThreads) k_mb_gather(
     const double nt = sh[0][0] > 0.0 ? sh[0][0] : 1.0;
     stats[0] = sh[1][0];
     stats[1] = sqrt(sh[2][0] / nt);
-    *counter = 0u;
   }
 }
 
@@ -364,19 +359,20 @@ int mb_gather(const ph_replay_cols& c, const int* seg, const double* mp, size_t 
   const int K = c.K ? (int)c.K : 1;
   const unsigned nb = ceil_div((size_t)n, kGaBlock);
   double* part = (double*)scratch(kSlotReplayPart, (size_t)nb * 3 * 8 + 64);
-  unsigned* ctr = (unsigned*)scratch(kSlotReplayCtr, 256);
-  if (!part || !ctr) return PH_ERR_NOMEM;
-  PH_TRY(ensure_zeroed_counter(ctr, st));
+  if (!part) return PH_ERR_NOMEM;
   if (!stats) {
     stats = (double*)scratch(kSlotReplayStats, 64);
     if (!stats) return PH_ERR_NOMEM;
   }
   const long N = (long)c.N;
   const int T = (int)c.T;
-#define PH_GATHER(R, TM)                                                                              \
-  k_mb_gather<R, TM><<<nb, kGaThreads, 0, st>>>((const R*)c.adv, (const R*)c.value, (const R*)c.act,  \
-                                                (const R*)c.logp, (const R*)c.term, N, T, K, seg,      \
-                                                (long)B, (R*)out, part, ctr, stats)
+#define PH_GATHER(R, TM)                                                                                \
+  do {                                                                                                  \
+    k_mb_gather<R, TM><<<nb, kGaThreads, 0, st>>>((const R*)c.adv, (const R*)c.value, (const R*)c.act,  \
+                                                  (const R*)c.logp, (const R*)c.term, N, T, K, seg,      \
+                                                  (long)B, (R*)out, part);                               \
+    k_mb_stats<<<1, kGaThreads, 0, st>>>(part, nb, stats);                                              \
+  } while (0)
   if (c.dtype == PH_F64) {
     if (c.time_major) PH_GATHER(double, true);
     else PH_GATHER(double, false);

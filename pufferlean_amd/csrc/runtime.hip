@@ -76,7 +76,6 @@ int ensure_zeroed_words(unsigned* words, int n, hipStream_t st) {
   return PH_OK;
 }
 
-int ensure_zeroed_counter(unsigned* counter, hipStream_t st) { return ensure_zeroed_words(counter, 64, st); }
 
 namespace {
 __global__ void k_zero_words_grid(unsigned* p, long n) {

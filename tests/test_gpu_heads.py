@@ -47,10 +47,12 @@ def word_unit(x):
 
 
 # ---- loss gradients -----------------------------------------------------------------------------
+# heads 3+9+2+5 (+ value) fit the 32-wide LDS tile; 20+17+3 run the row-per-lane kernel
+@pytest.mark.parametrize("sizes", [[3, 9, 2, 5], [20, 17, 3]])
 @pytest.mark.parametrize("vfclip", [0.0, 0.25])
-def test_ppo_grad_md_matches_oracle(gpu, vfclip):
-    sizes = [3, 9, 2, 5]
-    N, K, W = 5000, 4, 19
+def test_ppo_grad_md_matches_oracle(gpu, vfclip, sizes):
+    N, K, W = 5000, len(sizes), sum(sizes)
+    print(f"md grad sizes={sizes} vfclip={vfclip}", flush=True)
     out = (rng.normal(0xA01, N * (W + 1)).reshape(N, W + 1) * 2.0).astype(np.float32).astype(np.float64)
     acts = np.stack([rng.randint(0xA02 + h, N, s) for h, s in enumerate(sizes)], axis=1)
     adv, ret = rng.normal(0xA06, N), rng.normal(0xA07, N)
@@ -76,13 +78,13 @@ def test_ppo_grad_md_matches_oracle(gpu, vfclip):
     np.testing.assert_allclose(losses.cpu().numpy(), rL, rtol=1e-5, atol=max(1e-6, 2.0 / N))
 
 
-def test_ppo_grad_md_out_of_range_action_gives_nan_row(gpu):
-    """The kernel's range check: a bad action makes its row's logit gradients and log-prob NaN, as in
-    the oracle, and reads nothing outside the row."""
-    sizes = [3, 4]
-    N, K, W = 4, 2, 7
+@pytest.mark.parametrize("sizes", [[3, 4], [20, 17]])
+def test_ppo_grad_md_out_of_range_action_gives_nan_row(gpu, sizes):
+    """The kernels' range check (tiled and row-per-lane forms): a bad action makes its row's logit
+    gradients and log-prob NaN, as in the oracle, and reads nothing outside the row."""
+    N, K, W = 4, 2, sum(sizes)
     out = rng.normal(0xA0A, N * (W + 1)).reshape(N, W + 1).astype(np.float32).astype(np.float64)
-    acts = np.array([[0, 3], [3, 0], [-1, 2], [2, 3]], np.int32)
+    acts = np.array([[0, sizes[1] - 1], [sizes[0], 0], [-1, 2], [2, sizes[1] - 1]], np.int32)
     ref, rlp, _ = O.ppo_grad_md(out, acts.astype(np.float64), np.ones(N), np.zeros(N), np.full(N, -2.0), None,
                                 sizes)
     dout_, dact = cu(out), cu(acts, torch.int32)
@@ -99,9 +101,12 @@ def test_ppo_grad_md_out_of_range_action_gives_nan_row(gpu):
     assert rel(gg[ok], ref[ok]) < 1e-5 and rel(gg[[1, 2], W], ref[[1, 2], W]) < 1e-5
 
 
+# 4 dims fit the 32-wide LDS tile; 17 dims (35 columns) run the row-per-lane kernel
+@pytest.mark.parametrize("dim", [4, 17])
 @pytest.mark.parametrize("vfclip,lslo", [(0.0, -20.0), (0.25, -5.0)])
-def test_ppo_grad_cont_matches_oracle(gpu, vfclip, lslo):
-    dim, N = 4, 5000
+def test_ppo_grad_cont_matches_oracle(gpu, vfclip, lslo, dim):
+    N = 5000
+    print(f"cont grad dim={dim} vfclip={vfclip}", flush=True)
     O_ = 2 * dim + 1
     out = rng.normal(0xA11, N * O_).reshape(N, O_)
     out[:, dim:2 * dim] *= 0.7
