@@ -367,6 +367,19 @@ int ph_cuda_muon_step_mlp_resident(size_t policyH, const double* gRaw, size_t H,
 int ph_cuda_policy_load(const double* pm, size_t P, size_t* handle);
 int ph_cuda_policy_download(size_t handle, size_t P, double* pm);
 int ph_cuda_policy_free(size_t handle);
+/* Checkpoint byte layout of the trainers (ckptToBytes / bytesToCkpt, Puffer/RL/FFITrain.lean:40-69):
+ * [P as u64 little-endian][P doubles as their IEEE bits, little-endian], 8 (P + 1) bytes.
+ * ph_ckpt_decode reports P = min(header, whole doubles present), as bytesToCkpt does for a short
+ * file; with w NULL it only reports P. Host-only: no device needed. */
+size_t ph_ckpt_bytes(size_t P);
+int ph_ckpt_encode(const double* w, size_t P, uint8_t* out);
+int ph_ckpt_decode(const uint8_t* b, size_t nbytes, double* w, size_t cap, size_t* P_out);
+/* The same layout straight from / into a resident policy handle (savePolicyCheckpoint after
+ * policyDownloadFFI, MinGRUTrain.lean:866-873; the load path 680-692): save writes the handle's P
+ * weights (not the momentum) to out (ph_ckpt_bytes(P) bytes); load makes a new handle of
+ * [weights; zero momentum] and rejects a checkpoint whose parameter count differs from P. */
+int ph_cuda_policy_save_ckpt(size_t handle, size_t P, uint8_t* out);
+int ph_cuda_policy_load_ckpt(const uint8_t* b, size_t nbytes, size_t P, size_t* handle);
 /* lean_cuda_mg_loss_enable / lean_cuda_mg_read_losses (puffercuda.cu:336-352): the 7 dashboard
  * losses (policy, value, entropy, total, old_kl, kl, clipfrac) of the last surfaced minibatch. */
 int ph_cuda_mg_loss_enable(uint8_t on);

@@ -91,6 +91,11 @@ SIGNATURES: dict[str, list] = {
                              dbl, dbl, dbl, dbl, u8, dptr],
     "ph_cuda_train_update_resident": [sz, dptr, dptr, dptr, dptr, dptr, dptr, sz, dptr, sz, sz, sz, sz, sz,
                                       sz, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, u8, dptr],
+    "ph_ckpt_bytes": [sz],
+    "ph_ckpt_encode": [dptr, sz, vp],
+    "ph_ckpt_decode": [vp, sz, dptr, sz, szptr],
+    "ph_cuda_policy_save_ckpt": [sz, sz, vp],
+    "ph_cuda_policy_load_ckpt": [vp, sz, sz, szptr],
     "ph_cuda_train_update_wide_resident": [sz, dptr, dptr, dptr, dptr, dptr, dptr, sz, dptr, dptr, sz, sz, sz,
                                            sz, sz, sz, u32, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl, dbl,
                                            u8, dptr],
@@ -124,7 +129,7 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }
-_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long,
+_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long, "ph_ckpt_bytes": C.c_size_t,
              "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_cuda_available": C.c_uint8}
 
 _lib = None

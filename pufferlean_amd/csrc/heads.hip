@@ -112,11 +112,21 @@ constexpr int kTileP = 33;
 // pair advances by 256 / O rows and 256 % O columns with a carry, so no division runs per element.
 __device__ __forceinline__ void tile_load(const float* __restrict__ src, long ld, int O, long n0, int R,
                                           float* __restrict__ tile) {
+  // a lane's share is at most kTileW elements (R * O <= 256 * kTileW): every load is issued before
+  // the first LDS store waits on one
+  constexpr int kPer = kTileW;
   const int q = (int)blockDim.x / O, rm = (int)blockDim.x % O;
   int r = (int)threadIdx.x / O, c = (int)threadIdx.x % O;
   const float* s = src + n0 * ld;
-  while (r < R) {
-    tile[r * kTileP + c] = s[(long)r * ld + c];
+  float v[kPer];
+  int dst[kPer];
+#pragma unroll
+  for (int it = 0; it < kPer; it++) {
+    dst[it] = -1;
+    if (r < R) {
+      v[it] = s[(long)r * ld + c];
+      dst[it] = r * kTileP + c;
+    }
     r += q;
     c += rm;
     if (c >= O) {
@@ -124,6 +134,9 @@ __device__ __forceinline__ void tile_load(const float* __restrict__ src, long ld
       r++;
     }
   }
+#pragma unroll
+  for (int it = 0; it < kPer; it++)
+    if (dst[it] >= 0) tile[dst[it]] = v[it];
 }
 __device__ __forceinline__ void tile_store(float* __restrict__ dst, long ld, int O, long n0, int R,
                                            const float* __restrict__ tile) {
@@ -141,8 +154,10 @@ __device__ __forceinline__ void tile_store(float* __restrict__ dst, long ld, int
   }
 }
 
-// k_ppo_grad_md for W + 1 <= kTileW: each probability is computed once and kept with its head's
-// expected logit for the gradient pass.
+// k_ppo_grad_md for W + 1 <= kTileW and K <= kTileHeads: each probability is computed once and kept
+// with its head's expected logit for the gradient pass; the actions and the row's scalars are loaded
+// before the staging barrier, so their latency overlaps the tile's.
+constexpr int kTileHeads = 8;
 __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restrict__ out, long ldo,
                                                           const int* __restrict__ act, const float* __restrict__ adv,
                                                           const float* __restrict__ ret, const float* __restrict__ old,
@@ -154,22 +169,34 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
   __shared__ float tile[256 * kTileP];
   const long n0 = (long)blockIdx.x * 256;
   const int R = (int)(N - n0 < 256 ? N - n0 : 256);
-  const int t = threadIdx.x, O = W + 1;
+  const int t = threadIdx.x, O = W + 1, K = hs.K;
+  const long n = n0 + t;
+  const bool live = t < R;
+  int av[kTileHeads];
+  float A = 0.f, rv = 0.f, ol = 0.f, vold = 0.f;
+  if (live) {
+#pragma unroll
+    for (int h = 0; h < kTileHeads; h++) av[h] = h < K ? act[n * K + h] : 0;
+    A = adv[n];
+    rv = ret[n];
+    ol = old[n];
+    vold = ov ? ov[n] : 0.f;
+  }
   tile_load(out, ldo, O, n0, R, tile);
   __syncthreads();
   double lsum[6] = {0, 0, 0, 0, 0, 0};
-  if (t < R) {
-    const long n = n0 + t;
+  if (live) {
     float x[kTileW], p[kTileW], pout[kTileW];
 #pragma unroll
     for (int k = 0; k < kTileW; k++) x[k] = k < O ? tile[t * kTileP + k] : 0.f;
-    const int* a = act + n * hs.K;
     float joint = 0.f, entropy = 0.f;
     unsigned hit = 0u;
     bool inRange = true;
     int off = 0;
-    for (int h = 0; h < hs.K; h++) {
-      const int end = off + hs.n[h], ah = a[h];
+#pragma unroll
+    for (int h = 0; h < kTileHeads; h++) {
+      if (h >= K) break;
+      const int end = off + hs.n[h], ah = av[h];
       float m = -INFINITY;
 #pragma unroll
       for (int k = 0; k < kTileW; k++)
@@ -200,9 +227,8 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
       off = end;
     }
     if (!inRange) joint = __builtin_nanf("");
-    const float ratio = expf(joint - old[n]), lo = 1.f - clip, hi = 1.f + clip;
+    const float ratio = expf(joint - ol), lo = 1.f - clip, hi = 1.f + clip;
     const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
-    const float A = adv[n];
     const float dPol = !inRange ? __builtin_nanf("")
                      : (A * ratio <= A * rc) ? A * ratio : ((lo < ratio && ratio < hi) ? A * ratio : 0.f);
 #pragma unroll
@@ -213,11 +239,10 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
 #pragma unroll
     for (int k = 0; k < kTileW; k++)
       if (k == W) vnew = x[k];
-    const float vold = ov ? ov[n] : 0.f;
-    tile[t * kTileP + W] = -vf * vloss_grad(vnew, ret[n], vold, ov != nullptr, vfClip);
+    tile[t * kTileP + W] = -vf * vloss_grad(vnew, rv, vold, ov != nullptr, vfClip);
     if (newlp) newlp[n] = joint;
     if (newval) newval[n] = vnew;
-    if (losses) row_losses(joint, old[n], A, vnew, ret[n], vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
+    if (losses) row_losses(joint, ol, A, vnew, rv, vold, vfClip > 0.f && ov, vfClip, clip, entropy, lsum);
   }
   __syncthreads();
   tile_store(dout, ldd, O, n0, R, tile);
@@ -433,7 +458,7 @@ int ppo_grad_md(const float* out, size_t ldo, const int* act, const float* adv, 
   const unsigned grid = ceil_div(N, 256);
   double* part;
   PH_TRY(loss_part(losses, grid, part));
-  if (W + 1 <= kTileW)
+  if (W + 1 <= kTileW && K <= (size_t)kTileHeads)
     k_ppo_grad_md_tile<<<grid, 256, 0, st>>>(out, (long)ldo, act, adv, ret, old, ov, (long)N, hs, W, vf, ent, clip,
                                              vfClip, dout, (long)ldd, newlp, newval, part, losses);
   else

@@ -12,6 +12,9 @@
 #include <cmath>
 #include <cstdlib>
 
+#include <cstring>
+#include <vector>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -867,6 +870,65 @@ extern "C" int ph_cuda_policy_free(size_t handle) {
     PH_CHECK_HIP(hipFree((void*)handle));
   }
   return PH_OK;
+}
+
+// ---- checkpoint byte layout (FFITrain.lean:40-69): [P as u64 LE][P doubles as IEEE bits, LE] -------
+namespace {
+void put_u64le(uint8_t* b, uint64_t x) {
+  for (int k = 0; k < 8; k++) b[k] = (uint8_t)(x >> (8 * k));
+}
+uint64_t get_u64le(const uint8_t* b) {
+  uint64_t x = 0;
+  for (int k = 0; k < 8; k++) x |= (uint64_t)b[k] << (8 * k);
+  return x;
+}
+}  // namespace
+
+extern "C" size_t ph_ckpt_bytes(size_t P) { return 8 * (P + 1); }
+
+extern "C" int ph_ckpt_encode(const double* w, size_t P, uint8_t* out) {
+  PH_REQUIRE(out && (P == 0 || w), "ph_ckpt_encode: null buffer");
+  put_u64le(out, (uint64_t)P);
+  for (size_t i = 0; i < P; i++) {
+    uint64_t bits;
+    memcpy(&bits, &w[i], 8);
+    put_u64le(out + 8 * (i + 1), bits);
+  }
+  return PH_OK;
+}
+
+extern "C" int ph_ckpt_decode(const uint8_t* b, size_t nbytes, double* w, size_t cap, size_t* P_out) {
+  PH_REQUIRE(P_out && (nbytes == 0 || b), "ph_ckpt_decode: null buffer");
+  // bytesToCkpt: the header's count, bounded by the whole doubles the file holds
+  const size_t avail = nbytes >= 8 ? (nbytes - 8) / 8 : 0;
+  const size_t head = nbytes >= 8 ? (size_t)get_u64le(b) : 0;
+  const size_t P = head < avail ? head : avail;
+  *P_out = P;
+  if (!w) return PH_OK;
+  PH_REQUIRE(cap >= P, "ph_ckpt_decode: %zu doubles do not fit a buffer of %zu", P, cap);
+  for (size_t i = 0; i < P; i++) {
+    const uint64_t bits = get_u64le(b + 8 * (i + 1));
+    memcpy(&w[i], &bits, 8);
+  }
+  return PH_OK;
+}
+
+extern "C" int ph_cuda_policy_save_ckpt(size_t handle, size_t P, uint8_t* out) {
+  PH_REQUIRE(handle != 0 && out && P > 0, "ph_cuda_policy_save_ckpt: bad arguments");
+  std::vector<double> w(P);
+  PH_TRY(finish());
+  PH_TRY(down(w.data(), (const void*)handle, 8 * P));  // the weights: the first P of [params; mom]
+  return ph_ckpt_encode(w.data(), P, out);
+}
+
+extern "C" int ph_cuda_policy_load_ckpt(const uint8_t* b, size_t nbytes, size_t P, size_t* handle) {
+  PH_REQUIRE(handle && P > 0, "ph_cuda_policy_load_ckpt: bad arguments");
+  size_t Pf = 0;
+  PH_TRY(ph_ckpt_decode(b, nbytes, nullptr, 0, &Pf));
+  PH_REQUIRE(Pf == P, "ph_cuda_policy_load_ckpt: checkpoint has %zu params, this policy needs %zu", Pf, P);
+  std::vector<double> pm(2 * P, 0.0);  // momentum starts at zero, as the trainers reload
+  PH_TRY(ph_ckpt_decode(b, nbytes, pm.data(), P, &Pf));
+  return ph_cuda_policy_load(pm.data(), P, handle);
 }
 
 // ---- dashboard-loss channel --------------------------------------------------------------------

@@ -224,8 +224,41 @@ constexpr unsigned kB = 256;
 // Every value is computed with the chain's operations in the chain's order (ascending sums, no
 // contraction), so the result is bit-identical to the multi-launch form. The Q = A P (or P A)
 // product is consumed where it is made: the thread computing Q(i, j) updates X(i, j) in place, as
-// that phase reads only A and P. W/nW and M/nM may alias (each element is read and written by one
+// that phase reads only A and P (X is then read by no other thread of the phase). W/nW and M/nM may alias (each element is read and written by one
 // thread).
+// Four running sums s[2r + c] = s[2r + c] + u_r(l) * v_c(l) for l ascending, with
+// u_r(l) = U[ur + l * us] and v_c(l) = V[vc + l * vs]. Loads are issued four steps at a time, so a step
+// waits on LDS once per four; each sum still adds its products one at a time in ascending l.
+__device__ __forceinline__ void dot2x2(const double* U, int u0, int u1, int us, const double* V, int v0, int v1,
+                                       int vs, int L, double s[4]) {
+#pragma clang fp contract(off)
+  int l = 0;
+  for (; l + 4 <= L; l += 4) {
+    double a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      a0[k] = U[u0 + (l + k) * us];
+      a1[k] = U[u1 + (l + k) * us];
+      b0[k] = V[v0 + (l + k) * vs];
+      b1[k] = V[v1 + (l + k) * vs];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      s[0] = s[0] + a0[k] * b0[k];
+      s[1] = s[1] + a0[k] * b1[k];
+      s[2] = s[2] + a1[k] * b0[k];
+      s[3] = s[3] + a1[k] * b1[k];
+    }
+  }
+  for (; l < L; l++) {
+    const double a0 = U[u0 + l * us], a1 = U[u1 + l * us], b0 = V[v0 + l * vs], b1 = V[v1 + l * vs];
+    s[0] = s[0] + a0 * b0;
+    s[1] = s[1] + a0 * b1;
+    s[2] = s[2] + a1 * b0;
+    s[3] = s[3] + a1 * b1;
+  }
+}
+
 constexpr int kExactFusedMaxSteps = 8;
 constexpr long kExactFusedLds = 8192;  // doubles: 64 KB
 struct ExactCoeffs {
@@ -256,6 +289,7 @@ __global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, cons
   // Frobenius norm: row sums of squares in ascending column order, then the rows in order
   for (int r = tid; r < rows; r += T) {
     double sq = 0.0;
+#pragma unroll 8
     for (int j = 0; j < cols; j++) {
       const double v = X[r * cols + j];
       sq = sq + v * v;
@@ -265,47 +299,68 @@ __global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, cons
   __syncthreads();
   if (tid == 0) {
     double sq = 0.0;
+#pragma unroll 8
     for (int r = 0; r < rows; r++) sq = sq + P[r];
     inv = 1.0 / (sqrt(sq) + eps);
   }
   __syncthreads();
   for (int i = tid; i < n; i += T) X[i] = inv * X[i];
   __syncthreads();
+  // 2 x 2 output tiles per thread: four independent sums, each operand load serving two outputs.
+  // Every output keeps its own ascending sum. A(i, j) and A(j, i) are the same products in the same
+  // order, so only tiles on or above the diagonal are formed and the other half is mirrored.
+  const int tm = (mn + 1) / 2, tr = (rows + 1) / 2, tc = (cols + 1) / 2;
   for (int it = 0; it < nsteps; it++) {
     const double a = cf.v[3 * it], b = cf.v[3 * it + 1], c = cf.v[3 * it + 2];
-    for (int e = tid; e < mn * mn; e += T) {  // A = X X^T (wide) or X^T X (tall)
-      const int i = e / mn, j = e % mn;
-      double t = 0.0;
-      if (wide) {
-        for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * X[j * cols + l];
-      } else {
-        for (int l = 0; l < rows; l++) t = t + X[l * cols + i] * X[l * cols + j];
+    for (int e = tid; e < tm * tm; e += T) {  // A = X X^T (wide) or X^T X (tall)
+      const int ti = e / tm, tj = e % tm;
+      if (tj < ti) continue;
+      const int i0 = 2 * ti, j0 = 2 * tj;
+      const int i1 = i0 + 1 < mn ? i0 + 1 : i0, j1 = j0 + 1 < mn ? j0 + 1 : j0;  // clamped loads
+      double sv[4] = {0.0, 0.0, 0.0, 0.0};
+      if (wide)
+        dot2x2(X, i0 * cols, i1 * cols, 1, X, j0 * cols, j1 * cols, 1, cols, sv);
+      else
+        dot2x2(X, i0, i1, cols, X, j0, j1, cols, rows, sv);
+      const double s00 = sv[0], s01 = sv[1], s10 = sv[2], s11 = sv[3];
+      A[i0 * mn + j0] = s00;
+      A[j0 * mn + i0] = s00;
+      if (j0 + 1 < mn) {
+        A[i0 * mn + j0 + 1] = s01;
+        A[(j0 + 1) * mn + i0] = s01;
       }
-      A[e] = t;
+      if (i0 + 1 < mn) {
+        A[(i0 + 1) * mn + j0] = s10;
+        A[j0 * mn + i0 + 1] = s10;
+      }
+      if (i0 + 1 < mn && j0 + 1 < mn) {
+        A[(i0 + 1) * mn + j0 + 1] = s11;
+        A[(j0 + 1) * mn + i0 + 1] = s11;
+      }
     }
     __syncthreads();
-    for (int e = tid; e < n; e += T) {  // P = A X (wide) or X A (tall)
-      const int i = e / cols, j = e % cols;
-      double t = 0.0;
-      if (wide) {
-        for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * X[l * cols + j];
-      } else {
-        for (int l = 0; l < cols; l++) t = t + X[i * cols + l] * A[l * cols + j];
+    // P = A X (wide) or X A (tall), then Q = A P (wide) or P A (tall) with X = a X + b P + c Q
+    for (int pass = 0; pass < 2; pass++) {
+      const double* Y = pass == 0 ? X : P;  // right (wide) or left (tall) operand
+      for (int e = tid; e < tr * tc; e += T) {
+        const int i0 = 2 * (e / tc), j0 = 2 * (e % tc);
+        const int i1 = i0 + 1 < rows ? i0 + 1 : i0, j1 = j0 + 1 < cols ? j0 + 1 : j0;
+        double sv[4] = {0.0, 0.0, 0.0, 0.0};
+        if (wide)
+          dot2x2(A, i0 * rows, i1 * rows, 1, Y, j0, j1, cols, rows, sv);
+        else
+          dot2x2(Y, i0 * cols, i1 * cols, 1, A, j0, j1, cols, cols, sv);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int i = i0 + (q >> 1), j = j0 + (q & 1);
+          if (i >= rows || j >= cols) continue;
+          const int o = i * cols + j;
+          if (pass == 0) P[o] = sv[q];
+          else X[o] = a * X[o] + b * P[o] + c * sv[q];
+        }
       }
-      P[e] = t;
+      __syncthreads();
     }
-    __syncthreads();
-    for (int e = tid; e < n; e += T) {  // Q = A P (wide) or P A (tall); X = a X + b P + c Q
-      const int i = e / cols, j = e % cols;
-      double t = 0.0;
-      if (wide) {
-        for (int l = 0; l < rows; l++) t = t + A[i * rows + l] * P[l * cols + j];
-      } else {
-        for (int l = 0; l < cols; l++) t = t + P[i * cols + l] * A[l * cols + j];
-      }
-      X[e] = a * X[e] + b * P[e] + c * t;
-    }
-    __syncthreads();
   }
   for (int i = tid; i < n; i += T) nW[i] = c1 * W[i] + c2 * X[i];
 }
