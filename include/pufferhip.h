@@ -259,6 +259,13 @@ int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c, const flo
                        const float* obs, const int* act, const float* adv, const float* ret,
                        const float* oldlp, const float* oldval, const float* done, float* G,
                        float* newlp, float* newval, double* losses, void* stream);
+/* The same with K categorical heads (k_mg_ppo_b_md, puffercuda.cu:4940-4975): d->A is the logits
+ * width, the sum of head_sizes[K] (host array); act is int32 [T*B][K]; newlp is the joint log-prob.
+ * The loss on the head rows is ph_ppo_grad_md's; the rest of the BPTT is the categorical one. */
+int ph_mingru_ppo_grad_md(const ph_mingru_dims* d, const ph_ppo_coefs* c, const int* head_sizes, size_t K,
+                          const float* params, const float* obs, const int* act, const float* adv,
+                          const float* ret, const float* oldlp, const float* oldval, const float* done,
+                          float* G, float* newlp, float* newval, double* losses, void* stream);
 /* Grad-norm clip of G (scaled by gscale) then Muon on every matrix, stepvec on every bias, in place
  * on params/mom (the matrices: wEnc, each W_l, wDec, wVal). */
 int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params, float* mom,
@@ -413,21 +420,23 @@ uint8_t ph_ffi_cuda_available(void);
 /* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, P), obs (nobs >= T*B*D, host,
  * time-major; or nobs = 0 in the device-column mode, which gathers the minibatch from the resident obs
  * trajectory of ph_cuda_mg_obs_traj by the drawn segments, as the reference gathers its rollout's),
- * K = 1. Two scalar sources, chosen as the reference chooses them:
+ * K heads (K <= 1: one categorical head over A logits; K > 1: hs[K] (nhs >= K) holds the head sizes as
+ * doubles, summing to A, and every action field below is K wide). Two scalar sources, chosen as the
+ * reference chooses them:
  *   device-column mode: (nseg > 0 and nprio > 0: host segIdx[B] as doubles and mbPrio[B]) or (both 0
  *     and a fresh sampler result of B draws from ph_cuda_mg_vtrace_prio, consumed here), with the
- *     resident columns of ph_cuda_mg_prep for this T: the 6 scalars are gathered on the device
+ *     resident columns of ph_cuda_mg_prep for this T and K: the scalars are gathered on the device
  *     (ph_mb_gather) and, after the BPTT, value/ratio of the drawn segments are iterated in place
  *     (ph_mb_iterate), exactly the reference's order;
- *   host mode: scal = [act|adv|ret|old|term|ov] (nscal >= 6*T*B).
+ *   host mode: scal = [act (K per row)|adv|ret|old|term|ov] (nscal >= (K+5)*T*B).
  * Either way out receives the reference's host form [g (P); new_logp (T*B); new_value (T*B)] (the
  * reference also returns this form in device-column mode when its resident gradient buffer is
  * unavailable). Precision: bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
 int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
                             size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L, size_t A,
-                            size_t K, double vfCoef, double entCoef, double clipEps, double vfClip,
-                            const double* segIdx, size_t nseg, const double* mbPrio, size_t nprio,
-                            double* out);
+                            size_t K, const double* hs, size_t nhs, double vfCoef, double entCoef,
+                            double clipEps, double vfClip, const double* segIdx, size_t nseg,
+                            const double* mbPrio, size_t nprio, double* out);
 /* Prioritised replay, host-buffer forms. The resident columns are library-owned, one set per
  * process (the reference's g_dc* buffers), bound to the device current at ph_cuda_mg_prep. */
 /* lean_cuda_mg_prep (puffercuda.cu:316-336): upload the rollout columns rew, term, logp, val (N*T

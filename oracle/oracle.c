@@ -29,6 +29,9 @@
  *   orc_muon_mat / stepvec       closed form on diagonal inputs; mlp wrapper == per-tensor calls
  *   orc_gclip                    closed form
  *   orc_mingru_ppo_grad_seq      finite differences of its own forward objective (orc_mingru_objective)
+ *   orc_mingru_ppo_grad_seq_md   two heads equal one categorical head over the product space (decoder
+ *                                rows W1[i] + W2[j]): identical shared-layer gradients, head gradients
+ *                                the product's summed over the other head; K = 1 equals the categorical
  *   orc_mingru_heinsen           equals the sequential recurrence within roundoff
  *   orc_seg_l1                   exact on dyadic inputs (every summation order gives the same bits);
  *                                numpy row sums of |adv| within roundoff
@@ -572,14 +575,12 @@ double orc_gclip(double* g, size_t P, double sc, double maxNorm) {
 static inline double sigm(double x) { return 1.0 / (1.0 + exp(-x)); }
 static inline double gact(double x) { return x >= 0.0 ? x + 0.5 : sigm(x); }
 
-/* Single-sequence MinGRU PPO BPTT (pufferffi.c:763-876). Layout [wEnc(H*D)|bEnc(H)|L x W(3H*H)|
- * wDec(A*H)|bDec(A)|wVal(H)|bVal(1)]; W rows [0,H) hid, [H,2H) gate, [2H,3H) proj. Zero initial state,
- * state reset after a terminal, no gradient across a terminal. */
-void orc_mingru_ppo_grad_seq(const double* p, const double* obsSeq, const double* acts,
-                             const double* advs, const double* rets, const double* oldlps,
-                             const double* terms, const double* oldvals, size_t T, size_t H,
-                             size_t D, size_t L, size_t A, double vfCoef, double entCoef,
-                             double clipEps, double vfClip, double* out) {
+/* K == 0: one categorical head over the A logits, acts[t]; K >= 1: K heads of sizes[K] summing to A,
+ * acts[t*K + h] (MinGRUTrain.lean:130-200, the multi-discrete head on the same MinGRU core). */
+static void mingru_seq(const double* p, const double* obsSeq, const double* acts, const double* advs,
+                       const double* rets, const double* oldlps, const double* terms, const double* oldvals,
+                       size_t T, size_t H, size_t D, size_t L, size_t A, size_t K, const int* sizes,
+                       double vfCoef, double entCoef, double clipEps, double vfClip, double* out) {
   size_t szE = H * D, szL = 3 * H * H;
   size_t P = szE + H + L * szL + A * H + A + H + 1;
   const double* wEnc = p; const double* bEnc = p + szE; const double* Wl0 = p + szE + H;
@@ -646,14 +647,25 @@ void orc_mingru_ppo_grad_seq(const double* p, const double* obsSeq, const double
   double* dyg = (double*)calloc(H, sizeof(double));
   double* dyp = (double*)calloc(H, sizeof(double));
   double* dl = (double*)calloc(A ? A : 1, sizeof(double));
+  double* row = (double*)calloc(A + 1, sizeof(double));
+  double* drow = (double*)calloc(A + 1, sizeof(double));
   double dv;
   for (size_t k1 = 0; k1 < T; k1++) {
     size_t t = T - 1 - k1;
     const double* x = obsSeq + t * D;
     double nlp, nv;
-    orc_ppo_grad(lg + t * A, A, vv + t, 1, acts + t, advs + t, rets + t, oldlps + t,
-                 oldvals ? oldvals + t : NULL, 1, A, vfCoef, entCoef, clipEps, vfClip, 0, dl, A,
-                 &dv, 1, &nlp, &nv);
+    if (K == 0) {
+      orc_ppo_grad(lg + t * A, A, vv + t, 1, acts + t, advs + t, rets + t, oldlps + t,
+                   oldvals ? oldvals + t : NULL, 1, A, vfCoef, entCoef, clipEps, vfClip, 0, dl, A,
+                   &dv, 1, &nlp, &nv);
+    } else {
+      for (size_t k = 0; k < A; k++) row[k] = lg[t * A + k];
+      row[A] = vv[t];
+      orc_ppo_grad_md(row, A + 1, acts + t * K, advs + t, rets + t, oldlps + t, oldvals ? oldvals + t : NULL, 1,
+                      sizes, K, vfCoef, entCoef, clipEps, vfClip, drow, A + 1, &nlp, &nv);
+      for (size_t k = 0; k < A; k++) dl[k] = drow[k];
+      dv = drow[A];
+    }
     out[P + t] = nlp; out[P + T + t] = nv;
     const double* hft = hf + t * H;
     for (size_t j = 0; j < H; j++) dh[j] = 0.0;
@@ -698,7 +710,30 @@ void orc_mingru_ppo_grad_seq(const double* p, const double* obsSeq, const double
   }
   free(hin); free(prv); free(yh); free(yg); free(yp); free(oo); free(hf); free(lg); free(vv);
   free(st); free(h); free(y); free(hn); free(dOn); free(dpv); free(dh); free(dhi); free(dyh);
-  free(dyg); free(dyp); free(dl);
+  free(dyg); free(dyp); free(dl); free(row); free(drow);
+}
+
+/* Single-sequence MinGRU PPO BPTT (pufferffi.c:763-876). Layout [wEnc(H*D)|bEnc(H)|L x W(3H*H)|
+ * wDec(A*H)|bDec(A)|wVal(H)|bVal(1)]; W rows [0,H) hid, [H,2H) gate, [2H,3H) proj. Zero initial state,
+ * state reset after a terminal, no gradient across a terminal. */
+void orc_mingru_ppo_grad_seq(const double* p, const double* obsSeq, const double* acts,
+                             const double* advs, const double* rets, const double* oldlps,
+                             const double* terms, const double* oldvals, size_t T, size_t H,
+                             size_t D, size_t L, size_t A, double vfCoef, double entCoef,
+                             double clipEps, double vfClip, double* out) {
+  mingru_seq(p, obsSeq, acts, advs, rets, oldlps, terms, oldvals, T, H, D, L, A, 0, NULL, vfCoef, entCoef, clipEps,
+             vfClip, out);
+}
+
+/* The multi-discrete form (mingruGradSeqMD, MinGRUTrain.lean:140-230; the device's k_mg_ppo_b_md,
+ * puffercuda.cu:4940-4975): A = sum of sizes[K] decoder rows, acts [T][K], new_logp the joint. */
+void orc_mingru_ppo_grad_seq_md(const double* p, const double* obsSeq, const double* acts, const double* advs,
+                                const double* rets, const double* oldlps, const double* terms,
+                                const double* oldvals, size_t T, size_t H, size_t D, size_t L, size_t A,
+                                const int* sizes, size_t K, double vfCoef, double entCoef, double clipEps,
+                                double vfClip, double* out) {
+  mingru_seq(p, obsSeq, acts, advs, rets, oldlps, terms, oldvals, T, H, D, L, A, K, sizes, vfCoef, entCoef, clipEps,
+             vfClip, out);
 }
 
 /* Heinsen log-space scan (MinGRU.lean:116-168; tools/mingru_ref.py:113-131): with log a_t = log(1-z_t),

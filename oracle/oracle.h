@@ -118,6 +118,12 @@ void orc_mingru_ppo_grad_seq(const double* params, const double* obsSeq, const d
                              const double* terms, const double* oldvals, size_t T, size_t H,
                              size_t D, size_t L, size_t A, double vfCoef, double entCoef,
                              double clipEps, double vfClip, double* out);
+/* The same with K heads of sizes[K] summing to A; acts [T][K]; new_logp is the joint log-prob. */
+void orc_mingru_ppo_grad_seq_md(const double* p, const double* obsSeq, const double* acts, const double* advs,
+                                const double* rets, const double* oldlps, const double* terms,
+                                const double* oldvals, size_t T, size_t H, size_t D, size_t L, size_t A,
+                                const int* sizes, size_t K, double vfCoef, double entCoef, double clipEps,
+                                double vfClip, double* out);
 /* Log-space (Heinsen) parallel-scan form of the MinGRU layer recurrence for one sequence with zero
  * initial state and no resets: given gate/hid pre-activations (T x H) returns o (T x H)
  * (Puffer/Net/MinGRU.lean:116-168; tools/mingru_ref.py:113-154). */

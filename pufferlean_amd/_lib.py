@@ -68,6 +68,7 @@ SIGNATURES: dict[str, list] = {
     "ph_gclip": [vp, sz, flt, flt, vp],
     "ph_mingru_param_count": [vp],
     "ph_mingru_ppo_grad": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "ph_mingru_ppo_grad_md": [vp, vp, vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_mingru_muon": [vp, vp, vp, vp, vp, vp],
     "ph_mingru_step": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_seg_l1": [vp, vp, vp],
@@ -111,8 +112,8 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_mlp_forward_batch_bf16": [dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_ffi_bench_bf16_resident": [sz, sz, sz, sz],
     "ph_ffi_cuda_available": [],
-    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl,
-                                dptr, sz, dptr, sz, dptr],
+    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dptr, sz, dbl, dbl, dbl,
+                                dbl, dptr, sz, dptr, sz, dptr],
     "ph_cuda_mg_prep": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz],
     "ph_cuda_mg_cols_ready": [sz, sz, C.POINTER(C.c_uint8)],
     "ph_cuda_mg_obs_traj": [dptr, sz, sz, sz],

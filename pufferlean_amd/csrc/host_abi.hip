@@ -1335,21 +1335,32 @@ extern "C" int ph_ffi_gather_seq_minibatch(const double* obsCol, const double* a
 // this library does not run. Writes out[P + 2*T*B] = [summed gradient | new_logp | new_value].
 extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
                                        size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L,
-                                       size_t A, size_t K, double vfCoef, double entCoef, double clipEps,
-                                       double vfClip, const double* segIdx, size_t nseg, const double* mbPrio,
-                                       size_t nprio, double* out) {
-  PH_REQUIRE(K <= 1, "ph_cuda_mingru_ppo_grad: multi-discrete heads (K=%zu) are not supported", K);
-  const size_t TB = T * B;
+                                       size_t A, size_t K, const double* hs, size_t nhs, double vfCoef,
+                                       double entCoef, double clipEps, double vfClip, const double* segIdx,
+                                       size_t nseg, const double* mbPrio, size_t nprio, double* out) {
+  // K > 1: A is the logits width (the sum of the K head sizes in hs) and the action column is K wide
+  // (puffercuda.cu:5202-5205, 5216-5220)
+  const size_t Kh = K < 1 ? 1 : K;
+  HeadSizes heads{};
+  if (Kh > 1) {
+    PH_REQUIRE(hs && nhs >= Kh, "ph_cuda_mingru_ppo_grad: %zu head sizes for K=%zu heads", nhs, Kh);
+    size_t W = 0;
+    PH_TRY(sizes_from(hs, Kh, heads.n, W, "ph_cuda_mingru_ppo_grad"));
+    heads.K = (int)Kh;
+    PH_REQUIRE(W == A, "ph_cuda_mingru_ppo_grad: head sizes sum to %zu, A=%zu", W, A);
+  }
+  const size_t TB = T * B, NS = (Kh + 5) * TB;  // scal: [act (K per row) | adv | ret | old | term | ov]
   int dev = -1;
   const bool prioRes = nseg == 0 && nprio == 0 && g_dc.prio_fresh && g_dc.prioB == (long)B;
   g_dc.prio_fresh = false;
   if (prioRes || (nseg > 0 && nprio > 0)) PH_CHECK_HIP(hipGetDevice(&dev));
+  // a K-wide action column is gathered only from resident columns of the same width
   const bool devCol = (prioRes || (nseg > 0 && nprio > 0)) && g_dc.valid && g_dc.T == (long)T &&
-                      g_dc.K == 1 && g_dc.dev == dev;
-  PH_REQUIRE(devCol || nscal >= 6 * TB,
+                      g_dc.K == (long)Kh && g_dc.dev == dev;
+  PH_REQUIRE(devCol || nscal >= NS,
              "ph_cuda_mingru_ppo_grad: no scalar source: scal holds %zu of %zu values and the device-column "
              "mode is off (needs segIdx+mbPrio or a fresh ph_cuda_mg_vtrace_prio draw, and resident columns "
-             "for T=%zu)", nscal, 6 * TB, T);
+             "for T=%zu, K=%zu)", nscal, NS, T, Kh);
   // empty obs: gather the minibatch from the resident obs trajectory by the drawn segments
   // (puffercuda.cu:5226-5230, 5362-5363), which needs segment indices and a trajectory of these shapes
   const bool useTraj = nobs == 0 && devCol && g_traj.valid && g_traj.dev == dev && g_traj.N == g_dc.N &&
@@ -1372,10 +1383,10 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   float *pf, *xf, *sf, *G, *nlp, *nv;
   int *act, *segi;
   PH_TRY(carve(kHsMg, [&](Carve& cv) {
-    dp = cv.take<double>(P); dx = cv.take<double>(TB * D); ds = cv.take<double>(6 * TB);
+    dp = cv.take<double>(P); dx = cv.take<double>(TB * D); ds = cv.take<double>(NS);
     losses = cv.take<double>(8); pf = cv.take<float>(P); xf = cv.take<float>(TB * D);
-    sf = cv.take<float>(6 * TB); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
-    act = cv.take<int>(TB); segd = cv.take<double>(B); mpd = cv.take<double>(B); segi = cv.take<int>(B);
+    sf = cv.take<float>(NS); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
+    act = cv.take<int>(Kh * TB); segd = cv.take<double>(B); mpd = cv.take<double>(B); segi = cv.take<int>(B);
   }));
   PH_TRY(up(dp, params, P * 8));
   if (!useTraj) PH_TRY(up(dx, obs, TB * D * 8));
@@ -1395,7 +1406,7 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
     const ph_replay_cols cols = dc_cols();
     PH_TRY(mb_gather(cols, seg, mp, B, ds, nullptr, nullptr));
   } else {
-    PH_TRY(up(ds, scal, 6 * TB * 8));
+    PH_TRY(up(ds, scal, NS * 8));
   }
   PH_TRY(to_f32(dp, pf, P, nullptr));
   if (useTraj) {
@@ -1404,11 +1415,16 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   } else {
     PH_TRY(to_f32(dx, xf, (long)(TB * D), nullptr));
   }
-  PH_TRY(to_f32(ds, sf, (long)(6 * TB), nullptr));
-  k_f64_i32<<<ceil_div(TB, kT), kT>>>(ds, act, (long)TB);
+  PH_TRY(to_f32(ds, sf, (long)NS, nullptr));
+  k_f64_i32<<<ceil_div(Kh * TB, kT), kT>>>(ds, act, (long)(Kh * TB));
   PH_LAUNCH_CHECK();
-  PH_TRY(ph_mingru_ppo_grad(&d, &c, pf, xf, act, sf + TB, sf + 2 * TB, sf + 3 * TB, sf + 5 * TB, sf + 4 * TB, G,
-                            nlp, nv, g_mgLossOn ? losses : nullptr, nullptr));
+  const float* sc = sf + Kh * TB;  // adv | ret | old | term | ov
+  if (Kh > 1)
+    PH_TRY(ph_mingru_ppo_grad_md(&d, &c, heads.n, Kh, pf, xf, act, sc, sc + TB, sc + 2 * TB, sc + 4 * TB,
+                                 sc + 3 * TB, G, nlp, nv, g_mgLossOn ? losses : nullptr, nullptr));
+  else
+    PH_TRY(ph_mingru_ppo_grad(&d, &c, pf, xf, act, sc, sc + TB, sc + 2 * TB, sc + 4 * TB, sc + 3 * TB, G, nlp, nv,
+                              g_mgLossOn ? losses : nullptr, nullptr));
   if (devCol) {
     const ph_replay_cols cols = dc_cols();
     PH_TRY(mb_iterate(cols, seg, B, nlp, nv, nullptr));

@@ -337,8 +337,11 @@ PhGemmDesc gd(int ta, int tb, int M, int N, int K, int adt, const void* A, long 
 
 // Forward + backward over one minibatch: writes the summed gradient G[P] and new_logp/new_value.
 // TS: activation / weight-copy storage (uint16_t = bf16 with bf16 MFMA, float = fp32 MFMA).
+// heads NULL: one categorical head over the A logits (act [TB]); otherwise K categorical heads whose
+// sizes sum to A (act [TB][K]), the only difference being the loss kernel on the head rows
+// (puffercuda.cu:5202-5205: the BPTT is generic in the logits width).
 template <typename TS>
-int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float* params,
+int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const HeadSizes* heads, const float* params,
                       const float* obs, const int* act, const float* advn, const float* ret,
                       const float* oldlp, const float* oldval, const float* done, float* G,
                       float* newlp, float* newval, double* losses, hipStream_t st) {
@@ -393,8 +396,12 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const floa
     PH_TRY(gemm(g, st));
   }
   // fused PPO loss: dlogits into dl[:, :A], dvalue into dl[:, A]
-  PH_TRY(ppo_grad(b.logit, HP, b.logit + A, HP, act, advn, ret, oldlp, oldval, TB, A, c.vf_coef,
-                  c.ent_coef, c.clip_eps, c.vf_clip, 1, b.dl, HP, b.dl + A, HP, newlp, newval, losses, st));
+  if (heads)
+    PH_TRY(ppo_grad_md(b.logit, HP, act, advn, ret, oldlp, oldval, TB, heads->n, heads->K, c.vf_coef, c.ent_coef,
+                       c.clip_eps, c.vf_clip, b.dl, HP, newlp, newval, losses, st));
+  else
+    PH_TRY(ppo_grad(b.logit, HP, b.logit + A, HP, act, advn, ret, oldlp, oldval, TB, A, c.vf_coef,
+                    c.ent_coef, c.clip_eps, c.vf_clip, 1, b.dl, HP, b.dl + A, HP, newlp, newval, losses, st));
   // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh
   {
     PhGemmDesc g = gd(1, 0, HP, H, (int)TB, PH_F32, b.dl, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
@@ -440,7 +447,7 @@ long mingru_param_count(const ph_mingru_dims& d) {
   return (long)d.H * d.D + d.H + (long)d.L * 3 * d.H * d.H + (long)d.A * d.H + d.A + d.H + 1;
 }
 
-int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float* params,
+int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const HeadSizes* heads, const float* params,
                     const float* obs, const int* act, const float* advn, const float* ret,
                     const float* oldlp, const float* oldval, const float* done, float* G,
                     float* newlp, float* newval, double* losses, hipStream_t st) {
@@ -450,10 +457,16 @@ int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const float*
   PH_REQUIRE(d.precision == 0 || d.precision == 1, "mingru: precision must be 0 (bf16) or 1 (fp32)");
   PH_REQUIRE(d.L <= kLanes - 3, "mingru: at most %d layers", kLanes - 3);
   PH_REQUIRE((long)d.T * d.B <= INT32_MAX, "mingru: T*B exceeds int32");
+  if (heads) {
+    int W = 0;
+    for (int h = 0; h < heads->K; h++) W += heads->n[h];
+    PH_REQUIRE(heads->K >= 1 && heads->K <= kMaxHeads && W == d.A,
+               "mingru: %d head sizes summing to %d for %d logits", heads->K, W, d.A);
+  }
   if (d.precision == 1)
-    return mingru_ppo_grad_t<float>(d, c, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
+    return mingru_ppo_grad_t<float>(d, c, heads, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
                                     newval, losses, st);
-  return mingru_ppo_grad_t<uint16_t>(d, c, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
+  return mingru_ppo_grad_t<uint16_t>(d, c, heads, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
                                      newval, losses, st);
 }
 
@@ -498,7 +511,7 @@ int mingru_step(const ph_mingru_dims& d, const ph_ppo_coefs& c, const ph_muon_co
                     c.lam, c.rho_clip, c.c_clip, b.adv, b.tgt, st));
   // minibatch advantage normalisation
   PH_TRY(moments_normalize(PH_F32, b.adv, TB, b.advn, b.stats, st));
-  PH_TRY(mingru_ppo_grad(d, c, params, obs, act, b.advn, b.tgt, oldlp, oldval, done, G, b.newlp,
+  PH_TRY(mingru_ppo_grad(d, c, nullptr, params, obs, act, b.advn, b.tgt, oldlp, oldval, done, G, b.newlp,
                          b.newval, losses, st));
   PH_TRY(mingru_muon(d, m, params, mom, G, st));
   return PH_OK;
@@ -515,8 +528,25 @@ extern "C" int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c
                                   const float* oldlp, const float* oldval, const float* done, float* G,
                                   float* newlp, float* newval, double* losses, void* stream) {
   PH_REQUIRE(d && c, "ph_mingru_ppo_grad: null config");
-  return mingru_ppo_grad(*d, *c, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval,
+  return mingru_ppo_grad(*d, *c, nullptr, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval,
                          losses, as_stream(stream));
+}
+
+extern "C" int ph_mingru_ppo_grad_md(const ph_mingru_dims* d, const ph_ppo_coefs* c, const int* head_sizes,
+                                     size_t K, const float* params, const float* obs, const int* act,
+                                     const float* adv, const float* ret, const float* oldlp, const float* oldval,
+                                     const float* done, float* G, float* newlp, float* newval, double* losses,
+                                     void* stream) {
+  PH_REQUIRE(d && c && head_sizes, "ph_mingru_ppo_grad_md: null config");
+  PH_REQUIRE(K >= 1 && K <= (size_t)kMaxHeads, "ph_mingru_ppo_grad_md: K=%zu heads (1..%d)", K, kMaxHeads);
+  HeadSizes hs;
+  hs.K = (int)K;
+  for (size_t h = 0; h < K; h++) {
+    PH_REQUIRE(head_sizes[h] >= 1, "ph_mingru_ppo_grad_md: head %zu has %d actions", h, head_sizes[h]);
+    hs.n[h] = head_sizes[h];
+  }
+  return mingru_ppo_grad(*d, *c, &hs, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval, losses,
+                         as_stream(stream));
 }
 
 extern "C" int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params,

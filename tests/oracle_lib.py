@@ -44,6 +44,8 @@ _SIG = {
     "orc_gclip": ([vp, sz, d, d], d),
     "orc_mingru_ppo_grad_seq": ([vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d, d, d, d,
                                  vp], None),
+    "orc_mingru_ppo_grad_seq_md": ([vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, vp, sz, d, d, d, d, vp],
+                                    None),
     "orc_mingru_heinsen": ([vp, vp, sz, sz, vp], None),
     "orc_seg_l1": ([vp, sz, sz, vp], None),
     "orc_prio_sample": ([vp, sz, sz, d, d, C.c_uint64, vp, vp, vp, vp], None),

@@ -5,6 +5,7 @@ No compute calls here: only loading, symbol lookup and the calls that need no de
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from pufferlean_amd import _lib as L
@@ -63,9 +64,12 @@ def test_host_entries_reject_bad_arguments_without_device():
     # argument checks run before any device work
     import ctypes as C
     lib = L.lib()
-    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, 0.5, 0.01, 0.2, 0.0,
-                                       None, 0, None, 0, None) == L.PH_ERR_ARG
-    assert b"multi-discrete" in lib.ph_last_error()
+    hs = np.array([1.0, 1.0])  # two heads summing to 2, not A = 3
+    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, hs.ctypes.data_as(L.dptr), 2,
+                                       0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None) == L.PH_ERR_ARG
+    assert b"head sizes sum to 2" in lib.ph_last_error()
+    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, None, 0,
+                                       0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None) == L.PH_ERR_ARG
     assert lib.ph_cuda_policy_download(0, 4, None) == L.PH_ERR_ARG
 
 

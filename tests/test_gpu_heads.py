@@ -368,3 +368,93 @@ def test_train_update_wide_resident_matches_oracle_chain(gpu, mode, vfclip, mgn)
     assert rel(res[:Pn] - pm0[:Pn], ref[:Pn] - pm0[:Pn]) < 1e-4
     assert rel(res[Pn:], ref[Pn:]) < 1e-4
     np.testing.assert_allclose(losses, refL, rtol=1e-4, atol=2.0 / (NT // numMB))
+
+
+# ---- MinGRU gradient with multi-discrete heads -----------------------------------------------------
+def _mg_md_oracle(p, obs, act, adv, ret, old, term, ov, T, B, H, D, Ln, W, sizes):
+    """Sum over the B sequences of the oracle's K-head sequence gradient; act [T][B][K]."""
+    Pn = p.size
+    g, nlp = np.zeros(Pn), np.zeros((T, B))
+    for b in range(B):
+        o = np.zeros(Pn + 2 * T)
+        O.lib().orc_mingru_ppo_grad_seq_md(O.P(p), O.P(O.f64(obs[:, b, :])), O.P(O.f64(act[:, b, :])),
+                                           O.P(O.f64(adv[:, b])), O.P(O.f64(ret[:, b])), O.P(O.f64(old[:, b])),
+                                           O.P(O.f64(term[:, b])), O.P(O.f64(ov[:, b])), T, H, D, Ln, W,
+                                           O.P(np.ascontiguousarray(sizes, np.int32)), len(sizes), 0.5, 0.01, 0.2,
+                                           0.2, O.P(o))
+        g += o[:Pn]
+        nlp[:, b] = o[Pn:Pn + T]
+    return g, nlp
+
+
+# fp32 products: the parity bar. bf16 products: 5e-2, wider than the single-head 2e-2 because the joint
+# log-prob sums the K heads' bf16 logit errors before the ratio is formed (the reference records the
+# same for its bf16 multi-discrete tier, puffercuda.cu:4946-4951); 4.1 % measured on this case.
+@pytest.mark.parametrize("prec,tol", [("f32", 1e-5), ("bf16", 5e-2)])
+def test_mingru_md_host_mode_matches_oracle(gpu, monkeypatch, prec, tol):
+    if prec == "bf16":
+        monkeypatch.setenv("PUFFER_MG_PREC", "bf16")
+    else:
+        monkeypatch.delenv("PUFFER_MG_PREC", raising=False)
+    sizes = [3, 4, 2]
+    B, T, D, H, Ln, K = 8, 16, 8, 32, 2, 3
+    W = sum(sizes)
+    n = B * T
+    Pn = H * D + H + Ln * 3 * H * H + W * H + W + H + 1
+    p = rng.normal(0xB31, Pn) * 0.3
+    obs = rng.normal(0xB32, n * D).reshape(T, B, D)
+    act = np.stack([rng.randint(0xB33 + h, n, s) for h, s in enumerate(sizes)], 1).reshape(T, B, K).astype(np.float64)
+    adv, ret = rng.normal(0xB37, n).reshape(T, B), rng.normal(0xB38, n).reshape(T, B)
+    old = rng.randf(0xB39, n, -4.0, -2.5).reshape(T, B)
+    term = rng.bernoulli(0xB3A, n, 0.05).reshape(T, B)
+    ov = rng.normal(0xB3B, n).reshape(T, B)
+    scal = np.concatenate([act.ravel()] + [a.ravel() for a in (adv, ret, old, term, ov)])
+    out = np.zeros(Pn + 2 * n)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), scal.size, B, T, H, D, Ln, W, K,
+           dp(np.array(sizes, np.float64)), K, 0.5, 0.01, 0.2, 0.2, None, 0, None, 0, dp(out))
+    g, nlp = _mg_md_oracle(p, obs, act, adv, ret, old, term, ov, T, B, H, D, Ln, W, sizes)
+    assert rel(out[:Pn], g) < tol
+    assert rel(out[Pn:Pn + n], nlp.ravel()) < tol
+
+
+def test_mingru_md_device_column_mode(gpu, monkeypatch):
+    """K-wide resident columns: the device gather of the drawn segments feeds the same gradient as the
+    host form built from the oracle's gather (actions indexed by the draws)."""
+    monkeypatch.delenv("PUFFER_MG_PREC", raising=False)
+    sizes = [3, 4]
+    N, T, B, D, H, Ln, K = 32, 8, 12, 8, 16, 2, 2
+    W = sum(sizes)
+    n = N * T
+    Pn = H * D + H + Ln * 3 * H * H + W * H + W + H + 1
+    p = rng.normal(0xB41, Pn) * 0.3
+    rew, term = rng.normal(0xB42, n), rng.bernoulli(0xB43, n, 0.05)
+    act = np.stack([rng.randint(0xB44 + h, n, s) for h, s in enumerate(sizes)], 1).astype(np.float64)  # [N*T][K]
+    logp, val, boot = rng.randf(0xB46, n, -3.5, -2.0), rng.normal(0xB47, n), rng.normal(0xB48, N)
+    obs_roll = rng.normal(0xB49, n * D).reshape(N, T, D)
+    L.call("ph_cuda_mg_prep", dp(rew), dp(term), dp(act), dp(logp), dp(val), dp(boot), N, T, K)
+    L1 = np.zeros(N)
+    L.call("ph_cuda_mg_vtrace", N, T, 0.99, 0.95, 1.0, 1.0, dp(L1))
+    adv = np.zeros(n)
+    O.lib().orc_vtrace_mingru(O.P(rew), O.P(val), O.P(term), O.P(np.ones(n)), O.P(boot), N, T, 0.99, 0.95, 1.0, 1.0,
+                              O.P(adv))
+    idx, mp = np.zeros(B), np.zeros(B)
+    L.call("ph_ffi_prio_sample", dp(L1), N, T, B, 0.8, 0.3, 0x5151, dp(idx), dp(mp))
+    scal1, _ = O.gather_seq_minibatch(np.zeros(n), logp, term, adv, val, idx, mp, T)  # [act | adv | ret | old | term | ov]
+    e = idx.astype(np.int64)
+    act_mb = act.reshape(N, T, K)[e].transpose(1, 0, 2)  # [T][B][K]
+    scal = np.concatenate([act_mb.ravel(), scal1[T * B:]])
+    obs = np.ascontiguousarray(obs_roll[e].transpose(1, 0, 2))
+    hs = np.array(sizes, np.float64)
+    args = (B, T, H, D, Ln, W, K, dp(hs), K, 0.5, 0.01, 0.2, 0.2)
+    out_host = np.zeros(Pn + 2 * T * B)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
+           dp(out_host))
+    out_dev = np.zeros_like(out_host)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B, dp(out_dev))
+    assert rel(out_dev, out_host) < 1e-5
+    # a K-wide call does not gather from columns of another width
+    L.call("ph_cuda_mg_prep", dp(rew), dp(term), dp(act[:, 0].copy()), dp(logp), dp(val), dp(boot), N, T, 1)
+    L.call("ph_cuda_mg_vtrace", N, T, 0.99, 0.95, 1.0, 1.0, dp(L1))
+    with pytest.raises(L.PufferHipError, match="no scalar source"):
+        L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
+               dp(out_dev))

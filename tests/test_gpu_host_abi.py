@@ -376,8 +376,8 @@ def test_mingru_grad_host_mode_matches_oracle(gpu, monkeypatch):
     ov = rng.normal(0x1A8, n).reshape(T, B)
     scal = np.concatenate([a.ravel() for a in (act, adv, ret, old, term, ov)])
     out = np.zeros(Pn + 2 * n)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), 6 * n, B, T, H, D, Ln, A, 1, 0.5, 0.01, 0.2,
-           0.2, None, 0, None, 0, dp(out))
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), 6 * n, B, T, H, D, Ln, A, 1, None, 0, 0.5,
+           0.01, 0.2, 0.2, None, 0, None, 0, dp(out))
     g = np.zeros(Pn)
     nlp = np.zeros((T, B))
     for b in range(B):

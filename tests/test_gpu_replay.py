@@ -292,7 +292,7 @@ def test_mg_chain_device_columns_match_host_path(gpu, monkeypatch):
     L.call("ph_ffi_gather_seq_minibatch", None, dp(act), dp(logp), dp(term), dp(adv), dp(val), dp(idx), dp(mp),
            T, B, Dm, N, dp(scal))
     obs = np.ascontiguousarray(obs_roll[idx.astype(np.int64)].transpose(1, 0, 2))  # [T][B][D]
-    args = (B, T, H, Dm, Ln, A, 1, 0.5, 0.01, 0.2, 0.2)
+    args = (B, T, H, Dm, Ln, A, 1, None, 0, 0.5, 0.01, 0.2, 0.2)
     out_host = np.zeros(Pn + 2 * T * B)
     L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
            dp(out_host))

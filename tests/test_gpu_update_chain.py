@@ -100,8 +100,8 @@ def test_mingru_update_chain_matches_oracle(gpu, monkeypatch):
             L.call("ph_cuda_mg_vtrace_prio", N, T, gam, lam, rc, cc, mbSegs, alpha, beta, state, C.byref(used))
             assert used.value == 1
             out = np.zeros(P + 2 * T * mbSegs)
-            L.call("ph_cuda_mingru_ppo_grad", dp(wflat), None, 0, None, 0, mbSegs, T, H, Dm, Lr, A, 1, vf, ent, clip,
-                   vfclip, None, 0, None, 0, dp(out))
+            L.call("ph_cuda_mingru_ppo_grad", dp(wflat), None, 0, None, 0, mbSegs, T, H, Dm, Lr, A, 1, None, 0, vf,
+                   ent, clip, vfclip, None, 0, None, 0, dp(out))
             sc = 1.0 / (mbSegs * T)
             gclip = grad_clip(out[:P], maxgn, sc)
             wout = np.zeros(P)

@@ -263,3 +263,77 @@ def test_cont_losses_against_scipy_normal():
     for k in (0, 1, 4, 5, 6):
         np.testing.assert_allclose(got[k], ref[k], rtol=1e-9, atol=1e-12, err_msg=str(k))
     np.testing.assert_allclose(got[3], got[0] + 0.5 * got[1] - 0.01 * got[2], rtol=1e-14)
+
+
+# ---- MinGRU sequence gradient with multi-discrete heads ------------------------------------------
+def _mg_layout(H, D, L, A):
+    szE, szL = H * D, 3 * H * H
+    offDec = szE + H + L * szL
+    return offDec, offDec + A * H, offDec + A * H + A  # wDec, bDec, wVal offsets
+
+
+def _mg_seq(p, obs, acts, advs, rets, olds, terms, ovs, T, H, D, L, A, sizes=None, vfclip=0.2):
+    P = p.size
+    out = np.zeros(P + 2 * T)
+    f = lambda a: np.ascontiguousarray(a, np.float64)
+    if sizes is None:
+        O.lib().orc_mingru_ppo_grad_seq(O.P(f(p)), O.P(f(obs)), O.P(f(acts)), O.P(f(advs)), O.P(f(rets)),
+                                        O.P(f(olds)), O.P(f(terms)), O.P(f(ovs)), T, H, D, L, A, 0.5, 0.01, 0.2,
+                                        vfclip, O.P(out))
+    else:
+        O.lib().orc_mingru_ppo_grad_seq_md(O.P(f(p)), O.P(f(obs)), O.P(f(acts)), O.P(f(advs)), O.P(f(rets)),
+                                           O.P(f(olds)), O.P(f(terms)), O.P(f(ovs)), T, H, D, L, A,
+                                           O.P(np.ascontiguousarray(sizes, np.int32)), len(sizes), 0.5, 0.01, 0.2,
+                                           vfclip, O.P(out))
+    return out[:P], out[P:P + T], out[P + T:]
+
+
+def test_mingru_md_two_heads_equal_product_head():
+    """Heads of sizes 3 and 4 are one categorical head over the 12 pairs with decoder rows
+    W1[i] + W2[j] (and biases b1[i] + b2[j]): the same joint log-probs, the same gradients of every
+    shared layer, and each head's decoder gradient the product's summed over the other head."""
+    H, D, L, T, s1, s2 = 16, 8, 2, 12, 3, 4
+    W, A2 = s1 + s2, s1 * s2
+    P_md = H * D + H + L * 3 * H * H + W * H + W + H + 1
+    p = rng.normal(0x9A1, P_md) * 0.3
+    dec, bdec, val = _mg_layout(H, D, L, W)
+    W1, W2 = p[dec:dec + s1 * H].reshape(s1, H), p[dec + s1 * H:bdec].reshape(s2, H)
+    b1, b2 = p[bdec:bdec + s1], p[bdec + s1:val]
+    Wp = (W1[:, None, :] + W2[None, :, :]).reshape(A2, H)
+    bp = (b1[:, None] + b2[None, :]).reshape(A2)
+    pp = np.concatenate([p[:dec], Wp.ravel(), bp, p[val:]])
+    obs = rng.normal(0x9A2, T * D)
+    a1, a2 = rng.randint(0x9A3, T, s1), rng.randint(0x9A4, T, s2)
+    advs, rets, ovs = rng.normal(0x9A5, T), rng.normal(0x9A6, T), rng.normal(0x9A7, T, 0.0, 0.5)
+    olds = rng.normal(0x9A8, T, -2.3, 0.4)
+    terms = np.zeros(T)
+    terms[5] = 1.0
+    g, nlp, nv = _mg_seq(p, obs, np.stack([a1, a2], 1).astype(np.float64), advs, rets, olds, terms, ovs, T, H, D, L,
+                         W, sizes=[s1, s2])
+    gp, nlpp, nvp = _mg_seq(pp, obs, (a1 * s2 + a2).astype(np.float64), advs, rets, olds, terms, ovs, T, H, D, L,
+                            A2)
+    np.testing.assert_allclose(nlp, nlpp, rtol=1e-12, atol=1e-14)
+    np.testing.assert_array_equal(nv, nvp)
+    dec2, bdec2, val2 = _mg_layout(H, D, L, A2)
+    np.testing.assert_allclose(g[:dec], gp[:dec2], rtol=1e-9, atol=1e-12)          # encoder and layers
+    np.testing.assert_allclose(g[val:], gp[val2:], rtol=1e-9, atol=1e-12)          # value head
+    gW = gp[dec2:bdec2].reshape(s1, s2, H)
+    gb = gp[bdec2:val2].reshape(s1, s2)
+    np.testing.assert_allclose(g[dec:dec + s1 * H].reshape(s1, H), gW.sum(1), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(g[dec + s1 * H:bdec].reshape(s2, H), gW.sum(0), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(g[bdec:bdec + s1], gb.sum(1), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(g[bdec + s1:val], gb.sum(0), rtol=1e-9, atol=1e-12)
+
+
+def test_mingru_md_single_head_equals_categorical():
+    H, D, L, T, A = 16, 8, 1, 9, 5
+    P = H * D + H + L * 3 * H * H + A * H + A + H + 1
+    p = rng.normal(0x9B1, P) * 0.3
+    obs = rng.normal(0x9B2, T * D)
+    acts = rng.randint(0x9B3, T, A).astype(np.float64)
+    advs, rets, ovs = rng.normal(0x9B4, T), rng.normal(0x9B5, T), rng.normal(0x9B6, T)
+    olds, terms = rng.normal(0x9B7, T, -1.5, 0.3), np.zeros(T)
+    g, nlp, _ = _mg_seq(p, obs, acts[:, None], advs, rets, olds, terms, ovs, T, H, D, L, A, sizes=[A])
+    gc, nlpc, _ = _mg_seq(p, obs, acts, advs, rets, olds, terms, ovs, T, H, D, L, A)
+    np.testing.assert_allclose(g, gc, rtol=1e-10, atol=1e-13)
+    np.testing.assert_allclose(nlp, nlpc, rtol=1e-12)
