@@ -86,6 +86,19 @@ int transpose_bf16(const uint16_t* X, uint16_t* Xt, int rows, int cols, hipStrea
 int muon_mat_exact(int rows, int cols, const double* W, const double* G, const double* M, double* nW,
                    double* nM, double gscale, double lr, double wd, double mu, double eps,
                    const double* coeffs, int nsteps, hipStream_t st);
+// One matrix of a batched exact-tier step (nW/nM may alias W/M; c2 is set by the driver).
+struct ExactMat {
+  const double* W;
+  const double* G;
+  const double* M;
+  double* nW;
+  double* nM;
+  int rows, cols;
+  double c2;
+};
+constexpr int kExactBatchMax = 4;
+int muon_mat_exact_batch(const ExactMat* mats, int n, double gscale, double lr, double wd, double mu, double eps,
+                         const double* coeffs, int nsteps, hipStream_t st);
 int stepvec_exact(long n, const double* b, const double* g, const double* m, double* nb, double* nm,
                   double gscale, double lr, double wd, double mu, hipStream_t st);
 int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,

@@ -265,11 +265,22 @@ struct ExactCoeffs {
   double v[3 * kExactFusedMaxSteps];
 };
 
-__global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, const double* __restrict__ G,
-                                                           const double* M, double* nW, double* nM, int rows,
-                                                           int cols, double gscale, double mu, double eps,
-                                                           ExactCoeffs cf, int nsteps, double c1, double c2) {
+struct ExactBatch {
+  ExactMat m[kExactBatchMax];
+};
+
+// One workgroup per matrix of the batch (they are independent, so they run side by side).
+__global__ void __launch_bounds__(1024) k_muon_exact_fused(ExactBatch bt, double gscale, double mu, double eps,
+                                                           ExactCoeffs cf, int nsteps, double c1) {
 #pragma clang fp contract(off)
+  const ExactMat& mt = bt.m[blockIdx.x];
+  const double* W = mt.W;
+  const double* G = mt.G;
+  const double* M = mt.M;
+  double* nW = mt.nW;
+  double* nM = mt.nM;
+  const int rows = mt.rows, cols = mt.cols;
+  const double c2 = mt.c2;
   extern __shared__ double lds[];
   const int n = rows * cols, T = blockDim.x, tid = threadIdx.x;
   const bool wide = rows <= cols;
@@ -367,7 +378,29 @@ __global__ void __launch_bounds__(1024) k_muon_exact_fused(const double* W, cons
 
 }  // namespace
 
-// ---- exact tier host driver: one matrix, device f64 buffers ------------------------------------
+// ---- exact tier host drivers: device f64 buffers --------------------------------------------------
+// Matrices whose iterate, product and Gram matrix fit the LDS budget, in one launch of one workgroup
+// each; PH_ERR_UNSUPPORTED (nothing launched) when one does not fit or the batch is too large.
+int muon_mat_exact_batch(const ExactMat* mats, int n, double gscale, double lr, double wd, double mu, double eps,
+                         const double* coeffs, int nsteps, hipStream_t st) {
+  if (n < 1 || n > kExactBatchMax || nsteps > kExactFusedMaxSteps) return PH_ERR_UNSUPPORTED;
+  ExactBatch bt{};
+  long lds = 0;
+  for (int i = 0; i < n; i++) {
+    const ExactMat& m = mats[i];
+    const long e = (long)m.rows * m.cols, mn = m.rows < m.cols ? m.rows : m.cols;
+    if (e == 0 || 2 * e + mn * mn > kExactFusedLds) return PH_ERR_UNSUPPORTED;
+    if (2 * e + mn * mn > lds) lds = 2 * e + mn * mn;
+    bt.m[i] = m;
+    bt.m[i].c2 = lr * sqrt(fmax(1.0, (double)m.rows / (double)m.cols));
+  }
+  ExactCoeffs cf{};
+  for (int i = 0; i < 3 * nsteps; i++) cf.v[i] = coeffs[i];
+  k_muon_exact_fused<<<n, 1024, (size_t)lds * 8, st>>>(bt, gscale, mu, eps, cf, nsteps, 1.0 - lr * wd);
+  PH_LAUNCH_CHECK();
+  return PH_OK;
+}
+
 int muon_mat_exact(int rows, int cols, const double* W, const double* G, const double* M, double* nW,
                    double* nM, double gscale, double lr, double wd, double mu, double eps,
                    const double* coeffs, int nsteps, hipStream_t st) {
@@ -375,13 +408,10 @@ int muon_mat_exact(int rows, int cols, const double* W, const double* G, const d
   if (n == 0) return PH_OK;
   const int mn = rows < cols ? rows : cols;
   const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
-  if (2 * n + (long)mn * mn <= kExactFusedLds && nsteps <= kExactFusedMaxSteps) {
-    ExactCoeffs cf{};
-    for (int i = 0; i < 3 * nsteps; i++) cf.v[i] = coeffs[i];
-    k_muon_exact_fused<<<1, 1024, (size_t)(2 * n + (long)mn * mn) * 8, st>>>(
-        W, G, M, nW, nM, rows, cols, gscale, mu, eps, cf, nsteps, 1.0 - lr * wd, lr * scale);
-    PH_LAUNCH_CHECK();
-    return PH_OK;
+  {
+    const ExactMat one{W, G, M, nW, nM, rows, cols, 0.0};
+    const int r = muon_mat_exact_batch(&one, 1, gscale, lr, wd, mu, eps, coeffs, nsteps, st);
+    if (r != PH_ERR_UNSUPPORTED) return r;
   }
   double* ws = (double*)scratch(kSlotMuonExact, (size_t)(6 * n + (long)mn * mn + rows + 8) * 8);
   if (!ws) return PH_ERR_NOMEM;
