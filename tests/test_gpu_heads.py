@@ -458,3 +458,34 @@ def test_mingru_md_device_column_mode(gpu, monkeypatch):
     with pytest.raises(L.PufferHipError, match="no scalar source"):
         L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
                dp(out_dev))
+
+
+def test_mingru_rollout_step_then_multi_discrete_draw(gpu):
+    """The MinGRU rollout step with W = sum of head sizes logits (its rows are [logits | value]) feeds the
+    multi-discrete sampler directly: draws and joint log-probs against the oracle's step and sampler."""
+    sizes = [3, 4, 2]
+    N, Dm, H, Lr = 512, 16, 64, 2
+    W = sum(sizes)
+    P = H * Dm + H + Lr * 3 * H * H + W * H + W + H + 1
+    params = rng.normal(0xB51, P) * 0.3 / np.sqrt(max(Dm, H) / 8)
+    obs = rng.normal(0xB52, N * Dm).reshape(N, Dm)
+    dims = L.MinGRUDims(N, 1, Dm, H, Lr, W, 1)  # fp32 products
+    gp, gobs = cu(params), cu(obs)
+    state = torch.zeros(N * Lr * H, device="cuda")
+    out = torch.empty(N, W + 1, device="cuda")
+    draws = torch.empty((len(sizes) + 2) * N, device="cuda", dtype=torch.float64)
+    hs = (C.c_int * len(sizes))(*sizes)
+    L.call("ph_mingru_rollout_step", C.byref(dims), vp(gp), vp(gobs), vp(state), vp(out), st())
+    L.call("ph_sample_actions_md", L.PH_F32, vp(out), W + 1, N, hs, len(sizes), 0x4242, vp(draws), st())
+    torch.cuda.synchronize()
+    ref_out, _ = O.mingru_step(params.astype(np.float32).astype(np.float64),
+                               obs.astype(np.float32).astype(np.float64), np.zeros((N, Lr, H)), N, Dm, H, Lr, W)
+    y = out.cpu().numpy().astype(np.float64)
+    assert rel(y, ref_out) < 1e-5
+    got, ref = draws.cpu().numpy(), O.sample_md(y, sizes, 0x4242)  # the sampler on the device's own rows
+    K = len(sizes)
+    bad = sum(int(np.sum(got[h * N:(h + 1) * N] != ref[h * N:(h + 1) * N])) for h in range(K))
+    assert bad <= max(1, N // 500)
+    ok = np.all(np.stack([got[h * N:(h + 1) * N] == ref[h * N:(h + 1) * N] for h in range(K)]), axis=0)
+    assert np.allclose(got[K * N:(K + 1) * N][ok], ref[K * N:(K + 1) * N][ok], rtol=1e-5, atol=1e-5)
+    assert np.array_equal(got[(K + 1) * N:], ref[(K + 1) * N:])
