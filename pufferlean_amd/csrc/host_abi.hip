@@ -359,14 +359,12 @@ int stepvec_f64(long n, double* b, const double* g, double* m, double gscale, do
 // Whole-MLP Muon over [params | mom] in place (W1, W2 orthogonalised; b1, b2 by stepvec).
 int mlp_muon(const MlpShape& s, double* par, double* mom, const double* G, double gscale, double lr,
              double wd, double mu, double eps, bool mixed, hipStream_t st) {
-  if (!mixed) {  // both matrices in one launch when they fit a workgroup each
+  if (!mixed) {  // both matrices and both bias steps in one launch when the matrices fit a workgroup each
     const ExactMat mats[2] = {{par + s.oW1, G + s.oW1, mom + s.oW1, par + s.oW1, mom + s.oW1, s.H, s.D, 0.0},
                               {par + s.oW2, G + s.oW2, mom + s.oW2, par + s.oW2, mom + s.oW2, s.O, s.H, 0.0}};
-    const int r = muon_mat_exact_batch(mats, 2, gscale, lr, wd, mu, eps, kRefCoeffs, 5, st);
-    if (r == PH_OK) {
-      PH_TRY(stepvec_f64(s.H, par + s.ob1, G + s.ob1, mom + s.ob1, gscale, lr, wd, mu, st));
-      return stepvec_f64(s.O, par + s.ob2, G + s.ob2, mom + s.ob2, gscale, lr, wd, mu, st);
-    }
+    const ExactVec vecs[2] = {{par + s.ob1, G + s.ob1, mom + s.ob1, (long)s.H},
+                              {par + s.ob2, G + s.ob2, mom + s.ob2, (long)s.O}};
+    const int r = muon_mat_exact_batch(mats, 2, vecs, 2, gscale, lr, wd, mu, eps, kRefCoeffs, 5, st);
     if (r != PH_ERR_UNSUPPORTED) return r;
   }
   PH_TRY(muon_f64(s.H, s.D, par + s.oW1, G + s.oW1, mom + s.oW1, gscale, lr, wd, mu, eps, mixed, st));

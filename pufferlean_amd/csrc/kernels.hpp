@@ -96,9 +96,16 @@ struct ExactMat {
   int rows, cols;
   double c2;
 };
+// A bias vector stepped in the same launch (Nesterov + decay, as stepvec_exact; in place).
+struct ExactVec {
+  double* b;
+  const double* g;
+  double* m;
+  long n;
+};
 constexpr int kExactBatchMax = 4;
-int muon_mat_exact_batch(const ExactMat* mats, int n, double gscale, double lr, double wd, double mu, double eps,
-                         const double* coeffs, int nsteps, hipStream_t st);
+int muon_mat_exact_batch(const ExactMat* mats, int n, const ExactVec* vecs, int nv, double gscale, double lr,
+                         double wd, double mu, double eps, const double* coeffs, int nsteps, hipStream_t st);
 int stepvec_exact(long n, const double* b, const double* g, const double* m, double* nb, double* nm,
                   double gscale, double lr, double wd, double mu, hipStream_t st);
 int newton_schulz_fast(float* X, int rows, int cols, const float* coeffs, int nsteps, float eps,

@@ -267,12 +267,26 @@ struct ExactCoeffs {
 
 struct ExactBatch {
   ExactMat m[kExactBatchMax];
+  ExactVec v[kExactBatchMax];
+  int nm;
 };
 
-// One workgroup per matrix of the batch (they are independent, so they run side by side).
-__global__ void __launch_bounds__(1024) k_muon_exact_fused(ExactBatch bt, double gscale, double mu, double eps,
-                                                           ExactCoeffs cf, int nsteps, double c1) {
+// One workgroup per matrix of the batch (they are independent, so they run side by side), then one
+// per bias vector, which takes the f64 bias step (k_stepvec_f64's arithmetic) in place.
+__global__ void __launch_bounds__(1024) k_muon_exact_fused(ExactBatch bt, double gscale, double lr, double mu,
+                                                           double eps, ExactCoeffs cf, int nsteps, double c1) {
 #pragma clang fp contract(off)
+  if ((int)blockIdx.x >= bt.nm) {  // uniform per workgroup: the matrix path's barriers are not reached
+    const ExactVec& vt = bt.v[blockIdx.x - bt.nm];
+    for (long i = threadIdx.x; i < vt.n; i += blockDim.x) {
+      const double gi = vt.g[i] * gscale;
+      const double newm = mu * vt.m[i] + gi;
+      const double upd = gi + mu * newm;
+      vt.b[i] = vt.b[i] * c1 + lr * upd;
+      vt.m[i] = newm;
+    }
+    return;
+  }
   const ExactMat& mt = bt.m[blockIdx.x];
   const double* W = mt.W;
   const double* G = mt.G;
@@ -381,10 +395,13 @@ __global__ void __launch_bounds__(1024) k_muon_exact_fused(ExactBatch bt, double
 // ---- exact tier host drivers: device f64 buffers --------------------------------------------------
 // Matrices whose iterate, product and Gram matrix fit the LDS budget, in one launch of one workgroup
 // each; PH_ERR_UNSUPPORTED (nothing launched) when one does not fit or the batch is too large.
-int muon_mat_exact_batch(const ExactMat* mats, int n, double gscale, double lr, double wd, double mu, double eps,
-                         const double* coeffs, int nsteps, hipStream_t st) {
-  if (n < 1 || n > kExactBatchMax || nsteps > kExactFusedMaxSteps) return PH_ERR_UNSUPPORTED;
+int muon_mat_exact_batch(const ExactMat* mats, int n, const ExactVec* vecs, int nv, double gscale, double lr,
+                         double wd, double mu, double eps, const double* coeffs, int nsteps, hipStream_t st) {
+  if (n < 1 || n > kExactBatchMax || nv < 0 || nv > kExactBatchMax || nsteps > kExactFusedMaxSteps)
+    return PH_ERR_UNSUPPORTED;
   ExactBatch bt{};
+  bt.nm = n;
+  for (int i = 0; i < nv; i++) bt.v[i] = vecs[i];
   long lds = 0;
   for (int i = 0; i < n; i++) {
     const ExactMat& m = mats[i];
@@ -396,7 +413,7 @@ int muon_mat_exact_batch(const ExactMat* mats, int n, double gscale, double lr, 
   }
   ExactCoeffs cf{};
   for (int i = 0; i < 3 * nsteps; i++) cf.v[i] = coeffs[i];
-  k_muon_exact_fused<<<n, 1024, (size_t)lds * 8, st>>>(bt, gscale, mu, eps, cf, nsteps, 1.0 - lr * wd);
+  k_muon_exact_fused<<<n + nv, 1024, (size_t)lds * 8, st>>>(bt, gscale, lr, mu, eps, cf, nsteps, 1.0 - lr * wd);
   PH_LAUNCH_CHECK();
   return PH_OK;
 }
@@ -410,7 +427,7 @@ int muon_mat_exact(int rows, int cols, const double* W, const double* G, const d
   const double scale = sqrt(fmax(1.0, (double)rows / (double)cols));
   {
     const ExactMat one{W, G, M, nW, nM, rows, cols, 0.0};
-    const int r = muon_mat_exact_batch(&one, 1, gscale, lr, wd, mu, eps, coeffs, nsteps, st);
+    const int r = muon_mat_exact_batch(&one, 1, nullptr, 0, gscale, lr, wd, mu, eps, coeffs, nsteps, st);
     if (r != PH_ERR_UNSUPPORTED) return r;
   }
   double* ws = (double*)scratch(kSlotMuonExact, (size_t)(6 * n + (long)mn * mn + rows + 8) * 8);
