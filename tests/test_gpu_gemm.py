@@ -157,6 +157,24 @@ def test_gemm_unaligned_strided_bf16_storage_and_epilogue(gpu):
     assert rel(c, ref_r) < 1e-5
 
 
+def test_gemm_unaligned_mask_axpby_and_second_output(gpu):
+    """The ReLU-mask and alpha*acc + beta*aux epilogues, with a transposed bf16 second output, on a
+    15-wide reduction (the dgrad of a 15-wide head) through the padded staging."""
+    M, N, K = 3000, 128, 15
+    a, b = operands(M, N, K, 0, 0, 31)
+    ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    ref = oracle(a, b, 0, 0, M, N, K)
+    aux = torch.from_numpy(rng.normal(32, M * N).reshape(M, N).astype(np.float32)).cuda()
+    auxn = aux.cpu().numpy()
+    c = D.gemm(ga, gb, math="f32", epilogue=L.PH_EPI_RELU_MASK, aux=aux).cpu().numpy()
+    assert rel(c, np.where(auxn > 0, ref, 0)) < 1e-5
+    c2 = torch.empty((N, M), device="cuda", dtype=torch.bfloat16)
+    c = D.gemm(ga, gb, math="f32", epilogue=L.PH_EPI_AXPBY, aux=aux, alpha=0.5, beta=-1.5, out2=c2,
+               out2_trans=True).cpu().numpy()
+    assert rel(c, 0.5 * ref - 1.5 * auxn) < 1e-5
+    assert rel(c2.float().cpu().numpy(), c.T) < 4e-3
+
+
 def _bf(x):
     return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda().to(torch.bfloat16)
 
