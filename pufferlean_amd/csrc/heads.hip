@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
   __syncthreads();
   double lsum[6] = {0, 0, 0, 0, 0, 0};
   if (live) {
-    float x[kTileW], p[kTileW], pout[kTileW];
+    float x[kTileW], p[kTileW], pouth[kTileHeads];
 #pragma unroll
     for (int k = 0; k < kTileW; k++) x[k] = k < O ? tile[t * kTileP + k] : 0.f;
     float joint = 0.f, entropy = 0.f;
@@ -195,6 +195,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
     int off = 0;
 #pragma unroll
     for (int h = 0; h < kTileHeads; h++) {
+      pouth[h] = 0.f;
       if (h >= K) break;
       const int end = off + hs.n[h], ah = av[h];
       float m = -INFINITY;
@@ -215,9 +216,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
           entropy -= p[k] * (x[k] - lse);
           if (k == off + ah) xa = x[k];
         }
-#pragma unroll
-      for (int k = 0; k < kTileW; k++)
-        if (k >= off && k < end) pout[k] = po;
+      pouth[h] = po;
       if (ah >= 0 && ah < end - off) {
         joint += xa - lse;
         hit |= 1u << (off + ah);
@@ -231,10 +230,18 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
     const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
     const float dPol = !inRange ? __builtin_nanf("")
                      : (A * ratio <= A * rc) ? A * ratio : ((lo < ratio && ratio < hi) ? A * ratio : 0.f);
+    // the gradient pass walks the heads again: each head's expected logit stays one register
+    off = 0;
 #pragma unroll
-    for (int k = 0; k < kTileW; k++)
-      if (k < W)
-        tile[t * kTileP + k] = dPol * ((float)((hit >> k) & 1u) - p[k]) + ent * p[k] * (pout[k] - x[k]);
+    for (int h = 0; h < kTileHeads; h++) {
+      if (h >= K) break;
+      const int end = off + hs.n[h];
+#pragma unroll
+      for (int k = 0; k < kTileW; k++)
+        if (k >= off && k < end)
+          tile[t * kTileP + k] = dPol * ((float)((hit >> k) & 1u) - p[k]) + ent * p[k] * (pouth[h] - x[k]);
+      off = end;
+    }
     float vnew = 0.f;
 #pragma unroll
     for (int k = 0; k < kTileW; k++)
