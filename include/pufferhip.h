@@ -13,6 +13,18 @@
  *      host `const double*` (input) or `double*` (caller-allocated output of the documented size).
  *      They copy in, run, copy out and synchronise, like the reference entries. The Lean glue that
  *      maps lean_cuda_X(lean_obj_arg ...) onto ph_cuda_X(const double* ...) is a few lines each.
+ *
+ * Concurrency. Intermediate buffers (GEMM padding and split-K partials, the MinGRU activations, loss
+ * and reduction partials, the Newton-Schulz work items and control words) live in library-owned
+ * scratch, one buffer per purpose per device. Two calls in flight at once on different streams of
+ * one device race on that scratch: order them on one stream, or make the later stream wait for the
+ * earlier. (The library's own concurrent Muon lanes use per-lane scratch.)
+ *
+ * Graph capture. Every ph_* device entry can be captured into a HIP graph: it launches kernels
+ * only (no memset nodes, no host synchronisation). Run each shape once before capturing it, so its
+ * scratch already has full size. When a later call needs a larger buffer, the old one is retired,
+ * not freed, so a graph captured earlier keeps valid memory; ph_release_scratch() frees retired
+ * buffers and must only be called once no graph captured before it will be replayed.
  */
 #ifndef PUFFERHIP_H
 #define PUFFERHIP_H
@@ -51,6 +63,11 @@ int ph_version(void);
 /* Number of visible devices (0 if none). Replaces lean_ffi_cuda_available (pufferblas.c:1348). */
 int ph_device_count(void);
 int ph_synchronize(void* stream);
+/* Free the scratch buffers retired by growth (see "Graph capture" above) after a device
+ * synchronisation. Graphs captured before this call must not be replayed after it. */
+int ph_release_scratch(void);
+/* Number and total bytes of retired scratch buffers on the current device. */
+int ph_scratch_retired(size_t* count, size_t* bytes);
 
 /* ---------------------------------------------------------------------------------------------- */
 /* V-trace / GAE reverse scan. Replaces k_vtrace / k_vtrace_mingru (puffercuda.cu:69-90, 146-167)
@@ -165,6 +182,16 @@ int ph_newton_schulz(float* X, int rows, int cols, const float* coeffs, int nste
  * ph_newton_schulz. No counterpart in the reference (its NS walks the matrices in sequence). */
 int ph_newton_schulz_batch(float* const* X, const int* rows, const int* cols, int n,
                            const float* coeffs, int nsteps, float eps, int math, void* stream);
+/* The bf16 Newton-Schulz launches (ph_newton_schulz, _batch, ph_muon_mat, ph_mingru_muon and
+ * ph_mingru_step in bf16 math) run every matrix in one persistent launch whose work items wait, with
+ * a bounded spin, for the tiles of earlier phases computed by other workgroups. A wait that reaches
+ * its bound lets the launch finish with invalid matrices and records the failure on the device.
+ * ph_ns_status synchronises `stream`, reads and clears that record, and returns PH_ERR_HIP (with a
+ * message) when a launch since the last check gave up; PH_OK otherwise. */
+int ph_ns_status(void* stream);
+/* Spin bound of those waits, in polls of about a microsecond (0 restores the default, 2^20). A tiny
+ * bound makes the waits give up; it exists so that the failure report can be tested. */
+int ph_ns_set_spin_limit(unsigned polls);
 /* In-place Muon matrix step on fp32 state: M <- mu*M + gscale*G; U = gscale*G + mu*M;
  * W <- (1-lr*wd)*W + lr*sqrt(max(1,rows/cols))*NS(U). */
 int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,

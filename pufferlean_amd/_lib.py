@@ -51,6 +51,10 @@ SIGNATURES: dict[str, list] = {
     "ph_version": [],
     "ph_device_count": [],
     "ph_synchronize": [vp],
+    "ph_release_scratch": [],
+    "ph_scratch_retired": [szptr, szptr],
+    "ph_ns_status": [vp],
+    "ph_ns_set_spin_limit": [u32],
     "ph_vtrace": [i32, vp, vp, vp, vp, vp, sz, sz, i32, i32, i32, i32, dbl, dbl, dbl, dbl, vp, vp, vp],
     "ph_adv_normalize": [i32, vp, sz, vp, vp, vp],
     "ph_colsum": [vp, sz, sz, sz, vp, flt, i32, vp],

@@ -43,11 +43,20 @@ void set_error(const char* fmt, ...);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// LDS budget of every kernel in the library, per workgroup. Each kernel with a sizeable static LDS
+// footprint asserts against it, and dynamic LDS is checked on the host before the launch. Larger
+// footprints (a single workgroup may hold up to 160 KB on gfx950) stay out until a form using them
+// has been shown sound.
+constexpr int kMaxLdsBytes = 80 * 1024;
+
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // Growable per-slot device buffers owned by the library (allocated on first use, reused across
-// calls, freed at process exit). Slot ids are private to each translation unit's range.
+// calls). A slot that must grow retires its old buffer instead of freeing it, since a captured graph
+// may still use it; ph_release_scratch() frees retired buffers. Slot ids: kernels.hpp.
 void* scratch(int slot, size_t bytes);
+// The slot's current buffer, or nullptr if it has none (never allocates).
+void* scratch_peek(int slot);
 // scratch() whose memory is zero-filled (a fill kernel on st) whenever the slot is newly allocated;
 // the caller keeps it zero between uses.
 void* scratch_zeroed(int slot, size_t bytes, hipStream_t st);

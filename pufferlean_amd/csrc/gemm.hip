@@ -454,6 +454,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   constexpr int EPR = epilogue_rows(BM, LDC * 4, PIPE_BYTES);
   static_assert(EPR >= 32 && BM % EPR == 0, "epilogue staging rows");
   constexpr int C_BYTES = EPR * LDC * 4;
+  static_assert((PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES) <= kMaxLdsBytes, "LDS budget");
   __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
   uint16_t (*sA)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
   uint16_t (*sB)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
@@ -743,6 +744,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
   constexpr int EPR = epilogue_rows(BM, LDC * 4, PIPE_BYTES);
   static_assert(EPR >= 32 && BM % EPR == 0, "epilogue staging rows");
   constexpr int C_BYTES = EPR * LDC * 4;
+  static_assert((PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES) <= kMaxLdsBytes, "LDS budget");
   __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
   uint16_t* const stages = reinterpret_cast<uint16_t*>(smem);  // stage s: A at s*STAGE_EL, B after
   float* sC = reinterpret_cast<float*>(smem);
@@ -886,6 +888,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
   constexpr int LDC = BN + 4;
   constexpr int PIPE_BYTES = 2 * (BM + BN) * LDK * 4;
   constexpr int C_BYTES = BM * LDC * 4;
+  static_assert((PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES) <= kMaxLdsBytes, "LDS budget");
   __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
   float (*sA)[BM * LDK] = reinterpret_cast<float (*)[BM * LDK]>(smem);
   float (*sB)[BN * LDK] = reinterpret_cast<float (*)[BN * LDK]>(smem + 2 * BM * LDK * 4);

@@ -167,6 +167,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_md_tile(const float* __restric
                                                           float* __restrict__ newval, double* __restrict__ part,
                                                           double* __restrict__ losses) {
   __shared__ float tile[256 * kTileP];
+  static_assert(256 * kTileP * 4 <= kMaxLdsBytes, "LDS budget");
   const long n0 = (long)blockIdx.x * 256;
   const int R = (int)(N - n0 < 256 ? N - n0 : 256);
   const int t = threadIdx.x, O = W + 1, K = hs.K;
@@ -267,6 +268,7 @@ __global__ void __launch_bounds__(256) k_ppo_grad_cont_tile(const float* __restr
                                                             double* __restrict__ part,
                                                             double* __restrict__ losses) {
   __shared__ float tile[256 * kTileP];
+  static_assert(256 * kTileP * 4 <= kMaxLdsBytes, "LDS budget");
   const long n0 = (long)blockIdx.x * 256;
   const int R = (int)(N - n0 < 256 ? N - n0 : 256);
   const int t = threadIdx.x, W = 2 * d, O = W + 1;

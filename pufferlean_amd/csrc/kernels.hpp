@@ -138,6 +138,11 @@ int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float 
 int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);
 
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st);
+// Advantage moments over fixed chunks of kMomentsChunk elements: one partial per chunk and pass.
+constexpr size_t kMomentsChunk = 4096;
+inline size_t moments_chunks(size_t n) { return (n + kMomentsChunk - 1) / kMomentsChunk; }
+int moments_normalize_ws(int dtype, const void* x, size_t n, void* y, void* stats, void* part,
+                         hipStream_t st);
 int colsum_f32(const float* X, size_t N, int J, size_t ld, float* out, float scale, int accumulate,
                hipStream_t st);
 int colsum_bf16(const uint16_t* X, long N, int J, long ld, float* out, float scale, int accumulate,

@@ -304,17 +304,22 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
   const size_t o_stats = take(64);
   uint8_t* base = (uint8_t*)scratch(kSlotMgBufs, off);
   if (!base) return PH_ERR_NOMEM;
-  // The padded head columns of dl are never written by the loss kernel and must read as zero:
-  // cleared with a fill kernel whenever this region moves (first use or a new shape).
+  // The padded head columns of dl (past the A logits and the value) are never written by the loss
+  // kernels and must read as zero: cleared with a fill kernel whenever this region moves (first use
+  // or a new shape) or the head width changes (a wider head's columns would otherwise stay behind,
+  // NaN rows of an out-of-range action included).
   static void* zeroed_at[16] = {};
   static size_t zeroed_len[16] = {};
+  static int zeroed_a[16] = {};
   int dev = 0;
   PH_CHECK_HIP(hipGetDevice(&dev));
   const size_t dl_bytes = (size_t)TB * HP * 4;
-  if (zeroed_at[dev & 15] != (void*)(base + o_dl) || zeroed_len[dev & 15] != dl_bytes) {
+  if (zeroed_at[dev & 15] != (void*)(base + o_dl) || zeroed_len[dev & 15] != dl_bytes ||
+      zeroed_a[dev & 15] != d.A) {
     PH_TRY(fill_zero(base + o_dl, dl_bytes, st));
     zeroed_at[dev & 15] = base + o_dl;
     zeroed_len[dev & 15] = dl_bytes;
+    zeroed_a[dev & 15] = d.A;
   }
   b.obsb = base + o_obsb; b.x = base + o_x; b.cmb = base + o_cmb; b.o = base + o_o; b.dy = base + o_dy;
   b.dh0 = base + o_dh0; b.dh1 = base + o_dh1; b.wenc = base + o_wenc; b.wl = base + o_wl;

@@ -261,6 +261,7 @@ __device__ __forceinline__ void dot2x2(const double* U, int u0, int u1, int us, 
 
 constexpr int kExactFusedMaxSteps = 8;
 constexpr long kExactFusedLds = 8192;  // doubles: 64 KB
+static_assert(kExactFusedLds * 8 + 64 <= kMaxLdsBytes, "LDS budget of the fused exact Muon");
 struct ExactCoeffs {
   double v[3 * kExactFusedMaxSteps];
 };

@@ -40,6 +40,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <atomic>
 #include <utility>
 
 namespace ph {
@@ -74,6 +75,7 @@ struct NsLaunch {
   long n0, nt, n3;  // item counts of P0, of P1 (= P2) and of P3, summed over the matrices
   int nmat, nsteps;
   float eps;
+  unsigned spin;  // wait bound (polls)
 };
 
 // Buffers of step s start at base + s * stride (x*: the step's input iterate, e*/b*: its E and B').
@@ -141,13 +143,13 @@ __device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v) {
 // written through and is read for the first time after the wait). The wait is bounded: past the
 // limit it raises the launch's flag, and once the flag is up no further wait blocks, so the launch
 // always drains quickly (with wrong results) instead of hanging.
-__device__ void wait_done(unsigned* cnt, unsigned need, unsigned* flag) {
+__device__ void wait_done(unsigned* cnt, unsigned need, unsigned* flag, unsigned limit) {
   if (threadIdx.x == 0) {
     unsigned spins = 0;
     while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need &&
            __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
       __builtin_amdgcn_s_sleep(2);
-      if (++spins > kSpinLimit) {
+      if (++spins > limit) {
         __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(flag + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sticky record
         break;
@@ -340,6 +342,7 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
   __shared__ __align__(16) uint16_t sA[kGroups][2][kT * kPitch];
   __shared__ __align__(16) uint16_t sB[kGroups][2][kT * kPitch];
   __shared__ unsigned s_ticket;
+  static_assert(2 * kGroups * 2 * kT * kPitch * 2 + 16 <= kMaxLdsBytes, "LDS budget");
   unsigned* ctl = L.ctl;
   const long per = 2 * L.nt + L.n3;
   const long total = L.n0 + (long)L.nsteps * per;
@@ -380,7 +383,7 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
       continue;
     }
     const long need = g.n0 + (long)s * (2 * g.nt + g.n3) + (p - 1) * g.nt;
-    wait_done(done, (unsigned)need, &ctl[kCtlFlag]);
+    wait_done(done, (unsigned)need, &ctl[kCtlFlag], L.spin);
     const float a = L.coef[3 * s], b = L.coef[3 * s + 1], c = L.coef[3 * s + 2];
     const float sc = s == 0 ? norm_scale(g.part, g.n0, L.eps) : 1.f;
     const long xs = (long)s * g.mw, es = (long)s * g.mm;  // this step's buffers
@@ -516,6 +519,12 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
   }
 }
 
+std::atomic<unsigned> g_spin{kSpinLimit};
+
+__global__ void k_clear_word(unsigned* w) {
+  if (threadIdx.x == 0) *w = 0u;
+}
+
 int cu_count() {
   static int n[64] = {};
   int dev = 0;
@@ -578,6 +587,7 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
     L.ctl = ctl;
     L.nsteps = nsteps;
     L.eps = eps;
+    L.spin = g_spin.load(std::memory_order_relaxed);
     // one block per CU: measured faster than two (half as many blocks polling, and a CU's load
     // bandwidth goes to one tile at a time)
     const long cap = cu_count();
@@ -589,3 +599,26 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
 }
 
 }  // namespace ph
+
+using namespace ph;
+
+extern "C" int ph_ns_status(void* stream) {
+  const hipStream_t st = as_stream(stream);
+  PH_CHECK_HIP(hipStreamSynchronize(st));
+  unsigned* ctl = (unsigned*)scratch_peek(kSlotNsCtl);
+  if (!ctl) return PH_OK;  // no fused launch has run on this device
+  unsigned rec = 0;
+  PH_CHECK_HIP(hipMemcpy(&rec, ctl + kCtlFlag + 1, sizeof(rec), hipMemcpyDeviceToHost));
+  if (rec == 0u) return PH_OK;
+  k_clear_word<<<1, 64, 0, st>>>(ctl + kCtlFlag + 1);
+  PH_LAUNCH_CHECK();
+  PH_CHECK_HIP(hipStreamSynchronize(st));
+  set_error("newton_schulz (fused): a bounded wait for another workgroup's tiles gave up; the matrices "
+            "written by the launches since the last status check are invalid");
+  return PH_ERR_HIP;
+}
+
+extern "C" int ph_ns_set_spin_limit(unsigned polls) {
+  g_spin.store(polls ? polls : kSpinLimit, std::memory_order_relaxed);
+  return PH_OK;
+}

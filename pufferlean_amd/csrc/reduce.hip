@@ -225,8 +225,7 @@ int transpose_bf16(const uint16_t* X, uint16_t* Xt, int rows, int cols, hipStrea
 
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st) {
   if (n == 0) return PH_OK;
-  const size_t chunk = 4096;
-  size_t G = (n + chunk - 1) / chunk;
+  const size_t G = moments_chunks(n);
   const size_t es = dtype == PH_F64 ? 8 : 4;
   uint8_t* part = (uint8_t*)scratch(kSlotMomentsPart, 2 * G * es);
   if (!part) return PH_ERR_NOMEM;
@@ -234,6 +233,17 @@ int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, 
     stats = scratch(kSlotMomentsStats, 16);
     if (!stats) return PH_ERR_NOMEM;
   }
+  return moments_normalize_ws(dtype, x, n, y, stats, part, st);
+}
+
+// The same with the caller's workspace: part holds 2 * moments_chunks(n) elements of dtype, stats
+// 2 elements. Every partial is written before it is read, so neither needs clearing.
+int moments_normalize_ws(int dtype, const void* x, size_t n, void* y, void* stats, void* part_ws,
+                         hipStream_t st) {
+  if (n == 0) return PH_OK;
+  const size_t chunk = kMomentsChunk;
+  const size_t G = moments_chunks(n);
+  uint8_t* part = (uint8_t*)part_ws;
   const unsigned g = (unsigned)G;
   if (dtype == PH_F64) {
     using R = double;

@@ -74,6 +74,7 @@ __global__ void __launch_bounds__(kPsThreads) k_prio_sample(const double* __rest
                                                             double* __restrict__ mp) {
   __shared__ double red[kPsThreads];
   __shared__ double cumL[kPsLdsCum];
+  static_assert((kPsThreads + kPsLdsCum) * 8 <= kMaxLdsBytes, "LDS budget");
   const int tid = threadIdx.x;
   const long R = (N + kPsThreads - 1) / kPsThreads;
   const long lo = (long)tid * R < N ? (long)tid * R : N;

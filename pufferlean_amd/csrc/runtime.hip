@@ -5,6 +5,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "slot_table.hpp"
 
 namespace ph {
 
@@ -20,49 +21,48 @@ void set_error(const char* fmt, ...) {
 namespace {
 constexpr int kMaxDev = 16;
 constexpr int kSlots = 128;
-struct SlotTable {
-  void* ptr[kSlots] = {};
-  size_t bytes[kSlots] = {};
-  unsigned gen[kSlots] = {};   // allocations made for the slot so far
-  unsigned zgen[kSlots] = {};  // the allocation scratch_zeroed last cleared
-};
-SlotTable g_tables[kMaxDev];
+SlotTable<kSlots> g_tables[kMaxDev];
 std::mutex g_mu;
+std::set<void*> g_zeroed;  // word blocks ensure_zeroed_words has cleared (by address)
+
+int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return -1;
+  return dev;
+}
 }  // namespace
 
-// Buffers only grow; a grown slot is freed after a device sync so no queued kernel still reads it.
+// Buffers only grow. A grown slot's old buffer is retired, not freed (a captured graph may still use
+// it), so growth needs no device synchronisation and is legal between captures; ph_release_scratch()
+// frees the retired buffers.
 void* scratch(int slot, size_t bytes) {
-  if (slot < 0 || slot >= kSlots) return nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  const int dev = current_device();
+  if (dev < 0) return nullptr;
   std::lock_guard<std::mutex> lk(g_mu);
-  SlotTable& tb = g_tables[dev];
-  if (bytes == 0) bytes = 1;
-  if (tb.bytes[slot] >= bytes) return tb.ptr[slot];
-  if (tb.ptr[slot]) {
-    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-    (void)hipFree(tb.ptr[slot]);
-    tb.ptr[slot] = nullptr;
-    tb.bytes[slot] = 0;
-  }
-  size_t rounded = (bytes + 255) & ~(size_t)255;
-  void* p = nullptr;
-  if (hipMalloc(&p, rounded) != hipSuccess) {
-    (void)hipGetLastError();
-    set_error("device allocation of %zu bytes failed (slot %d)", rounded, slot);
-    return nullptr;
-  }
-  tb.ptr[slot] = p;
-  tb.bytes[slot] = rounded;
-  tb.gen[slot]++;
+  void* p = g_tables[dev].get(slot, bytes, [&](size_t n) -> void* {
+    void* q = nullptr;
+    if (hipMalloc(&q, n) != hipSuccess) {
+      (void)hipGetLastError();
+      set_error("device allocation of %zu bytes failed (slot %d)", n, slot);
+      return nullptr;
+    }
+    return q;
+  });
+  if (!p && (slot < 0 || slot >= kSlots)) set_error("scratch: slot %d out of range", slot);
   return p;
+}
+
+void* scratch_peek(int slot) {
+  const int dev = current_device();
+  if (dev < 0) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_tables[dev].peek(slot);
 }
 
 namespace {
 __global__ void k_zero_words(unsigned* p, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
 }
-std::set<void*> g_zeroed;
 }  // namespace
 
 int ensure_zeroed_words(unsigned* words, int n, hipStream_t st) {
@@ -87,12 +87,12 @@ __global__ void k_zero_words_grid(unsigned* p, long n) {
 void* scratch_zeroed(int slot, size_t bytes, hipStream_t st) {
   void* p = scratch(slot, bytes);
   if (!p) return nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+  const int dev = current_device();
+  if (dev < 0) return nullptr;
   size_t sz = 0;
   {
     std::lock_guard<std::mutex> lk(g_mu);
-    SlotTable& tb = g_tables[dev];
+    SlotTable<kSlots>& tb = g_tables[dev];
     if (tb.zgen[slot] != tb.gen[slot]) {
       tb.zgen[slot] = tb.gen[slot];
       sz = tb.bytes[slot];
@@ -202,6 +202,39 @@ extern "C" int ph_device_count(void) {
     return 0;
   }
   return n;
+}
+
+extern "C" int ph_release_scratch(void) {
+  const int dev = ph::current_device();
+  if (dev < 0) {
+    ph::set_error("ph_release_scratch: no current device");
+    return PH_ERR_HIP;
+  }
+  PH_CHECK_HIP(hipDeviceSynchronize());
+  std::lock_guard<std::mutex> lk(ph::g_mu);
+  hipError_t err = hipSuccess;
+  ph::g_tables[dev].release([&](void* p) {
+    ph::g_zeroed.erase(p);
+    const hipError_t e = hipFree(p);
+    if (e != hipSuccess && err == hipSuccess) err = e;
+  });
+  if (err != hipSuccess) {
+    ph::set_error("ph_release_scratch: hipFree failed: %s", hipGetErrorString(err));
+    return PH_ERR_HIP;
+  }
+  return PH_OK;
+}
+
+extern "C" int ph_scratch_retired(size_t* count, size_t* bytes) {
+  const int dev = ph::current_device();
+  if (dev < 0) {
+    ph::set_error("ph_scratch_retired: no current device");
+    return PH_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lk(ph::g_mu);
+  if (count) *count = ph::g_tables[dev].retired.size();
+  if (bytes) *bytes = ph::g_tables[dev].retired_bytes;
+  return PH_OK;
 }
 
 extern "C" int ph_synchronize(void* stream) {

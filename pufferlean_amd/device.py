@@ -156,6 +156,28 @@ def newton_schulz(X, *, coeffs=CONST_COEFFS, eps=1e-7, math="bf16"):
     return X
 
 
+def ns_status():
+    """Synchronises the current stream and raises if a fused Newton-Schulz launch since the last check
+    gave up a bounded wait (its matrices are invalid); clears the record."""
+    L.call("ph_ns_status", _stream())
+
+
+def ns_set_spin_limit(polls=0):
+    """Bound of the fused Newton-Schulz waits (0: the default)."""
+    L.call("ph_ns_set_spin_limit", int(polls))
+
+
+def scratch_retired():
+    """(count, bytes) of scratch buffers retired by growth and not yet released."""
+    n, b = C.c_size_t(0), C.c_size_t(0)
+    L.call("ph_scratch_retired", C.byref(n), C.byref(b))
+    return n.value, b.value
+
+
+def release_scratch():
+    L.call("ph_release_scratch")
+
+
 def newton_schulz_batch(Xs, *, coeffs=CONST_COEFFS, eps=1e-7, math="bf16"):
     """In-place fast-tier NS of several independent fp32 matrices; equal to calling newton_schulz on
     each. bf16: one fused launch per 16 matrices; fp32: concurrently on the library's stream lanes."""

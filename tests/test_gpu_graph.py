@@ -67,3 +67,42 @@ def test_graph_replays_match_eager(gpu, precision):
         _ = (torch.ones(1000, device="cuda") * 2).sum().item()  # eager work between replays
         assert torch.equal(p, ref[k][0]), f"replay {k}: parameters differ from the eager step"
         assert torch.equal(m, ref[k][1]), f"replay {k}: momentum differs from the eager step"
+
+
+def test_captured_gemm_survives_scratch_growth(gpu):
+    """A graph captured around a GEMM that stages zero-padded operand copies (a 28-wide reduction)
+    keeps valid staging memory when a later, larger call grows the same scratch slots: the old
+    buffers are retired, not freed, until ph_release_scratch."""
+    M, N, K = 4096, 128, 28
+    a = _t(rng.normal(0x910, M * K)).view(M, K)
+    b = _t(rng.normal(0x911, N * K) / np.sqrt(K)).view(N, K)
+    ref = D.gemm(a, b, trans_b=True, math="bf16")
+    c = torch.empty_like(ref)
+    D.gemm(a, b, trans_b=True, math="bf16", out=c)  # warm-up sizes the slots for this shape
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            D.gemm(a, b, trans_b=True, math="bf16", out=c)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    n0, _ = D.scratch_retired()
+    # a larger unaligned call than any before it grows the padding slots
+    M2 = 1 << 20
+    a2 = _t(rng.normal(0x912, M2 * K)).view(M2, K)
+    big = D.gemm(a2, b, trans_b=True, math="bf16")
+    torch.cuda.synchronize()
+    n1, b1 = D.scratch_retired()
+    assert n1 > n0 and b1 > 0
+    for k in range(3):
+        c.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = (torch.ones(1000, device="cuda") * 2).sum().item()
+        assert torch.equal(c, ref), f"replay {k} after the slot grew"
+    assert big.shape == (M2, N)
+    del graph
+    D.release_scratch()
+    assert D.scratch_retired() == (0, 0)

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle_lib as O
+from pufferlean_amd import _lib
 from pufferlean_amd import device as D
 from pufferlean_amd import rng
 
@@ -155,3 +156,27 @@ def test_gclip(gpu):
     t = torch.from_numpy(g).cuda()
     D.gclip(t, scale=0.5, max_norm=10.0)
     assert rel(t.cpu().numpy(), ref) < 1e-6
+
+
+def test_ns_wait_failure_is_reported(gpu):
+    """A fused launch whose bounded waits give up (forced from the host with a one-poll bound) still
+    ends normally, and ph_ns_status reports it once; with the default bound the record stays clear
+    and the batch holds the 1e-2 bar."""
+    mats = [rng.normal(0x340 + i, r * c, 0.0, 0.02).reshape(r, c).astype(np.float32)
+            for i, (r, c) in enumerate(CONFIG3)]
+    D.ns_status()  # clear anything an earlier test left
+    D.ns_set_spin_limit(1)
+    try:
+        batch = [torch.from_numpy(m).cuda() for m in mats]
+        D.newton_schulz_batch(batch, coeffs=O.BASELINE_COEFFS, math="bf16")
+        with pytest.raises(_lib.PufferHipError, match="gave up"):
+            D.ns_status()
+    finally:
+        D.ns_set_spin_limit(0)
+    D.ns_status()  # the report cleared the record
+    batch = [torch.from_numpy(m).cuda() for m in mats]
+    D.newton_schulz_batch(batch, coeffs=O.BASELINE_COEFFS, math="bf16")
+    D.ns_status()
+    for m, b in zip(mats, batch):
+        ref = O.newton_schulz(m.astype(np.float64), O.BASELINE_COEFFS, 1e-7, form=1)
+        assert rel(b.cpu().numpy(), ref) < 1e-2
