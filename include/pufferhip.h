@@ -89,6 +89,14 @@ int ph_vtrace(int dtype, const void* rew, const void* val, const void* term, con
  * NNTrain.lean:274-279). Deterministic reduction. stats (device, 2 elements of dtype: mean,
  * std+eps) may be NULL. */
 int ph_adv_normalize(int dtype, const void* adv, size_t n, void* out, void* stats, void* stream);
+/* ph_adv_normalize without any device allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same kernels and fixed-order reduction, so the results are bit-identical to
+ * ph_adv_normalize's. The partials (and the statistics when stats is NULL) live in a fixed 64 KB
+ * device array per GPU, held until the process ends, so n is limited to 4096 * 4096 = 16,777,216
+ * elements (PH_ERR_ARG beyond). Calls on one GPU share that array: calls that overlap in time on one
+ * GPU (different streams) race. */
+int ph_adv_normalize_noalloc(int dtype, const void* adv, size_t n, void* out, void* stats, void* stream);
 
 /* Column sums out[j] (+)= scale * sum_n X[n*ld + j] (k_colsum, puffercuda.cu:676-683). */
 int ph_colsum(const float* X, size_t N, size_t J, size_t ld, float* out, float scale,

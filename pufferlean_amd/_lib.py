@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list] = {
     "ph_ns_set_spin_limit": [u32],
     "ph_vtrace": [i32, vp, vp, vp, vp, vp, sz, sz, i32, i32, i32, i32, dbl, dbl, dbl, dbl, vp, vp, vp],
     "ph_adv_normalize": [i32, vp, sz, vp, vp, vp],
+    "ph_adv_normalize_noalloc": [i32, vp, sz, vp, vp, vp],
     "ph_colsum": [vp, sz, sz, sz, vp, flt, i32, vp],
     "ph_convert": [i32, vp, i32, vp, sz, vp],
     "ph_ppo_grad": [vp, sz, vp, sz, vp, vp, vp, vp, vp, sz, sz, flt, flt, flt, flt, i32, vp, sz,
