@@ -306,6 +306,36 @@ int ph_mingru_ppo_grad_md(const ph_mingru_dims* d, const ph_ppo_coefs* c, const 
 int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params, float* mom,
                    float* G, void* stream);
 /* ---------------------------------------------------------------------------------------------- */
+/* MLP policy update on the device. The reference's MLP policy is D -> H (ReLU) -> A+1 (A logits and
+ * the value in one head matrix; flattenMLP [W1|b1|W2|b2], pufferblas.c:699-747, puffercuda.cu:748-820);
+ * these entries take L >= 1 hidden layers of width H (at most 8) and repeat the hidden layer:
+ * params = [W1(H*D) | b1(H) | W2(H*H) | b2(H) | ... | WL | bL | Wo((A+1)*H) | bo(A+1)], fp32. With
+ * L = 1 this is flattenMLP. Rows are [N][D] observations; math is PH_MATH_F32 (fp32 MFMA) or
+ * PH_MATH_BF16 (bf16 MFMA on the fp32 operands, the reference's FAST_16BF). */
+typedef struct { int N, D, H, L, A; } ph_mlp_dims;
+long ph_mlp_param_count(const ph_mlp_dims* d);
+/* out[N][A+1] = the forward's head outputs (logits, value). */
+int ph_mlp_forward(const ph_mlp_dims* d, int math, const float* params, const float* obs, float* out,
+                   void* stream);
+/* Summed PPO gradient over the N rows into G (fp32 [P], overwritten): the fused loss of ph_ppo_grad
+ * without the max shift (as k_ppo_dout), then the backward (lean_cuda_mlp_ppo_grad,
+ * puffercuda.cu:748-820, for any L). adv is the (normalised) advantage, ret the value target, old the
+ * behaviour log-prob, ov the old value (NULL: no value clip); newlp/newval/losses may be NULL. */
+int ph_mlp_ppo_grad(const ph_mlp_dims* d, const ph_ppo_coefs* c, int math, const float* params,
+                    const float* obs, const int* act, const float* adv, const float* ret, const float* old,
+                    const float* ov, float* G, float* newlp, float* newval, double* losses, void* stream);
+/* One whole PPO+Muon update over N = T*B time-major rows (row t*B + b): the forward; per row the
+ * log-prob of the taken action and the value; vec-form V-trace (variant 0) with the ratio
+ * exp(logp - behav_logp); advantage normalisation; the PPO gradient with old = behav_logp and the
+ * V-trace targets as returns; then G scaled by m->gscale and clipped (m->max_grad_norm), Muon on every
+ * matrix and stepvec on every bias, in place on params/mom (fp32). The reference runs this chain as
+ * computePuffAdvantageV -> normalizeAdv -> lean_cuda_train_step (VecTrain.lean:98-114, NNTrain.lean:
+ * 274-279, puffercuda.cu:988-1092). G receives the scaled, clipped gradient. */
+int ph_mlp_update(const ph_mlp_dims* d, int T, const ph_ppo_coefs* c, const ph_muon_coefs* m, int math,
+                  float* params, float* mom, const float* obs, const int* act, const float* behav_logp,
+                  const float* rew, const float* done, float* G, double* losses, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- */
 /* Rollout policy forward and categorical sampler: the producers of the behaviour log-prob and value
  * columns the update consumes. */
 /* Categorical draw per row (k_sample / k_sample_f32, puffercuda.cu:1429-1460; CPU twin

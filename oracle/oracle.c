@@ -24,6 +24,9 @@
  *   orc_ppo_losses               hand-computed two-row case
  *   orc_gemm                     numpy matmul on all four transpose forms
  *   orc_mlp_ppo_grad             finite differences of the summed objective through the MLP
+ *   orc_mlp_deep_ppo_grad        L = 1 equals orc_mlp_ppo_grad bit for bit; L = 2, 3 (with and without
+ *                                the value clip) against central finite differences of an
+ *                                independently written numpy objective
  *   orc_newton_schulz            scaled-orthogonal input closed form (scalar quintic); diagonal input
  *                                closed form; form 0 vs form 1 within roundoff; tall/wide transpose
  *   orc_muon_mat / stepvec       closed form on diagonal inputs; mlp wrapper == per-tensor calls
@@ -430,6 +433,67 @@ void orc_mlp_ppo_grad(const double* p, const double* obs, const double* act, con
   for (size_t n = 0; n < N; n++) for (size_t j = 0; j < H; j++) gb1[j] += dH1[n * H + j];
   orc_gemm(1, 0, H, D, N, 1.0, dH1, H, obs, D, 0.0, gW1, D, threads);
   free(H1); free(Out); free(dOut); free(dH1);
+}
+
+/* The same gradient for L >= 1 hidden ReLU layers of width H and the combined head (pufferblas.c:699-747
+ * with its one hidden layer repeated): p = [W1(H*D) | b1(H) | W2(H*H) | b2(H) | ... | WL | bL |
+ * Wo(O*H) | bo(O)], O = A+1, value in output column A. ov (may be NULL) and vfClip select the clipped
+ * value loss. newlp/newval (may be NULL) receive the per-row log-prob of the action and the value.
+ * With L = 1, ov = NULL the operations are those of orc_mlp_ppo_grad in the same order. */
+void orc_mlp_deep_ppo_grad(const double* p, const double* obs, const double* act, const double* adv,
+                           const double* ret, const double* old, const double* ov, size_t N, size_t D,
+                           size_t H, size_t L, size_t A, double vfCoef, double entCoef, double clipEps,
+                           double vfClip, double* g, double* newlp, double* newval, int threads) {
+  size_t O = A + 1;
+  size_t P = H * D + H + (L - 1) * (H * H + H) + O * H + O;
+  for (size_t i = 0; i < P; i++) g[i] = 0.0;
+  /* offsets of layer l's weight and bias (l = 0..L-1), then the head */
+  size_t* oW = (size_t*)malloc(sizeof(size_t) * (L + 1));
+  size_t* ob = (size_t*)malloc(sizeof(size_t) * (L + 1));
+  size_t off = 0;
+  for (size_t l = 0; l < L; l++) {
+    size_t in = l == 0 ? D : H;
+    oW[l] = off; off += H * in;
+    ob[l] = off; off += H;
+  }
+  oW[L] = off; off += O * H;
+  ob[L] = off;
+  double** Hs = (double**)malloc(sizeof(double*) * L);
+  for (size_t l = 0; l < L; l++) Hs[l] = (double*)malloc(sizeof(double) * N * H);
+  double* Out = (double*)malloc(sizeof(double) * N * O);
+  double* dOut = (double*)malloc(sizeof(double) * N * O);
+  double* dA = (double*)malloc(sizeof(double) * N * H);
+  double* dB = (double*)malloc(sizeof(double) * N * H);
+  for (size_t l = 0; l < L; l++) {
+    const double* X = l == 0 ? obs : Hs[l - 1];
+    size_t in = l == 0 ? D : H;
+    orc_gemm(0, 1, N, H, in, 1.0, X, in, p + oW[l], in, 0.0, Hs[l], H, threads);
+    const double* b = p + ob[l];
+    for (size_t n = 0; n < N; n++)
+      for (size_t j = 0; j < H; j++) { double v = Hs[l][n * H + j] + b[j]; Hs[l][n * H + j] = v > 0.0 ? v : 0.0; }
+  }
+  orc_gemm(0, 1, N, O, H, 1.0, Hs[L - 1], H, p + oW[L], H, 0.0, Out, O, threads);
+  for (size_t n = 0; n < N; n++) for (size_t k = 0; k < O; k++) Out[n * O + k] += p[ob[L] + k];
+  orc_ppo_grad(Out, O, Out + A, O, act, adv, ret, old, ov, N, A, vfCoef, entCoef, clipEps, vfClip, 0,
+               dOut, O, dOut + A, O, newlp, newval);
+  for (size_t n = 0; n < N; n++) for (size_t k = 0; k < O; k++) g[ob[L] + k] += dOut[n * O + k];
+  orc_gemm(1, 0, O, H, N, 1.0, dOut, O, Hs[L - 1], H, 0.0, g + oW[L], H, threads);
+  orc_gemm(0, 0, N, H, O, 1.0, dOut, O, p + oW[L], H, 0.0, dA, H, threads);
+  for (size_t l = L; l-- > 0;) {
+    /* dA = gradient at layer l's output; mask by its activation */
+    for (size_t n = 0; n < N; n++)
+      for (size_t j = 0; j < H; j++) if (!(Hs[l][n * H + j] > 0.0)) dA[n * H + j] = 0.0;
+    for (size_t n = 0; n < N; n++) for (size_t j = 0; j < H; j++) g[ob[l] + j] += dA[n * H + j];
+    const double* X = l == 0 ? obs : Hs[l - 1];
+    size_t in = l == 0 ? D : H;
+    orc_gemm(1, 0, H, in, N, 1.0, dA, H, X, in, 0.0, g + oW[l], in, threads);
+    if (l > 0) {
+      orc_gemm(0, 0, N, H, H, 1.0, dA, H, p + oW[l], H, 0.0, dB, H, threads);
+      double* t = dA; dA = dB; dB = t;
+    }
+  }
+  for (size_t l = 0; l < L; l++) free(Hs[l]);
+  free(Hs); free(Out); free(dOut); free(dA); free(dB); free(oW); free(ob);
 }
 
 /* ------------------------------------------------------------------------------------------------ */

@@ -87,6 +87,10 @@ void orc_mlp_ppo_grad(const double* params, const double* obs, const double* act
                       const double* adv, const double* ret, const double* old, size_t N, size_t H,
                       size_t D, size_t A, double vfCoef, double entCoef, double clipEps, double* g,
                       int threads);
+void orc_mlp_deep_ppo_grad(const double* p, const double* obs, const double* act, const double* adv,
+                           const double* ret, const double* old, const double* ov, size_t N, size_t D,
+                           size_t H, size_t L, size_t A, double vfCoef, double entCoef, double clipEps,
+                           double vfClip, double* g, double* newlp, double* newval, int threads);
 
 /* ---- Muon / Newton-Schulz ---- */
 /* The reference's 5-triple schedule (pufferblas.c:1362-1364). */

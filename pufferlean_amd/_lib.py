@@ -39,6 +39,10 @@ class MuonCoefs(C.Structure):
                 ("max_grad_norm", C.c_float), ("gscale", C.c_float), ("nsteps", C.c_int),
                 ("math", C.c_int), ("coeffs", C.c_void_p)]
 
+class MLPDims(C.Structure):
+    _fields_ = [("N", C.c_int), ("D", C.c_int), ("H", C.c_int), ("L", C.c_int), ("A", C.c_int)]
+
+
 class ReplayCols(C.Structure):
     _fields_ = [("dtype", C.c_int), ("time_major", C.c_int), ("N", C.c_size_t), ("T", C.c_size_t),
                 ("K", C.c_size_t), ("adv", C.c_void_p), ("value", C.c_void_p), ("ratio", C.c_void_p),
@@ -76,6 +80,10 @@ SIGNATURES: dict[str, list] = {
     "ph_mingru_ppo_grad_md": [vp, vp, vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_mingru_muon": [vp, vp, vp, vp, vp, vp],
     "ph_mingru_step": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "ph_mlp_param_count": [vp],
+    "ph_mlp_forward": [vp, i32, vp, vp, vp, vp],
+    "ph_mlp_ppo_grad": [vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "ph_mlp_update": [vp, i32, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "ph_seg_l1": [vp, vp, vp],
     "ph_prio_sample": [vp, sz, sz, dbl, dbl, u64, vp, vp, vp],
     "ph_mb_gather": [vp, vp, vp, sz, vp, vp, vp],
@@ -135,7 +143,7 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
 }
-_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long, "ph_ckpt_bytes": C.c_size_t,
+_RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long, "ph_mlp_param_count": C.c_long, "ph_ckpt_bytes": C.c_size_t,
              "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_cuda_available": C.c_uint8}
 
 _lib = None

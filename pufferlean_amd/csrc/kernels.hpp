@@ -25,6 +25,7 @@ enum : int {
   kSlotRollout = 19,  // rollout step: layer inputs, layer products, padded head
   kSlotMgBufs = 20,
   kSlotHeadsPart = 21,     // multi-discrete / Gaussian heads: dashboard-loss block partials
+  kSlotMlpBufs = 22,       // deep MLP update: activations, head outputs and their gradients
   kSlotGemmPadB = 23,      // zero-padded copy of a GEMM's B operand (unaligned shapes)
   kSlotLane = 24,     // 24..47: 8 concurrent update lanes x 3 slots (U, NS buffers, GEMM split-K)
   kSlotHost = 48,     // 48..127: host-buffer entry points
@@ -150,6 +151,8 @@ int colsum_bf16(const uint16_t* X, long N, int J, long ld, float* out, float sca
 int convert(int src_dtype, const void* x, int dst_dtype, void* y, size_t n, hipStream_t st);
 
 long mingru_param_count(const ph_mingru_dims& d);
+constexpr int kMlpMaxLayers = 8;  // hidden layers of the device MLP update
+long mlp_param_count(const ph_mlp_dims& d);
 
 // Prioritised replay (replay.hip). Column descriptor as in the C ABI.
 int seg_l1(const ph_replay_cols& c, double* L1, hipStream_t st);

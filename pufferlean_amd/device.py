@@ -270,6 +270,54 @@ def mingru_step(cfg, params, mom, obs, act, oldlp, oldval, rew, done, logrho, bo
     return params, mom, G
 
 
+# ---- MLP policy (L hidden layers, combined head) -----------------------------------------------------
+
+class MLPConfig:
+    """Dimensions and coefficients of the device MLP update: N rows, obs D, L hidden layers of H, A
+    actions (+ the value column)."""
+
+    def __init__(self, N, D, H, L, A, *, gamma=0.99, lam=0.95, rho_clip=1.0, c_clip=1.0, clip_eps=0.2,
+                 vf_coef=0.5, ent_coef=0.01, vf_clip=0.0, lr=0.015, wd=0.0, mu=0.95, eps=1e-7,
+                 max_grad_norm=0.0, gscale=None, coeffs=CONST_COEFFS, math="f32", muon_math="f32"):
+        import numpy as np
+        self.dims = _L.MLPDims(N, D, H, L, A)
+        self.ppo = _L.PPOCoefs(gamma, lam, rho_clip, c_clip, clip_eps, vf_coef, ent_coef, vf_clip)
+        self._coeffs = np.ascontiguousarray(np.asarray(coeffs, dtype=np.float32).reshape(-1, 3))
+        self.math = {"bf16": _L.PH_MATH_BF16, "f32": _L.PH_MATH_F32}[math]
+        mm = {"bf16": _L.PH_MATH_BF16, "f32": _L.PH_MATH_F32}[muon_math]
+        self.muon = _L.MuonCoefs(lr, wd, mu, eps, max_grad_norm, 1.0 / N if gscale is None else gscale,
+                                 self._coeffs.shape[0], mm, self._coeffs.ctypes.data_as(C.c_void_p))
+
+    @property
+    def P(self):
+        return int(_L.lib().ph_mlp_param_count(C.byref(self.dims)))
+
+
+def mlp_forward(cfg, params, obs, out=None):
+    _dev(params, obs)
+    out = out if out is not None else torch.empty((cfg.dims.N, cfg.dims.A + 1), device=params.device)
+    L.call("ph_mlp_forward", C.byref(cfg.dims), cfg.math, _p(params), _p(obs), _p(out), _stream())
+    return out
+
+
+def mlp_ppo_grad(cfg, params, obs, act, adv, ret, old, ov=None, G=None, newlp=None, newval=None, losses=None):
+    _dev(params, obs, act, adv, ret, old, ov)
+    G = G if G is not None else torch.empty(cfg.P, device=params.device)
+    L.call("ph_mlp_ppo_grad", C.byref(cfg.dims), C.byref(cfg.ppo), cfg.math, _p(params), _p(obs), _p(act),
+           _p(adv), _p(ret), _p(old), _p(ov), _p(G), _p(newlp), _p(newval), _p(losses), _stream())
+    return G
+
+
+def mlp_update(cfg, T, params, mom, obs, act, behav_logp, rew, done, G=None, losses=None):
+    """One PPO+Muon update over N = T*B time-major rows, in place on params/mom; returns G."""
+    _dev(params, mom, obs, act, behav_logp, rew, done)
+    G = G if G is not None else torch.empty(cfg.P, device=params.device)
+    L.call("ph_mlp_update", C.byref(cfg.dims), int(T), C.byref(cfg.ppo), C.byref(cfg.muon), cfg.math,
+           _p(params), _p(mom), _p(obs), _p(act), _p(behav_logp), _p(rew), _p(done), _p(G), _p(losses),
+           _stream())
+    return G
+
+
 # ---- prioritised replay ----------------------------------------------------------------------------
 class ReplayColumns:
     """The rollout columns of N segments x T steps as ph_replay_cols describes them.

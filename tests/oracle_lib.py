@@ -37,6 +37,7 @@ _SIG = {
     "orc_dense_forward": ([vp, vp, vp, sz, sz, sz, vp], None),
     "orc_mlp_forward": ([vp, vp, sz, sz, sz, sz, vp], None),
     "orc_mlp_ppo_grad": ([vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, d, d, d, vp, i], None),
+    "orc_mlp_deep_ppo_grad": ([vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d, d, d, d, vp, vp, vp, i], None),
     "orc_newton_schulz": ([vp, i, i, vp, i, d, i, vp], None),
     "orc_muon_mat": ([i, i, vp, vp, vp, vp, vp, d, d, d, d, d, vp, i, i], None),
     "orc_stepvec": ([i, vp, vp, vp, vp, vp, d, d, d, d], None),
@@ -276,3 +277,20 @@ def sample_cont(Y, dim, rng_state, lslo=-20.0, lshi=2.0):
     out = np.zeros((dim + 2) * N)
     lib().orc_sample_cont(P(Y), O, N, dim, rng_state & 0xFFFFFFFFFFFFFFFF, lslo, lshi, P(out))
     return out
+
+
+def mlp_deep_param_count(D, H, L, A):
+    return H * D + H + (L - 1) * (H * H + H) + (A + 1) * H + A + 1
+
+
+def mlp_deep_ppo_grad(p, obs, act, adv, ret, old, ov, N, D, H, L, A, *, vf=0.5, ent=0.01, clip=0.2,
+                      vfclip=0.0, threads=8):
+    """Summed gradient of the L-hidden-layer combined-head MLP; returns (g, newlp, newval)."""
+    g = np.zeros(mlp_deep_param_count(D, H, L, A))
+    nlp = np.zeros(N)
+    nv = np.zeros(N)
+    lib().orc_mlp_deep_ppo_grad(P(f64(p)), P(f64(obs)), P(f64(act)), P(f64(adv)), P(f64(ret)), P(f64(old)),
+                                None if ov is None else P(f64(ov)), N, D, H, L, A, vf, ent, clip, vfclip,
+                                P(g), P(nlp), P(nv), threads)
+    return g, nlp, nv
+

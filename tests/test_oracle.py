@@ -305,6 +305,59 @@ def test_mlp_ppo_grad_finite_differences():
     np.testing.assert_allclose(g, fd, rtol=1e-5, atol=1e-6)
 
 
+def _deep_objective(p, obs, act, adv, ret, old, ov, N, D, H, L, A, vfclip):
+    O_ = A + 1
+    x = obs.reshape(N, D)
+    off = 0
+    for l in range(L):
+        fan = D if l == 0 else H
+        W = p[off: off + H * fan].reshape(H, fan); off += H * fan
+        b = p[off: off + H]; off += H
+        x = np.maximum(x @ W.T + b, 0)
+    Wo = p[off: off + O_ * H].reshape(O_, H); off += O_ * H
+    out = x @ Wo.T + p[off: off + O_]
+    return sum(_objective(out[n, :A], out[n, A], int(act[n]), adv[n], ret[n], old[n],
+                          None if ov is None else ov[n], 0.5, 0.01, 0.2, vfclip) for n in range(N))
+
+
+def test_mlp_deep_one_layer_is_reference_mlp():
+    N, D, H, A = 33, 6, 9, 4
+    O_ = A + 1
+    P_ = H * D + H + O_ * H + O_
+    p = rng.normal(40, P_) * 0.5
+    obs = rng.randf(41, N * D, -1, 1)
+    act = rng.randint(42, N, A).astype(float)
+    adv, ret = rng.normal(43, N), rng.normal(44, N)
+    old = rng.randf(45, N, -1.8, -0.8)
+    g = np.zeros(P_)
+    L.orc_mlp_ppo_grad(O.P(p), O.P(obs), O.P(act), O.P(adv), O.P(ret), O.P(old), N, H, D, A, 0.5,
+                       0.01, 0.2, O.P(g), 1)
+    gd, _, _ = O.mlp_deep_ppo_grad(p, obs, act, adv, ret, old, None, N, D, H, 1, A, threads=1)
+    assert np.array_equal(gd, g)
+
+
+@pytest.mark.parametrize("L_,vfclip", [(2, 0.0), (3, 0.0), (2, 0.25)])
+def test_mlp_deep_finite_differences(L_, vfclip):
+    N, D, H, A = 10, 4, 6, 2
+    P_ = O.mlp_deep_param_count(D, H, L_, A)
+    p = rng.normal(50 + L_, P_) * 0.6
+    obs = rng.randf(51, N * D, -1, 1)
+    act = rng.randint(52, N, A).astype(float)
+    adv, ret = rng.normal(53, N), rng.normal(54, N)
+    old = rng.randf(55, N, -1.2, -0.4)
+    ov = rng.normal(56, N)
+    g, nlp, nv = O.mlp_deep_ppo_grad(p, obs, act, adv, ret, old, ov, N, D, H, L_, A, vfclip=vfclip,
+                                     threads=1)
+    h = 1e-6
+    fd = np.zeros(P_)
+    for i in range(P_):
+        e = np.zeros(P_); e[i] = h
+        fd[i] = (_deep_objective(p + e, obs, act, adv, ret, old, ov, N, D, H, L_, A, vfclip)
+                 - _deep_objective(p - e, obs, act, adv, ret, old, ov, N, D, H, L_, A, vfclip)) / (2 * h)
+    np.testing.assert_allclose(g, fd, rtol=1e-5, atol=1e-6)
+    assert np.all(np.isfinite(nlp)) and np.all(nlp < 0) and nv.shape == (N,)
+
+
 def test_mlp_forward_matches_numpy():
     N, D, H, O_ = 9, 4, 6, 3
     p = rng.normal(30, H * D + H + O_ * H + O_)
