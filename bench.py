@@ -19,6 +19,8 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
   replay  prioritised replay between V-trace and the BPTT on 4096 segments x 64 with 4096 draws:
           segment |adv| sums, sampler, minibatch gather (+ normalisation), value/ratio iterate, in
           the fp32 time-major layout and in the reference's f64 segment-major layout
+  cartpole the CartPole-sized PPO+Muon update: 1024 envs x 64 steps, MLP 4 -> 128 -> 128 -> (2 + 1),
+          V-trace -> normalisation -> gradient -> Muon, fp32 and bf16 MFMA products
   heads   multi-discrete (heads 9 and 5, 262,144 rows) and Gaussian (4 dims, 131,072 rows) loss
           gradients with their dashboard losses, the two samplers over one step of 4096 / 2048
           agents, and the whole wide update (4 epochs, hidden 128) through its host-buffer entry
@@ -26,6 +28,10 @@ Components, each on its own synthetic seeded inputs already resident in HBM:
 Component times are HIP-event times of a HIP graph holding `steps` launches (device time per launch,
 no host launch path; "us_eager" is the same loop launched from Python). Events are recorded on the
 stream the kernels run on.
+
+CPU baselines (the oracle, on up to 16 host cores of the same box, in the same run): cpu_baseline is the
+headline's (the MinGRU gradient over a sample of segments plus Muon); cpu_baselines holds one per config
+(CartPole update, policy GEMMs, Newton-Schulz batch, V-trace), each the median of repeated runs.
 """
 from __future__ import annotations
 
@@ -277,6 +283,57 @@ def bench_vtrace(steps, warmup):
             "bytes": bytes_, "single_call_us": round(ms1 * 1e3, 2)}
 
 
+# CartPole-sized update: 1024 envs x 64 steps, obs 4 -> 128 -> 128 -> (2 + 1)
+CP_B, CP_T, CP_D, CP_H, CP_L, CP_A = 1024, 64, 4, 128, 2, 2
+
+
+def cartpole_inputs(seed_base=1):
+    """Seeded CartPole workload: weights N(0, 1/fan_in), zero biases, obs U[-1,1], actions uniform over 2,
+    rewards 1, dones Bernoulli(0.02); the behaviour log-probs are filled in from the forward."""
+    import numpy as np
+    from pufferlean_amd import rng
+    s = lambda k: rng.seed_for(seed_base, k)
+    N = CP_B * CP_T
+    parts = []
+    for l in range(CP_L):
+        fan = CP_D if l == 0 else CP_H
+        parts += [rng.normal(s(l), CP_H * fan) / np.sqrt(fan), np.zeros(CP_H)]
+    parts += [rng.normal(s(8), (CP_A + 1) * CP_H) / np.sqrt(CP_H), np.zeros(CP_A + 1)]
+    return np.concatenate(parts), dict(obs=rng.randf(s(10), N * CP_D, -1.0, 1.0), act=rng.randint(s(11), N, CP_A),
+                                       rew=np.ones(N), done=rng.bernoulli(s(12), N, 0.02),
+                                       noise=rng.normal(s(13), N, 0.0, 0.05))
+
+
+def bench_cartpole(steps, warmup):
+    """The whole CartPole PPO update (forward, V-trace, advantage normalisation, PPO gradient, Muon on
+    every matrix) through ph_mlp_update, graph-captured; samples/s = 65,536 rows / update time."""
+    import numpy as np
+    import torch
+    from pufferlean_amd import device as D
+    params, c = cartpole_inputs()
+    N = CP_B * CP_T
+    out = {"rows": N, "envs": CP_B, "horizon": CP_T, "net": f"{CP_D}->{CP_H}x{CP_L}->{CP_A}+1"}
+    flops_fwd = 2.0 * N * (CP_D * CP_H + (CP_L - 1) * CP_H * CP_H + CP_H * (CP_A + 1))
+    for name, math_ in (("f32", "f32"), ("bf16", "bf16")):
+        cfg = D.MLPConfig(N, CP_D, CP_H, CP_L, CP_A, math=math_, muon_math="f32")
+        p0 = _t(params)
+        obs = _t(c["obs"]).view(N, CP_D)
+        act = _t(c["act"], np.int32)
+        lg = D.mlp_forward(cfg, p0, obs)
+        lp = torch.log_softmax(lg[:, :CP_A].double(), 1).gather(1, act.long().view(-1, 1)).view(-1)
+        behav = (lp + _t(c["noise"], np.float64)).float()
+        rew, done = _t(c["rew"]), _t(c["done"])
+        p = p0.clone()
+        mom = torch.zeros_like(p)
+        G = torch.empty_like(p)
+        ms = time_graph(lambda: D.mlp_update(cfg, CP_T, p, mom, obs, act, behav, rew, done, G=G), steps, warmup)
+        tf = 3.0 * flops_fwd / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 1), "samples_per_s": round(N / (ms * 1e-3), 1),
+                     "gemm_tflops": round(tf, 2), "finite": bool(torch.isfinite(p).all().item())}
+    out["gemm_flops"] = 3.0 * flops_fwd
+    return out
+
+
 def bench_replay(steps, warmup):
     import numpy as np
     import torch
@@ -490,30 +547,212 @@ def measured_traffic():
 
 
 # ------------------------------------------------------------------------------------------------
-def cpu_baseline_ppo(budget_s=15.0):
-    """The oracle's single-sequence MinGRU PPO gradient (f64, one thread, the reference CPU path's
-    algorithm) over sampled segments of the headline workload; samples/s = rows / second."""
-    import numpy as np
+# CPU baselines: the oracle (the reference CPU path's algorithm, f64 unless noted) on the host cores of
+# the GPU box, in the same run. Each figure is the median of repeated runs (after one warm-up) within a
+# time budget; the sample each one covers is stated.
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, budget_s, min_reps=3, max_reps=11):
+    import statistics
+    fn()  # warm-up
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < max_reps and (len(ts) < min_reps or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts)
+
+
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
+    return O
+
+
+def cpu_baseline_gemm(nt, budget_s=8.0):
+    """Config 2 on the oracle's blocked f64 GEMM over nt threads (the reference's CPU GEMMs are OpenBLAS
+    dgemm): GFLOP/s per form."""
+    import numpy as np
+    from pufferlean_amd import rng
+    O = _oracle()
+    M, K, N = 16384, 512, 512
+    X = rng.normal(rng.seed_for(2, 0), M * K).reshape(M, K)
+    W = rng.normal(rng.seed_for(2, 1), N * K).reshape(N, K) / np.sqrt(512)
+    dY = rng.normal(rng.seed_for(2, 2), M * N).reshape(M, N)
+    C1 = np.zeros((M, N)); C2 = np.zeros((M, K)); C3 = np.zeros((N, K))
+    forms = {"fwd": lambda: O.lib().orc_gemm_blocked(0, 1, M, N, K, O.P(X), K, O.P(W), K, O.P(C1), N, nt),
+             "dgrad": lambda: O.lib().orc_gemm_blocked(0, 0, M, K, N, O.P(dY), N, O.P(W), K, O.P(C2), K, nt),
+             "wgrad": lambda: O.lib().orc_gemm_blocked(1, 0, N, K, M, O.P(dY), N, O.P(X), K, O.P(C3), K, nt)}
+    out = {}
+    for name, fn in forms.items():
+        t, reps = _median_time(fn, budget_s / 3)
+        out[name] = {"value": round(2.0 * M * N * K / t / 1e9, 2), "unit": "GFLOP/s", "ms": round(t * 1e3, 1),
+                     "reps": reps}
+    return {"forms": out, "cores": nt, "kind": "port",
+            "sample": "the whole 16384x512x512 product per form, f64, blocked and packed, OpenMP"}
+
+
+def cpu_baseline_ns(nt, budget_s=12.0):
+    """Config 3: the oracle's Newton-Schulz (the reference's naive f64 products) on the six matrices over
+    nt threads, and on one thread for one step of one 512x512 matrix, scaled to the batch by flops."""
+    import numpy as np
+    from pufferlean_amd import rng
+    O = _oracle()
+    shapes = [(512, 512)] * 4 + [(512, 1024)] * 2
+    mats = [rng.normal(rng.seed_for(3, i), r * c, 0.0, 0.02).reshape(r, c) for i, (r, c) in enumerate(shapes)]
+    flops = sum(5 * (4 * min(r, c) ** 2 * max(r, c) + 2 * min(r, c) ** 3) for r, c in shapes)
+    old = O.lib().orc_set_threads(nt)
+    try:
+        t_mt, reps = _median_time(lambda: [O.newton_schulz(m, O.BASELINE_COEFFS, 1e-7, form=1) for m in mats],
+                                  budget_s * 0.6, min_reps=2, max_reps=5)
+    finally:
+        O.lib().orc_set_threads(old)
+    one = mats[0]
+    t_1, reps1 = _median_time(lambda: O.newton_schulz(one, O.BASELINE_COEFFS[:1], 1e-7, form=1), budget_s * 0.4,
+                              min_reps=2, max_reps=5)
+    f1 = 4 * 512 ** 3 + 2 * 512 ** 3
+    return {"value": round(flops / t_mt / 1e9, 2), "unit": "GFLOP/s", "us": round(t_mt * 1e6, 1), "cores": nt,
+            "reps": reps, "single_thread": {"value": round(f1 / t_1 / 1e9, 3), "unit": "GFLOP/s",
+                                            "batch_us_scaled": round(t_1 * flops / f1 * 1e6, 1), "reps": reps1},
+            "kind": "port", "sample": "all six matrices x 5 steps on nt threads; one step of one 512x512 "
+                                      "matrix on one thread, scaled to the batch's flops"}
+
+
+def cpu_baseline_vtrace(nt, budget_s=3.0):
+    """Config 4: the oracle's fp32 V-trace scan (puffercuda.cu:120-132 restated) on 4096 x 64,
+    time-major, one thread and nt threads over segments."""
+    import numpy as np
+    from pufferlean_amd import rng
+    O = _oracle()
+    B, T = 4096, 64
+    n = B * T
+    val, rew = O.f32(rng.normal(rng.seed_for(4, 1), n)), O.f32(rng.normal(rng.seed_for(4, 2), n))
+    done = O.f32(rng.bernoulli(rng.seed_for(4, 3), n, 0.01))
+    lr = O.f32(rng.normal(rng.seed_for(4, 4), n, 0.0, 0.1))
+    boot = O.f32(rng.normal(rng.seed_for(4, 5), B))
+    adv = np.zeros(n, np.float32); tgt = np.zeros(n, np.float32)
+    args = lambda: (O.P(rew), O.P(val), O.P(done), O.P(lr), O.P(boot), B, T, 1, 1, 1, 1, 0.99, 0.95, 1.0, 1.0,
+                    O.P(adv), O.P(tgt))
+    t1, r1 = _median_time(lambda: O.lib().orc_vtrace_f32(*args()), budget_s / 2, min_reps=5, max_reps=21)
+    tm, rm = _median_time(lambda: O.lib().orc_vtrace_f32_mt(*args(), nt), budget_s / 2, min_reps=5, max_reps=21)
+    by = 24.0 * n + 4.0 * B
+    return {"value": round(by / tm / 1e9, 2), "unit": "GB/s", "us": round(tm * 1e6, 1), "cores": nt, "reps": rm,
+            "single_thread": {"value": round(by / t1 / 1e9, 2), "unit": "GB/s", "us": round(t1 * 1e6, 1),
+                              "reps": r1},
+            "kind": "port", "sample": "the whole 4096 x 64 fp32 scan (bootstrapped variant, log-ratio input)"}
+
+
+def cpu_baseline_cartpole(nt, budget_s=12.0):
+    """Config 1: the whole CartPole update on the oracle (f64): forward, V-trace, normalisation, the
+    gradient of the 4->128->128->3 MLP, Muon on the three matrices; GEMMs and NS products on nt threads."""
+    import numpy as np
+    O = _oracle()
+    params, c = cartpole_inputs()
+    N = CP_B * CP_T
+    act = c["act"].astype(float)
+    z = np.zeros(N)
+    _, lp, _ = O.mlp_deep_ppo_grad(params, c["obs"], act, z, z, z, None, N, CP_D, CP_H, CP_L, CP_A, threads=nt)
+    behav = lp + c["noise"]
+    cf = O.coeffs_array(O.BASELINE_COEFFS)
+
+    def update():
+        _, lpn, val = O.mlp_deep_ppo_grad(params, c["obs"], act, z, z, z, None, N, CP_D, CP_H, CP_L, CP_A,
+                                          threads=nt)
+        adv, tgt = O.vtrace(c["rew"], val, c["done"], lpn - behav, None, CP_B, CP_T, variant=0, time_major=True,
+                            rho_is_log=True)
+        advn = np.zeros(N)
+        O.lib().orc_adv_normalize(O.P(adv), N, O.P(advn))
+        g, _, _ = O.mlp_deep_ppo_grad(params, c["obs"], act, advn, tgt, behav, None, N, CP_D, CP_H, CP_L, CP_A,
+                                      threads=nt)
+        off = 0
+        for l in range(CP_L + 1):
+            rows, cols = (CP_A + 1 if l == CP_L else CP_H), (CP_D if l == 0 else CP_H)
+            k = rows * cols
+            a = np.zeros(k); b = np.zeros(k)
+            O.lib().orc_muon_mat(rows, cols, O.P(params[off:off + k].copy()), O.P(g[off:off + k] / N),
+                                 O.P(np.zeros(k)), O.P(a), O.P(b), 1.0, 0.015, 0.0, 0.95, 1e-7, O.P(cf), 5, 1)
+            off += k + rows
+
+    old = O.lib().orc_set_threads(nt)
+    try:
+        t, reps = _median_time(update, budget_s, min_reps=3, max_reps=11)
+    finally:
+        O.lib().orc_set_threads(old)
+    return {"value": round(N / t, 1), "unit": "samples/s", "ms": round(t * 1e3, 1), "cores": nt, "reps": reps,
+            "kind": "port", "sample": "the whole 65,536-row update (two forwards: V-trace inputs, then the "
+                                      "gradient's), f64"}
+
+
+def cpu_baseline_ppo(nt, budget_s=20.0):
+    """Config 5 (the headline): the oracle's single-sequence MinGRU PPO gradient (f64, the reference CPU
+    path's algorithm) over a sample of segments spread on nt threads, scaled to the 4096 segments, plus
+    Muon (f64 Newton-Schulz, nt threads) on the five matrices; samples/s = 262,144 / (gradient + Muon)."""
+    import numpy as np
+    O = _oracle()
     params, cols = mingru_inputs(B5, T5, D5, H5, L5, A5)
     P = params.size
-    obs = cols["obs"].reshape(T5, B5, D5)
-    seg_cols = {k: cols[k].reshape(T5, B5) for k in ("act", "rew", "val", "old", "done")}
-    t0 = time.perf_counter()
-    done_segs = 0
-    out = np.zeros(P + 2 * T5)
-    while time.perf_counter() - t0 < budget_s and done_segs < B5:
-        b = done_segs
-        f = lambda k: O.f64(seg_cols[k][:, b])
-        O.lib().orc_mingru_ppo_grad_seq(O.P(params), O.P(O.f64(obs[:, b, :])), O.P(f("act")),
-                                        O.P(f("rew")), O.P(f("val")), O.P(f("old")), O.P(f("done")),
-                                        O.P(f("val")), T5, H5, D5, L5, A5, 0.5, 0.01, 0.2, 0.0, O.P(out))
-        done_segs += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(done_segs * T5 / dt, 1), "unit": "samples/s", "cores": 1, "kind": "port",
-            "sample": f"{done_segs} of 4096 segments x 64 steps: forward+backward PPO gradient "
-                      f"(f64, single thread) in {dt:.1f} s; Muon (<2% of the CPU step) not included"}
+    S = min(B5, 4 * nt)
+    obs = cols["obs"].reshape(T5, B5, D5)[:, :S, :]
+    pick = lambda k: O.f64(cols[k].reshape(T5, B5)[:, :S])
+    act, rew, val, old_, done = (pick(k) for k in ("act", "rew", "val", "old", "done"))
+    out = np.zeros(P + 2 * T5 * S)
+    grad = lambda: O.lib().orc_mingru_ppo_grad_batch(
+        O.P(params), O.P(O.f64(obs)), O.P(act), O.P(rew), O.P(val), O.P(old_), O.P(done), O.P(val), S, T5, H5,
+        D5, L5, A5, 0.5, 0.01, 0.2, 0.0, O.P(out), nt)
+    t_g, reps = _median_time(grad, budget_s * 0.6, min_reps=2, max_reps=5)
+    cf = O.coeffs_array(O.BASELINE_COEFFS)
+    szE, szL = H5 * D5, 3 * H5 * H5
+    mats = [(0, H5, D5)] + [(szE + H5 + l * szL, 3 * H5, H5) for l in range(L5)]
+    offDec = szE + H5 + L5 * szL
+    mats += [(offDec, A5, H5), (offDec + A5 * H5 + A5, 1, H5)]
+    g = out[:P] / (B5 * T5)
+
+    def muon():
+        for off, r, c in mats:
+            k = r * c
+            a = np.zeros(k); b = np.zeros(k)
+            O.lib().orc_muon_mat(r, c, O.P(params[off:off + k].copy()), O.P(g[off:off + k].copy()),
+                                 O.P(np.zeros(k)), O.P(a), O.P(b), 1.0, 0.015, 0.0, 0.95, 1e-7, O.P(cf), 5, 1)
+
+    old = O.lib().orc_set_threads(nt)
+    try:
+        t0 = time.perf_counter()
+        muon()
+        t_m = time.perf_counter() - t0
+    finally:
+        O.lib().orc_set_threads(old)
+    t_step = t_g * B5 / S + t_m
+    return {"value": round(B5 * T5 / t_step, 1), "unit": "samples/s", "cores": nt, "kind": "port",
+            "sample": f"gradient of {S} of 4096 segments x 64 steps on {nt} threads (median of {reps}), scaled to "
+                      f"4096, plus one Muon pass over the 5 matrices (f64 Newton-Schulz, {nt} threads, "
+                      f"{t_m:.2f} s); step {t_step:.1f} s",
+            "gradient_s_per_segment": round(t_g / S, 4), "muon_s": round(t_m, 2)}
+
+
+def cpu_baselines(only):
+    nt = cpu_threads()
+    out = {"threads": nt, "cpu_model": cpu_model(), "nproc": os.cpu_count()}
+    for name, fn in (("cartpole", cpu_baseline_cartpole), ("gemm", cpu_baseline_gemm), ("ns", cpu_baseline_ns),
+                     ("vtrace", cpu_baseline_vtrace)):
+        if only in ("all", name):
+            out[name] = fn(nt)
+            print(f"# cpu baseline {name} done", file=sys.stderr, flush=True)
+    return out
 
 
 def main():
@@ -562,6 +801,9 @@ def main():
     if args.only in ("all", "heads"):
         comps["heads"] = bench_heads(args.steps, args.warmup)
         print("# heads done", file=sys.stderr, flush=True)
+    if args.only in ("all", "cartpole"):
+        comps["cartpole"] = bench_cartpole(args.steps, args.warmup)
+        print("# cartpole done", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": head["samples_per_s"] if head else None,
@@ -570,10 +812,11 @@ def main():
         "ms_per_step": head["ms"] if head else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded splitmix64; random-init weights)",
-        "config": {"workload": "MinGRU PPO+Muon minibatch step: obs 128 -> enc 512 -> 2x MinGRU 512 -> "
-                               "16-way + value; 4096 segments x 64 steps",
+        "config": {"workload": "MinGRU PPO+Muon minibatch step: obs 128 -> enc 512 -> 2x MinGRU 512 "
+                               "(sequential scan over the 64 steps, as the reference trains) -> 16-way + value; "
+                               "4096 segments x 64 steps",
                    "segments": B5, "horizon": T5, "hidden": H5, "layers": L5, "actions": A5,
-                   "obs": D5},
+                   "obs": D5, "scan": "sequential"},
     }
     if head:
         dk = head["dominant_kernel"]
@@ -583,8 +826,12 @@ def main():
                             "algorithmic_bytes": dk["hbm_bytes"]}
         line["step"] = {k: v for k, v in head.items() if k != "dominant_kernel"}
     line["components"] = comps
-    if not args.no_cpu_baseline and head:
-        line["cpu_baseline"] = cpu_baseline_ppo()
+    if not args.no_cpu_baseline:
+        nt = cpu_threads()
+        if head:
+            line["cpu_baseline"] = dict(cpu_baseline_ppo(nt), cpu_model=cpu_model())
+            print("# cpu baseline ppo done", file=sys.stderr, flush=True)
+        line["cpu_baselines"] = cpu_baselines(args.only)
     print(json.dumps(line))
     return 0
 

@@ -56,6 +56,10 @@
  *                                orc_ppo_grad; the clamp mask zeroes saturated log-stds
  *   orc_sample_md / _cont        numpy inverse-CDF / Box-Muller on the pinned splitmix64 words; Gaussian
  *                                draw moments; K = 1 logp equals log softmax
+ *   timed CPU baselines          orc_vtrace_f32_mt equals orc_vtrace_f32 bit for bit; orc_gemm_blocked
+ *                                equals numpy matmul within roundoff; orc_mingru_ppo_grad_batch equals
+ *                                the sum of orc_mingru_ppo_grad_seq over its segments; threaded
+ *                                Newton-Schulz (orc_set_threads) equals the serial one bit for bit
  *   orc_wide_losses              mode 1 with K = 1 equals orc_ppo_losses; two heads equal one head over
  *                                the product space; mode 2 logp and entropy against scipy's normal
  *                                logpdf / entropy; special cases (adv 0, ratio 1, no value clip)
@@ -501,8 +505,20 @@ const double ORC_MUON_COEFFS[5][3] = {
     {4.0848, -6.8946, 2.9270}, {3.9505, -6.3029, 2.6377}, {3.7418, -5.5913, 2.3037},
     {2.8769, -3.1427, 1.2046}, {2.8366, -3.0525, 1.2012}};
 
+/* Threads of the naive Newton-Schulz products (orc_set_threads; 1 unless a timed CPU baseline sets it).
+ * Each output row is one thread's, so the results do not depend on the count. */
+static int g_ns_threads = 1;
+int orc_set_threads(int n) {
+  int old = g_ns_threads;
+  g_ns_threads = n > 1 ? n : 1;
+  return old;
+}
+
 /* C[m x n] = A[m x k] B[k x n], naive, accumulation over l in ascending order (Muon.lean:19-32). */
 static void mm_naive(const double* A, const double* B, double* C, int m, int k, int n) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(g_ns_threads) if (g_ns_threads > 1)
+#endif
   for (int i = 0; i < m; i++)
     for (int j = 0; j < n; j++) {
       double t = 0.0;
@@ -1230,3 +1246,165 @@ void orc_sample_cont(const double* Y, size_t ldy, size_t N, size_t d, uint64_t r
     out[(d + 1) * N + n] = row[2 * d];
   }
 }
+
+/* ------------------------------------------------------------------------------------------------ */
+/* Timed CPU baselines (bench.py's cpu_baseline legs). Same arithmetic as the functions above, spread
+ * over threads. */
+
+/* V-trace over segments in parallel (each segment's scan is orc_vtrace_f32's, unchanged). */
+void orc_vtrace_f32_mt(const float* rew, const float* val, const float* term, const float* rho,
+                       const float* boot, size_t B, size_t T, int variant, int time_major, int rho_is_log,
+                       int clamp, float gamma, float lam, float rhoClip, float cClip, float* adv, float* tgt,
+                       int threads) {
+  int nt = threads > 1 ? threads : 1;
+  size_t chunk = (B + (size_t)nt - 1) / (size_t)nt;
+  {
+    /* thread w scans segments [b0, b1) in either layout */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nt)
+#endif
+    for (int w = 0; w < nt; w++) {
+      size_t b0 = (size_t)w * chunk, b1 = b0 + chunk < B ? b0 + chunk : B;
+      for (size_t b = b0; b < b1; b++) {
+        float last = 0;
+        size_t t0;
+        if (variant == 0) {
+          if (T == 0) continue;
+          size_t il = time_major ? (T - 1) * B + b : b * T + T - 1;
+          adv[il] = 0;
+          if (tgt) tgt[il] = adv[il] + val[il];
+          t0 = T - 1;
+        } else {
+          t0 = T;
+        }
+        for (size_t k = 0; k < t0; k++) {
+          size_t t = t0 - 1 - k;
+          size_t i = time_major ? t * B + b : b * T + t;
+          size_t in = time_major ? (t + 1) * B + b : b * T + t + 1;
+          float wgt = rho_is_log ? expf(rho[i]) : rho[i];
+          float rh = wgt < rhoClip ? wgt : rhoClip;
+          float c = wgt < cClip ? wgt : cClip;
+          float r = clamp ? clamp1f(rew[i]) : rew[i];
+          float delta, nnt;
+          if (variant == 0) {
+            nnt = (term[i] != 0) ? 0.0f : 1.0f;
+            delta = rh * (r + gamma * val[in] * nnt - val[i]);
+          } else {
+            nnt = (term[i] > 0.5f) ? 0.0f : 1.0f;
+            float vnext = (t + 1 < T) ? val[in] : boot[b];
+            delta = rh * r + gamma * vnext * nnt - val[i];
+          }
+          last = delta + gamma * lam * c * last * nnt;
+          adv[i] = last;
+          if (tgt) tgt[i] = last + val[i];
+        }
+      }
+    }
+  }
+}
+
+/* C = op(A) op(B) (row-major, f64) with cache blocking: threads take 64-row blocks of C; for each
+ * 256-deep k block the op(B) panel is packed contiguous per thread and every C row block is updated
+ * in 4 x 8 register tiles. A timing baseline for the policy GEMMs (the reference runs them through
+ * OpenBLAS cblas_dgemm, pufferblas.c:720-743). */
+void orc_gemm_blocked(int transA, int transB, size_t M, size_t N, size_t K, const double* A, size_t lda,
+                      const double* B, size_t ldb, double* C, size_t ldc, int threads) {
+  enum { MB = 64, KB = 256 };
+  int nt = threads > 1 ? threads : 1;
+  long nblk = (long)((M + MB - 1) / MB);
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nt)
+#endif
+  {
+    double* Bp = (double*)malloc(sizeof(double) * KB * (N ? N : 1));
+    double* Ap = (double*)malloc(sizeof(double) * MB * KB);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (long blk = 0; blk < nblk; blk++) {
+      size_t i0 = (size_t)blk * MB, mb = i0 + MB <= M ? MB : M - i0;
+      for (size_t i = 0; i < mb; i++) for (size_t j = 0; j < N; j++) C[(i0 + i) * ldc + j] = 0.0;
+      for (size_t k0 = 0; k0 < K; k0 += KB) {
+        size_t kb = k0 + KB <= K ? KB : K - k0;
+        /* pack op(B)[k0..k0+kb) x N as kb rows of N, op(A) block as mb rows of kb */
+        for (size_t k = 0; k < kb; k++)
+          for (size_t j = 0; j < N; j++) Bp[k * N + j] = transB ? B[j * ldb + k0 + k] : B[(k0 + k) * ldb + j];
+        for (size_t i = 0; i < mb; i++)
+          for (size_t k = 0; k < kb; k++) Ap[i * kb + k] = transA ? A[(k0 + k) * lda + i0 + i] : A[(i0 + i) * lda + k0 + k];
+        size_t i = 0;
+        for (; i + 4 <= mb; i += 4) {
+          size_t j = 0;
+          for (; j + 8 <= N; j += 8) {
+            double acc[4][8] = {{0}};
+            for (size_t k = 0; k < kb; k++) {
+              const double* br = Bp + k * N + j;
+              for (int r = 0; r < 4; r++) {
+                double a = Ap[(i + r) * kb + k];
+                for (int q = 0; q < 8; q++) acc[r][q] += a * br[q];
+              }
+            }
+            for (int r = 0; r < 4; r++) for (int q = 0; q < 8; q++) C[(i0 + i + r) * ldc + j + q] += acc[r][q];
+          }
+          for (; j < N; j++)
+            for (int r = 0; r < 4; r++) {
+              double t = 0.0;
+              for (size_t k = 0; k < kb; k++) t += Ap[(i + r) * kb + k] * Bp[k * N + j];
+              C[(i0 + i + r) * ldc + j] += t;
+            }
+        }
+        for (; i < mb; i++)
+          for (size_t j = 0; j < N; j++) {
+            double t = 0.0;
+            for (size_t k = 0; k < kb; k++) t += Ap[i * kb + k] * Bp[k * N + j];
+            C[(i0 + i) * ldc + j] += t;
+          }
+      }
+    }
+    free(Bp); free(Ap);
+  }
+}
+
+/* Summed single-sequence MinGRU gradients over B segments of time-major columns (obs [T][B][D], the
+ * rest [T][B]), segments spread over threads; each thread sums its segments in order, then the thread
+ * sums are added in thread order. out = [G (P) | newlp [T][B] | newval [T][B]]. */
+void orc_mingru_ppo_grad_batch(const double* p, const double* obs, const double* act, const double* adv,
+                               const double* ret, const double* old, const double* term, const double* ov,
+                               size_t B, size_t T, size_t H, size_t D, size_t L, size_t A, double vfCoef,
+                               double entCoef, double clipEps, double vfClip, double* out, int threads) {
+  int nt = threads > 1 ? threads : 1;
+  size_t P = H * D + H + L * 3 * H * H + A * H + A + H + 1;
+  double* part = (double*)calloc((size_t)nt * P, sizeof(double));
+  size_t chunk = (B + (size_t)nt - 1) / (size_t)nt;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nt)
+#endif
+  for (int w = 0; w < nt; w++) {
+    double* seq = (double*)malloc(sizeof(double) * T * (D + 7));
+    double* res = (double*)malloc(sizeof(double) * (P + 2 * T));
+    double* ob = seq; double* ac = ob + T * D; double* ad = ac + T; double* re = ad + T; double* ol = re + T;
+    double* te = ol + T; double* ovs = te + T;
+    size_t b0 = (size_t)w * chunk, b1 = b0 + chunk < B ? b0 + chunk : B;
+    for (size_t b = b0; b < b1; b++) {
+      for (size_t t = 0; t < T; t++) {
+        size_t r = t * B + b;
+        memcpy(ob + t * D, obs + r * D, sizeof(double) * D);
+        ac[t] = act[r]; ad[t] = adv[r]; re[t] = ret[r]; ol[t] = old[r]; te[t] = term[r];
+        ovs[t] = ov ? ov[r] : 0.0;
+      }
+      mingru_seq(p, ob, ac, ad, re, ol, te, ovs, T, H, D, L, A, 0, NULL, vfCoef, entCoef, clipEps, vfClip, res);
+      for (size_t i = 0; i < P; i++) part[(size_t)w * P + i] += res[i];
+      for (size_t t = 0; t < T; t++) {
+        out[P + t * B + b] = res[P + t];
+        out[P + T * B + t * B + b] = res[P + T + t];
+      }
+    }
+    free(seq); free(res);
+  }
+  for (size_t i = 0; i < P; i++) {
+    double s = 0.0;
+    for (int w = 0; w < nt; w++) s += part[(size_t)w * P + i];
+    out[i] = s;
+  }
+  free(part);
+}
+

@@ -187,6 +187,19 @@ void orc_sample_md(const double* Y, size_t ldy, size_t N, const int* sizes, size
 void orc_sample_cont(const double* Y, size_t ldy, size_t N, size_t d, uint64_t rng, double lslo, double lshi,
                      double* out);
 
+/* timed CPU baselines */
+int orc_set_threads(int n);
+void orc_vtrace_f32_mt(const float* rew, const float* val, const float* term, const float* rho,
+                       const float* boot, size_t B, size_t T, int variant, int time_major, int rho_is_log,
+                       int clamp, float gamma, float lam, float rhoClip, float cClip, float* adv, float* tgt,
+                       int threads);
+void orc_gemm_blocked(int transA, int transB, size_t M, size_t N, size_t K, const double* A, size_t lda,
+                      const double* B, size_t ldb, double* C, size_t ldc, int threads);
+void orc_mingru_ppo_grad_batch(const double* p, const double* obs, const double* act, const double* adv,
+                               const double* ret, const double* old, const double* term, const double* ov,
+                               size_t B, size_t T, size_t H, size_t D, size_t L, size_t A, double vfCoef,
+                               double entCoef, double clipEps, double vfClip, double* out, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,12 @@ _SIG = {
     "orc_ppo_grad_cont": ([vp, sz, vp, vp, vp, vp, vp, sz, sz, d, d, d, d, d, d, vp, sz, vp, vp], None),
     "orc_sample_md": ([vp, sz, sz, vp, sz, C.c_uint64, vp], None),
     "orc_sample_cont": ([vp, sz, sz, sz, C.c_uint64, d, d, vp], None),
+    "orc_set_threads": ([i], i),
+    "orc_vtrace_f32_mt": ([vp, vp, vp, vp, vp, sz, sz, i, i, i, i, C.c_float, C.c_float, C.c_float, C.c_float,
+                           vp, vp, i], None),
+    "orc_gemm_blocked": ([i, i, sz, sz, sz, vp, sz, vp, sz, vp, sz, i], None),
+    "orc_mingru_ppo_grad_batch": ([vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, d, d, d, d, vp, i],
+                                  None),
     "orc_wide_losses": ([i, vp, sz, vp, vp, vp, vp, vp, sz, vp, sz, sz, d, d, d, d, d, d, vp], None),
 }
 
