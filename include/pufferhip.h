@@ -494,14 +494,23 @@ uint8_t ph_ffi_cuda_available(void);
  *     (ph_mb_gather) and, after the BPTT, value/ratio of the drawn segments are iterated in place
  *     (ph_mb_iterate), exactly the reference's order;
  *   host mode: scal = [act (K per row)|adv|ret|old|term|ov] (nscal >= (K+5)*T*B).
- * Either way out receives the reference's host form [g (P); new_logp (T*B); new_value (T*B)] (the
- * reference also returns this form in device-column mode when its resident gradient buffer is
- * unavailable). Precision: bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
-int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
-                            size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L, size_t A,
-                            size_t K, const double* hs, size_t nhs, double vfCoef, double entCoef,
+ * The returned length is the mode, as the reference's return size (Puffer/Float/CUDA.lean:138-148,
+ * puffercuda.cu:5237-5248, 5560-5580):
+ *   *out_len = 0 (resident): the device-column mode leaves the summed gradient on the device for the
+ *     next ph_cuda_mingru_muon_resident with an empty gClip, copies nothing back and does not wait;
+ *   *out_len = P + 2*T*B (host): out receives [g (P); new_logp (T*B); new_value (T*B)]; the host mode
+ *     always, the device-column mode only if the resident gradient buffer cannot be allocated.
+ * out must hold P + 2*T*B. params: nparams >= P host weights, or nparams = 0 to take the weights the
+ * last resident Muon step left in its policy handle (the reference's g_mgw hand-off).
+ * Precision: bf16 activations and MFMA when PUFFER_MG_PREC=bf16, else fp32. */
+int ph_cuda_mingru_ppo_grad(const double* params, size_t nparams, const double* obs, size_t nobs,
+                            const double* scal, size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L,
+                            size_t A, size_t K, const double* hs, size_t nhs, double vfCoef, double entCoef,
                             double clipEps, double vfClip, const double* segIdx, size_t nseg,
-                            const double* mbPrio, size_t nprio, double* out);
+                            const double* mbPrio, size_t nprio, double* out, size_t* out_len);
+/* No counterpart in the reference (a test and debugging aid): copies the unconsumed resident gradient
+ * (P values) to out without consuming it. */
+int ph_cuda_mg_resident_grad(size_t P, double* out);
 /* Prioritised replay, host-buffer forms. The resident columns are library-owned, one set per
  * process (the reference's g_dc* buffers), bound to the device current at ph_cuda_mg_prep. */
 /* lean_cuda_mg_prep (puffercuda.cu:316-336): upload the rollout columns rew, term, logp, val (N*T
@@ -568,12 +577,19 @@ int ph_cuda_mlp_ppo_grad_md(const double* params, const double* obs, const doubl
 int ph_cuda_mlp_ppo_grad_cont(const double* params, const double* obs, const double* acts, const double* advs,
                               const double* rets, const double* oldlps, size_t N, size_t H, size_t D, size_t d,
                               double vfCoef, double entCoef, double clipEps, uint8_t bf16, double* g);
-/* lean_cuda_mingru_muon_resident (puffercuda.cu:5727), host-gradient mode: gClip (nG >= P) is the
- * clipped gradient; Muon on every flattenMG matrix of the handle (fp32-MFMA Newton-Schulz on f64
- * state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the biases, in place. wOut: P. */
+/* lean_cuda_mingru_muon_resident (puffercuda.cu:5727-5976): Muon on every flattenMG matrix of the
+ * handle (fp32-MFMA Newton-Schulz on f64 state; PUFFER_MUON_EXACT=1: exact f64), stepvec on the
+ * biases, in place. Two gradient forms, as the reference's:
+ *   nG >= P (host): gClip is the gradient, already clipped by the caller; wOut (P) receives the new
+ *     weights, *wOut_len = P;
+ *   nG = 0 (resident): consumes the gradient the last device-column ph_cuda_mingru_ppo_grad left on the
+ *     device, clips it there (s = sum (g*gscale)^2; cc = (maxGradNorm > 0 and sqrt(s) > maxGradNorm ?
+ *     maxGradNorm/sqrt(s) : 1)*gscale, k_gclip_norm/k_gclip_scale, puffercuda.cu:5122-5131), copies
+ *     nothing back and does not wait, *wOut_len = 0; an error if no such gradient is present.
+ * Either way the next ph_cuda_mingru_ppo_grad may pass nparams = 0 to use the new weights. */
 int ph_cuda_mingru_muon_resident(size_t policyH, const double* gClip, size_t nG, size_t H, size_t D,
                                  size_t L, size_t A, double lr, double wd, double mu, double eps,
-                                 double maxGradNorm, double gscale, double* wOut);
+                                 double maxGradNorm, double gscale, double* wOut, size_t* wOut_len);
 
 #ifdef __cplusplus
 }

@@ -125,8 +125,9 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_mlp_forward_batch_bf16": [dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_ffi_bench_bf16_resident": [sz, sz, sz, sz],
     "ph_ffi_cuda_available": [],
-    "ph_cuda_mingru_ppo_grad": [dptr, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dptr, sz, dbl, dbl, dbl,
-                                dbl, dptr, sz, dptr, sz, dptr],
+    "ph_cuda_mingru_ppo_grad": [dptr, sz, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dptr, sz, dbl, dbl,
+                                dbl, dbl, dptr, sz, dptr, sz, dptr, szptr],
+    "ph_cuda_mg_resident_grad": [sz, dptr],
     "ph_cuda_mg_prep": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz],
     "ph_cuda_mg_cols_ready": [sz, sz, C.POINTER(C.c_uint8)],
     "ph_cuda_mg_obs_traj": [dptr, sz, sz, sz],
@@ -141,7 +142,7 @@ SIGNATURES: dict[str, list] = {
     "ph_cuda_mlp_ppo_grad_md": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, u8, dptr],
     "ph_cuda_mlp_ppo_grad_cont": [dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dbl, dbl, dbl, u8, dptr],
     "ph_ffi_gather_seq_minibatch": [dptr, dptr, dptr, dptr, dptr, dptr, dptr, dptr, sz, sz, sz, sz, dptr],
-    "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr],
+    "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr, szptr],
 }
 _RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long, "ph_mlp_param_count": C.c_long, "ph_ckpt_bytes": C.c_size_t,
              "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_cuda_available": C.c_uint8}

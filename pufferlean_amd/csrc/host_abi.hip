@@ -58,7 +58,27 @@ enum : int {
   kHsSample = kSlotHost + 16, // sampler staging
   kHsObsTraj = kSlotHost + 17,  // resident obs trajectory of the MinGRU chain (f32)
   kHsHeads = kSlotHost + 18,    // multi-discrete / continuous head staging
+  kHsGradRes = kSlotHost + 19,  // the MinGRU gradient left on the device for the resident Muon (f64)
 };
+
+// The resident hand-off between the MinGRU gradient and the resident Muon (the reference's bg 70 with
+// its g_mgg_fresh stamp, and the g_mgw stamp of the weights the Muon leaves for the next gradient,
+// puffercuda.cu:5237-5248, 5560-5580, 5727-5768, 5950-5968). The gradient stamp is consumed by one Muon
+// step; the weights stamp names the policy handle whose weights the next gradient may take when the
+// caller passes no parameters.
+struct ResGrad {
+  bool fresh = false;
+  int dev = -1;
+  long P = 0;
+};
+ResGrad g_mgg;
+struct ResWeights {
+  bool valid = false;
+  int dev = -1;
+  long P = 0;
+  size_t handle = 0;
+};
+ResWeights g_mgw;
 
 // Carves typed sub-buffers from one scratch slot: run the layout once to size it, allocate, run it
 // again to assign.
@@ -873,6 +893,7 @@ extern "C" int ph_cuda_policy_download(size_t handle, size_t P, double* pm) {
   return down(pm, (const void*)handle, 16 * P);
 }
 extern "C" int ph_cuda_policy_free(size_t handle) {
+  if (handle && g_mgw.handle == handle) g_mgw = ResWeights{};
   if (handle) {
     PH_CHECK_HIP(hipDeviceSynchronize());
     PH_CHECK_HIP(hipFree((void*)handle));
@@ -1135,6 +1156,7 @@ struct DcState {
 };
 DcState g_dc;
 
+
 // The resident obs trajectory [N*T][D] f32, row e*T+t (the reference's g_dMGObsTraj,
 // puffercuda.cu:2136), bound to the device current when it was stored.
 struct ObsTraj {
@@ -1341,11 +1363,12 @@ extern "C" int ph_ffi_gather_seq_minibatch(const double* obsCol, const double* a
 // or the device-column mode (puffercuda.cu:5226-5240 mode choice; 5366-5383 gather; 5554-5558
 // iterate). obs is always the host array: the resident obs trajectory belongs to a rollout, which
 // this library does not run. Writes out[P + 2*T*B] = [summed gradient | new_logp | new_value].
-extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, size_t nobs, const double* scal,
-                                       size_t nscal, size_t B, size_t T, size_t H, size_t D, size_t L,
-                                       size_t A, size_t K, const double* hs, size_t nhs, double vfCoef,
+extern "C" int ph_cuda_mingru_ppo_grad(const double* params, size_t nparams, const double* obs, size_t nobs,
+                                       const double* scal, size_t nscal, size_t B, size_t T, size_t H, size_t D,
+                                       size_t L, size_t A, size_t K, const double* hs, size_t nhs, double vfCoef,
                                        double entCoef, double clipEps, double vfClip, const double* segIdx,
-                                       size_t nseg, const double* mbPrio, size_t nprio, double* out) {
+                                       size_t nseg, const double* mbPrio, size_t nprio, double* out,
+                                       size_t* out_len) {
   // K > 1: A is the logits width (the sum of the K head sizes in hs) and the action column is K wide
   // (puffercuda.cu:5202-5205, 5216-5220)
   const size_t Kh = K < 1 ? 1 : K;
@@ -1377,7 +1400,7 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
              "ph_cuda_mingru_ppo_grad: obs holds %zu of %zu values and no resident obs trajectory matches "
              "(the device-column mode with a ph_cuda_mg_obs_traj trajectory of N=%ld segments, T=%zu, D=%zu)",
              nobs, TB * D, g_dc.N, T, D);
-  PH_REQUIRE(params && (useTraj || obs) && out && (devCol || scal), "ph_cuda_mingru_ppo_grad: null buffer");
+  PH_REQUIRE((useTraj || obs) && out && out_len && (devCol || scal), "ph_cuda_mingru_ppo_grad: null buffer");
   if (devCol && !prioRes) {
     PH_REQUIRE(nseg >= B && nprio >= B && segIdx && mbPrio,
                "ph_cuda_mingru_ppo_grad: segIdx/mbPrio hold %zu/%zu of %zu draws", nseg, nprio, B);
@@ -1385,6 +1408,16 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   }
   ph_mingru_dims d{(int)B, (int)T, (int)D, (int)H, (int)L, (int)A, env_is("PUFFER_MG_PREC", "bf16") ? 0 : 1};
   const long P = mingru_param_count(d);
+  // empty params: the weights the last resident Muon step left on the device (its policy handle)
+  if (nparams == 0) {
+    if (dev < 0) PH_CHECK_HIP(hipGetDevice(&dev));
+    PH_REQUIRE(g_mgw.valid && g_mgw.P == P && g_mgw.dev == dev,
+               "ph_cuda_mingru_ppo_grad: empty params but no resident weights of P=%ld on this device (the "
+               "resident Muon leaves them; a policy handle freed since then drops them)", P);
+  } else {
+    PH_REQUIRE(params && nparams >= (size_t)P, "ph_cuda_mingru_ppo_grad: params hold %zu of P=%ld values",
+               nparams, P);
+  }
   ph_ppo_coefs c{};
   c.vf_coef = vfCoef; c.ent_coef = entCoef; c.clip_eps = clipEps; c.vf_clip = vfClip;
   double *dp, *dx, *ds, *losses, *segd, *mpd;
@@ -1396,7 +1429,7 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
     sf = cv.take<float>(NS); G = cv.take<float>(P); nlp = cv.take<float>(TB); nv = cv.take<float>(TB);
     act = cv.take<int>(Kh * TB); segd = cv.take<double>(B); mpd = cv.take<double>(B); segi = cv.take<int>(B);
   }));
-  PH_TRY(up(dp, params, P * 8));
+  if (nparams) PH_TRY(up(dp, params, P * 8));
   if (!useTraj) PH_TRY(up(dx, obs, TB * D * 8));
   const int* seg = nullptr;
   if (devCol) {
@@ -1416,7 +1449,7 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   } else {
     PH_TRY(up(ds, scal, NS * 8));
   }
-  PH_TRY(to_f32(dp, pf, P, nullptr));
+  PH_TRY(to_f32(nparams ? dp : (const double*)g_mgw.handle, pf, P, nullptr));
   if (useTraj) {
     k_gather_obs_traj<<<ceil_div(TB * D, kT), kT>>>(g_traj.obs, seg, (long)B, (long)T, (long)D, xf);
     PH_LAUNCH_CHECK();
@@ -1436,6 +1469,23 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   if (devCol) {
     const ph_replay_cols cols = dc_cols();
     PH_TRY(mb_iterate(cols, seg, B, nlp, nv, nullptr));
+    // resident mode (the reference's size-0 return): the summed gradient stays on the device for the
+    // resident Muon, nothing is copied back and nothing waits; host mode only if that buffer cannot be had
+    double* gres = (double*)scratch(kHsGradRes, P * 8);
+    if (gres) {
+      k_f32_f64<<<ceil_div(P, kT), kT>>>(G, gres, P, 1.0);
+      PH_LAUNCH_CHECK();
+      g_mgg.fresh = true;
+      g_mgg.dev = dev;
+      g_mgg.P = P;
+      *out_len = 0;
+      if (g_mgLossOn) {
+        PH_TRY(finish());
+        PH_TRY(down(g_mgLoss, losses, 7 * 8));
+      }
+      return PH_OK;
+    }
+    (void)hipGetLastError();
   }
   double* o = (double*)scratch(kHsMgOut, (P + 2 * TB) * 8);
   if (!o) return PH_ERR_NOMEM;
@@ -1445,7 +1495,19 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
   PH_LAUNCH_CHECK();
   PH_TRY(finish());
   if (g_mgLossOn) PH_TRY(down(g_mgLoss, losses, 7 * 8));
+  *out_len = (size_t)P + 2 * TB;
   return down(out, o, (P + 2 * TB) * 8);
+}
+
+extern "C" int ph_cuda_mg_resident_grad(size_t P, double* out) {
+  int dev = -1;
+  PH_CHECK_HIP(hipGetDevice(&dev));
+  PH_REQUIRE(out && g_mgg.fresh && g_mgg.P == (long)P && g_mgg.dev == dev,
+             "ph_cuda_mg_resident_grad: no unconsumed resident gradient of P=%zu", P);
+  double* gres = (double*)scratch_peek(kHsGradRes);
+  PH_REQUIRE(gres, "ph_cuda_mg_resident_grad: resident gradient buffer missing");
+  PH_TRY(finish());
+  return down(out, gres, P * 8);
 }
 
 // Host-gradient mode of lean_cuda_mingru_muon_resident (puffercuda.cu:5727): the clipped gradient
@@ -1455,20 +1517,36 @@ extern "C" int ph_cuda_mingru_ppo_grad(const double* params, const double* obs, 
 // not provided.
 extern "C" int ph_cuda_mingru_muon_resident(size_t policyH, const double* gClip, size_t nG, size_t H, size_t D,
                                             size_t L, size_t A, double lr, double wd, double mu, double eps,
-                                            double maxGradNorm, double gscale, double* wOut) {
-  (void)maxGradNorm;
-  (void)gscale;
+                                            double maxGradNorm, double gscale, double* wOut, size_t* wOut_len) {
   PH_REQUIRE(policyH != 0, "ph_cuda_mingru_muon_resident: no policy handle");
   const size_t szE = H * D, szL = 3 * H * H;
   const size_t P = szE + H + L * szL + A * H + A + H + 1;
-  PH_REQUIRE(gClip && nG >= P, "ph_cuda_mingru_muon_resident: the host gradient (P=%zu) is required", P);
-  PH_REQUIRE(wOut, "ph_cuda_mingru_muon_resident: null output");
+  PH_REQUIRE(wOut_len, "ph_cuda_mingru_muon_resident: null output length");
+  int dev = -1;
+  PH_CHECK_HIP(hipGetDevice(&dev));
+  // empty gClip: consume the gradient the last MinGRU gradient call left on the device, clipped here
+  // (k_gclip_norm / k_gclip_scale, puffercuda.cu:5122-5131); the stamp is consumed by this step
+  const bool gres = nG == 0 && g_mgg.fresh && g_mgg.P == (long)P && g_mgg.dev == dev;
+  if (nG == 0) g_mgg.fresh = false;
+  PH_REQUIRE(nG > 0 || gres,
+             "ph_cuda_mingru_muon_resident: empty gClip but no resident gradient of P=%zu is present (the "
+             "MinGRU gradient leaves one only in its device-column mode)", P);
+  PH_REQUIRE(gres || (gClip && nG >= P), "ph_cuda_mingru_muon_resident: gClip holds %zu of P=%zu values", nG,
+             P);
+  PH_REQUIRE(gres || wOut, "ph_cuda_mingru_muon_resident: null output");
   const bool mixed = !env_is("PUFFER_MUON_EXACT", "1");
   double* W = (double*)policyH;
   double* M = W + P;
-  double* G = (double*)scratch(kHsGrad, P * 8);
-  if (!G) return PH_ERR_NOMEM;
-  PH_TRY(up(G, gClip, P * 8));
+  double* G;
+  if (gres) {
+    G = (double*)scratch_peek(kHsGradRes);
+    PH_REQUIRE(G, "ph_cuda_mingru_muon_resident: resident gradient buffer missing");
+    PH_TRY(gclip_f64(G, (long)P, gscale, maxGradNorm, nullptr));
+  } else {
+    G = (double*)scratch(kHsGrad, P * 8);
+    if (!G) return PH_ERR_NOMEM;
+    PH_TRY(up(G, gClip, P * 8));
+  }
   const size_t offW = szE + H, offDec = offW + L * szL, offBDec = offDec + A * H, offVal = offBDec + A,
                offBVal = offVal + H;
   PH_TRY(muon_f64((int)H, (int)D, W, G, M, 1.0, lr, wd, mu, eps, mixed, nullptr));
@@ -1480,6 +1558,17 @@ extern "C" int ph_cuda_mingru_muon_resident(size_t policyH, const double* gClip,
   PH_TRY(stepvec_f64((long)A, W + offBDec, G + offBDec, M + offBDec, 1.0, lr, wd, mu, nullptr));
   PH_TRY(muon_f64(1, (int)H, W + offVal, G + offVal, M + offVal, 1.0, lr, wd, mu, eps, mixed, nullptr));
   PH_TRY(stepvec_f64(1, W + offBVal, G + offBVal, M + offBVal, 1.0, lr, wd, mu, nullptr));
+  // the next gradient may take these weights from the handle (empty params)
+  g_mgw.valid = true;
+  g_mgw.dev = dev;
+  g_mgw.P = (long)P;
+  g_mgw.handle = policyH;
+  if (gres) {  // resident form: nothing copied back, nothing waited for (the reference's empty return)
+    PH_LAUNCH_CHECK();
+    *wOut_len = 0;
+    return PH_OK;
+  }
   PH_TRY(finish());
+  *wOut_len = P;
   return down(wOut, W, P * 8);
 }

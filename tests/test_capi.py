@@ -65,11 +65,11 @@ def test_host_entries_reject_bad_arguments_without_device():
     import ctypes as C
     lib = L.lib()
     hs = np.array([1.0, 1.0])  # two heads summing to 2, not A = 3
-    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, hs.ctypes.data_as(L.dptr), 2,
-                                       0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None) == L.PH_ERR_ARG
+    assert lib.ph_cuda_mingru_ppo_grad(None, 0, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, hs.ctypes.data_as(L.dptr),
+                                       2, 0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None, None) == L.PH_ERR_ARG
     assert b"head sizes sum to 2" in lib.ph_last_error()
-    assert lib.ph_cuda_mingru_ppo_grad(None, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, None, 0,
-                                       0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None) == L.PH_ERR_ARG
+    assert lib.ph_cuda_mingru_ppo_grad(None, 0, None, 0, None, 0, 1, 1, 8, 8, 1, 3, 2, None, 0,
+                                       0.5, 0.01, 0.2, 0.0, None, 0, None, 0, None, None) == L.PH_ERR_ARG
     assert lib.ph_cuda_policy_download(0, 4, None) == L.PH_ERR_ARG
 
 

@@ -410,8 +410,10 @@ def test_mingru_md_host_mode_matches_oracle(gpu, monkeypatch, prec, tol):
     ov = rng.normal(0xB3B, n).reshape(T, B)
     scal = np.concatenate([act.ravel()] + [a.ravel() for a in (adv, ret, old, term, ov)])
     out = np.zeros(Pn + 2 * n)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), scal.size, B, T, H, D, Ln, W, K,
-           dp(np.array(sizes, np.float64)), K, 0.5, 0.01, 0.2, 0.2, None, 0, None, 0, dp(out))
+    ln = C.c_size_t(0)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), n * D, dp(scal), scal.size, B, T, H, D, Ln, W, K,
+           dp(np.array(sizes, np.float64)), K, 0.5, 0.01, 0.2, 0.2, None, 0, None, 0, dp(out), C.byref(ln))
+    assert ln.value == out.size
     g, nlp = _mg_md_oracle(p, obs, act, adv, ret, old, term, ov, T, B, H, D, Ln, W, sizes)
     assert rel(out[:Pn], g) < tol
     assert rel(out[Pn:Pn + n], nlp.ravel()) < tol
@@ -447,17 +449,24 @@ def test_mingru_md_device_column_mode(gpu, monkeypatch):
     hs = np.array(sizes, np.float64)
     args = (B, T, H, D, Ln, W, K, dp(hs), K, 0.5, 0.01, 0.2, 0.2)
     out_host = np.zeros(Pn + 2 * T * B)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
-           dp(out_host))
+    ln = C.c_size_t(0)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
+           dp(out_host), C.byref(ln))
+    assert ln.value == out_host.size
+    # device-column mode: the gradient stays on the device (resident mode, zero-length result)
     out_dev = np.zeros_like(out_host)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B, dp(out_dev))
-    assert rel(out_dev, out_host) < 1e-5
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
+           dp(out_dev), C.byref(ln))
+    assert ln.value == 0
+    g_dev = np.zeros(Pn)
+    L.call("ph_cuda_mg_resident_grad", Pn, dp(g_dev))
+    assert rel(g_dev, out_host[:Pn]) < 1e-5
     # a K-wide call does not gather from columns of another width
     L.call("ph_cuda_mg_prep", dp(rew), dp(term), dp(act[:, 0].copy()), dp(logp), dp(val), dp(boot), N, T, 1)
     L.call("ph_cuda_mg_vtrace", N, T, 0.99, 0.95, 1.0, 1.0, dp(L1))
     with pytest.raises(L.PufferHipError, match="no scalar source"):
-        L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
-               dp(out_dev))
+        L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
+               dp(out_dev), C.byref(ln))
 
 
 def test_mingru_rollout_step_then_multi_discrete_draw(gpu):

@@ -376,8 +376,10 @@ def test_mingru_grad_host_mode_matches_oracle(gpu, monkeypatch):
     ov = rng.normal(0x1A8, n).reshape(T, B)
     scal = np.concatenate([a.ravel() for a in (act, adv, ret, old, term, ov)])
     out = np.zeros(Pn + 2 * n)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), n * D, dp(scal), 6 * n, B, T, H, D, Ln, A, 1, None, 0, 0.5,
-           0.01, 0.2, 0.2, None, 0, None, 0, dp(out))
+    ln = C.c_size_t(0)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), n * D, dp(scal), 6 * n, B, T, H, D, Ln, A, 1, None, 0,
+           0.5, 0.01, 0.2, 0.2, None, 0, None, 0, dp(out), C.byref(ln))
+    assert ln.value == out.size
     g = np.zeros(Pn)
     nlp = np.zeros((T, B))
     for b in range(B):
@@ -420,8 +422,10 @@ def test_mingru_muon_resident_host_gradient(gpu, monkeypatch):
         L.call("ph_cuda_policy_load", dp(np.concatenate([W, M])), Pn, C.byref(h))
         try:
             wout = np.zeros(Pn)
+            wl = C.c_size_t(0)
             L.call("ph_cuda_mingru_muon_resident", h.value, dp(G), Pn, H, D, Ln, A, 0.02, 0.0, 0.95, 1e-7, 0.5, 1.0,
-                   dp(wout))
+                   dp(wout), C.byref(wl))
+            assert wl.value == Pn
             full = np.zeros(2 * Pn)
             L.call("ph_cuda_policy_download", h.value, Pn, dp(full))
         finally:

@@ -294,14 +294,20 @@ def test_mg_chain_device_columns_match_host_path(gpu, monkeypatch):
     obs = np.ascontiguousarray(obs_roll[idx.astype(np.int64)].transpose(1, 0, 2))  # [T][B][D]
     args = (B, T, H, Dm, Ln, A, 1, None, 0, 0.5, 0.01, 0.2, 0.2)
     out_host = np.zeros(Pn + 2 * T * B)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
-           dp(out_host))
+    ln = C.c_size_t(0)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, dp(scal), scal.size, *args, None, 0, None, 0,
+           dp(out_host), C.byref(ln))
+    assert ln.value == out_host.size
 
-    # device-column mode with the same draws: the same gather on the same resident data
+    # device-column mode with the same draws: the same gather on the same resident data; the gradient
+    # stays on the device (resident mode: zero-length result)
     out_dev = np.zeros_like(out_host)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
-           dp(out_dev))
-    assert np.array_equal(out_dev, out_host)
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, None, 0, *args, dp(idx), B, dp(mp), B,
+           dp(out_dev), C.byref(ln))
+    assert ln.value == 0
+    g_dev = np.zeros(Pn)
+    L.call("ph_cuda_mg_resident_grad", Pn, dp(g_dev))
+    assert np.array_equal(g_dev, out_host[:Pn])
 
     # ... and it iterated value/ratio of the drawn segments: V-trace again sees the new columns
     nlp = out_host[Pn:Pn + T * B].astype(np.float32)
@@ -322,15 +328,20 @@ def test_mg_chain_device_columns_match_host_path(gpu, monkeypatch):
     L.call("ph_ffi_prio_sample", dp(L1b), N, T, B, alpha, beta, 0x99, dp(idx3), dp(mp3))
     obs3 = np.ascontiguousarray(obs_roll[idx3.astype(np.int64)].transpose(1, 0, 2))
     out_res = np.zeros_like(out_host)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs3), obs3.size, None, 0, *args, None, 0, None, 0, dp(out_res))
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs3), obs3.size, None, 0, *args, None, 0, None, 0, dp(out_res),
+           C.byref(ln))
+    assert ln.value == 0
+    g_res = np.zeros(Pn)
+    L.call("ph_cuda_mg_resident_grad", Pn, dp(g_res))
     scal3, _ = O.gather_seq_minibatch(act, logp, term, adv2, val2, idx3, mp3, T)
     out_chk = np.zeros_like(out_host)
-    L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs3), obs3.size, dp(scal3), scal3.size, *args, None, 0, None, 0,
-           dp(out_chk))
-    assert relmax(out_res, out_chk) < 1e-5
+    L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs3), obs3.size, dp(scal3), scal3.size, *args, None, 0, None,
+           0, dp(out_chk), C.byref(ln))
+    assert relmax(g_res, out_chk[:Pn]) < 1e-5
     # the stamp was consumed: without scal or draws there is no scalar source
     with pytest.raises(L.PufferHipError, match="no scalar source"):
-        L.call("ph_cuda_mingru_ppo_grad", dp(p), dp(obs), obs.size, None, 0, *args, None, 0, None, 0, dp(out_res))
+        L.call("ph_cuda_mingru_ppo_grad", dp(p), Pn, dp(obs), obs.size, None, 0, *args, None, 0, None, 0,
+               dp(out_res), C.byref(ln))
     monkeypatch.setenv("PUFFER_MG_DEVPRIO", "0")
     L.call("ph_cuda_mg_vtrace_prio", N, T, gam, lam, rc, cc, B, alpha, beta, 0x99, C.byref(used))
     assert used.value == 0
