@@ -482,6 +482,27 @@ int ph_ffi_mlp_forward_batch_bf16(const double* p, const double* X, size_t N, si
 double ph_ffi_bench_bf16_resident(size_t N, size_t D, size_t H, size_t reps);
 /* lean_ffi_cuda_available (pufferblas.c:1348-1352). */
 uint8_t ph_ffi_cuda_available(void);
+/* The persistent resident MLP policy of the rollout (lean_ffi_mlp_policy_load / _update / _forward /
+ * _free, pufferblas.c:460-592): flattenMLP weights [W1(H*D) | b1(H) | W2(O*H) | b2(O)] uploaded once
+ * (W1 as bf16 RNE of its fp32 value, the rest fp32) into an opaque handle on the current device; the
+ * forward sends the N x D observations up as bf16, runs relu(X W1^T + b1) (bf16 products, fp32 out,
+ * kept on the device) then (. W2^T + b2) (bf16 MFMA on fp32), and returns Y[N*O] f64. update re-uploads
+ * the weights (dims unchanged); free releases the handle. Where the reference falls back to its host
+ * weights or returns 0, these return an error status. */
+int ph_ffi_mlp_policy_load(const double* params, size_t D, size_t H, size_t O, size_t* handle);
+int ph_ffi_mlp_policy_update(size_t handle, const double* params);
+int ph_ffi_mlp_policy_forward(size_t handle, const double* X, size_t N, double* Y);
+int ph_ffi_mlp_policy_free(size_t handle);
+/* The handle's output width O (0 for a null handle): the forward returns N*O values. */
+size_t ph_ffi_mlp_policy_outputs(size_t handle);
+/* lean_ffi_bench_mlp2_bf16_resident (pufferblas.c:421-452): GF/s (2ND*H + 2NHO per forward) of `reps`
+ * device-resident two-layer forwards (after 5 warm-up passes); lean_ffi_bench_mlp2_bf16_wres
+ * (pufferblas.c:598-636): the same with the bf16 observations uploaded and the outputs downloaded
+ * (pinned staging) every forward. -1 without a device. */
+double ph_ffi_bench_mlp2_bf16_resident(size_t N, size_t D, size_t H, size_t O, size_t reps);
+double ph_ffi_bench_mlp2_bf16_wres(size_t N, size_t D, size_t H, size_t O, size_t reps);
+/* lean_cuda_selftest (puffercuda.cu:41-60): out[i] = 2i + 1 computed on the device (n values). */
+int ph_cuda_selftest(size_t n, double* out);
 /* lean_cuda_mingru_ppo_grad (puffercuda.cu:5206): params (flattenMG, P), obs (nobs >= T*B*D, host,
  * time-major; or nobs = 0 in the device-column mode, which gathers the minibatch from the resident obs
  * trajectory of ph_cuda_mg_obs_traj by the drawn segments, as the reference gathers its rollout's),

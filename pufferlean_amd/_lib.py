@@ -125,6 +125,14 @@ SIGNATURES: dict[str, list] = {
     "ph_ffi_mlp_forward_batch_bf16": [dptr, dptr, sz, sz, sz, sz, dptr],
     "ph_ffi_bench_bf16_resident": [sz, sz, sz, sz],
     "ph_ffi_cuda_available": [],
+    "ph_ffi_mlp_policy_load": [dptr, sz, sz, sz, szptr],
+    "ph_ffi_mlp_policy_update": [sz, dptr],
+    "ph_ffi_mlp_policy_forward": [sz, dptr, sz, dptr],
+    "ph_ffi_mlp_policy_free": [sz],
+    "ph_ffi_mlp_policy_outputs": [sz],
+    "ph_ffi_bench_mlp2_bf16_resident": [sz, sz, sz, sz, sz],
+    "ph_ffi_bench_mlp2_bf16_wres": [sz, sz, sz, sz, sz],
+    "ph_cuda_selftest": [sz, dptr],
     "ph_cuda_mingru_ppo_grad": [dptr, sz, dptr, sz, dptr, sz, sz, sz, sz, sz, sz, sz, sz, dptr, sz, dbl, dbl,
                                 dbl, dbl, dptr, sz, dptr, sz, dptr, szptr],
     "ph_cuda_mg_resident_grad": [sz, dptr],
@@ -145,7 +153,8 @@ SIGNATURES: dict[str, list] = {
     "ph_cuda_mingru_muon_resident": [sz, dptr, sz, sz, sz, sz, sz, dbl, dbl, dbl, dbl, dbl, dbl, dptr, szptr],
 }
 _RESTYPES = {"ph_last_error": C.c_char_p, "ph_mingru_param_count": C.c_long, "ph_mlp_param_count": C.c_long, "ph_ckpt_bytes": C.c_size_t,
-             "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_cuda_available": C.c_uint8}
+             "ph_ffi_bench_bf16_resident": C.c_double, "ph_ffi_bench_mlp2_bf16_resident": C.c_double,
+             "ph_ffi_bench_mlp2_bf16_wres": C.c_double, "ph_ffi_mlp_policy_outputs": C.c_size_t, "ph_ffi_cuda_available": C.c_uint8}
 
 _lib = None
 _lock = threading.Lock()
