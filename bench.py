@@ -58,12 +58,30 @@ def _ev():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_loop(fn, steps, warmup):
-    """Average ms per call of fn() over `steps` calls after `warmup`, bracketed by syncs."""
+# The GPU's clocks ramp up over the first tens of milliseconds of sustained work (a 0.5 ms GEMM runs
+# about 20 % slower in its first ~60 launches of a process); warm-up therefore runs for at least this
+# long, whatever the warm-up count, so the timed region measures steady state.
+WARM_S = 0.25
+
+
+def warm(fn, warmup, min_s=WARM_S):
+    """Run fn() `warmup` times, then keep running it until `min_s` seconds of device work have passed."""
+    import time
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_loop(fn, steps, warmup):
+    """Average ms per call of fn() over `steps` calls after the warm-up, bracketed by syncs."""
+    import torch
+    warm(fn, warmup)
     s, e = _ev()
     s.record()
     for _ in range(steps):
@@ -142,9 +160,7 @@ def bench_ppo_step(steps, warmup, eager=False):
         run = graph.replay
     else:
         run = step
-    for _ in range(2):
-        run()
-    torch.cuda.synchronize()
+    warm(run, 2)
     e0, e1 = _ev()
     e0.record()
     for _ in range(steps):
@@ -188,8 +204,7 @@ def time_graph(fn, steps, warmup):
                 fn()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    g.replay()
-    torch.cuda.synchronize()
+    warm(g.replay, 1)
     a, b = _ev()
     a.record()
     g.replay()

@@ -384,8 +384,12 @@ constexpr bool kChunk8 = (BN % 8 == 0) && ((BM * (BN / 8)) % NT == 0);
 
 // vec: 0 element stores, 4 four-column chunks, 8 eight-column chunks (bf16 C only). Staged rows
 // [0, BM/2) are C rows m0.., rows [BM/2, BM) are C rows mhi.. (mhi = m0 + BM/2 for a contiguous tile).
-template <int EPI, typename TC, int BM, int BN, int NT, int LDC>
-__device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m0, int mhi, int n0, int vec) {
+// NT threads (tid = 0..NT-1) share the tile; WAVE: they are one wavefront flushing its own staging
+// area, so LDS ordering needs no block barrier (a wave's LDS operations complete in issue order).
+template <int EPI, typename TC, int BM, int BN, int NT, int LDC, bool WAVE = false>
+__device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m0, int mhi, int n0, int vec,
+                                             int tid) {
+  static_assert(!WAVE || NT == 64, "a wave-local flush runs on one wavefront");
   auto grow = [&](int lr) { return lr < BM / 2 ? m0 + lr : mhi + (lr - BM / 2); };
   constexpr int CPR = BN / 4;               // 4-column chunks per row
   constexpr int NCH = BM * CPR / NT;        // chunks per thread
@@ -405,14 +409,14 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
         float4 v[G][2];
 #pragma unroll
         for (int q = 0; q < G; q++) {
-          const int c = threadIdx.x + (q0 + q) * NT;
+          const int c = tid + (q0 + q) * NT;
           const float* src = &sC[(c / CPR8) * LDC + (c % CPR8) * 8];
           v[q][0] = *reinterpret_cast<const float4*>(src);
           v[q][1] = *reinterpret_cast<const float4*>(src + 4);
         }
 #pragma unroll
         for (int q = 0; q < G; q++) {
-          const int c = threadIdx.x + (q0 + q) * NT;
+          const int c = tid + (q0 + q) * NT;
           const int lr = c / CPR8, lc = (c % CPR8) * 8;
           const int row = grow(lr), col = n0 + lc;
           if (row >= g.M || col >= g.N) continue;
@@ -433,12 +437,12 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
     float4 v[NCH];
 #pragma unroll
     for (int q = 0; q < NCH; q++) {
-      const int c = threadIdx.x + q * NT;
+      const int c = tid + q * NT;
       v[q] = *reinterpret_cast<const float4*>(&sC[(c / CPR) * LDC + (c % CPR) * 4]);
     }
 #pragma unroll
     for (int q = 0; q < NCH; q++) {
-      const int c = threadIdx.x + q * NT;
+      const int c = tid + q * NT;
       const int lr = c / CPR, lc = (c % CPR) * 4;
       const int row = grow(lr), col = n0 + lc;
       if (row >= g.M || col >= g.N) continue;
@@ -454,7 +458,7 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
   } else if (vec == 0) {
     // unaligned or ragged shapes: element stores
 #pragma unroll 1
-    for (int c = threadIdx.x; c < BM * BN; c += NT) {
+    for (int c = tid; c < BM * BN; c += NT) {
       const int lr = c / BN, lc = c % BN;
       const int row = grow(lr), col = n0 + lc;
       if (row >= g.M || col >= g.N) continue;
@@ -466,9 +470,10 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
   if constexpr (EPI >= 0) {
     if (vec != 0 && g.C2 && g.c2_trans) {
       // transposed bf16 copy: chunks of 4 consecutive rows of one column -> one 8-byte store
-      lds_barrier();
+      if constexpr (WAVE) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      else lds_barrier();
       constexpr int CPC = BM / 4;
-      for (int c = threadIdx.x; c < BN * CPC; c += NT) {
+      for (int c = tid; c < BN * CPC; c += NT) {
         const int lc = c / CPC, lr = (c % CPC) * 4;  // 4 rows inside one half (BM/2 % 4 == 0)
         const int row = grow(lr), col = n0 + lc;
         if (row >= g.M || col >= g.N) continue;
@@ -480,10 +485,12 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
   }
 }
 
-template <typename TC, int BM, int BN, int NT, int LDC>
-__device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0, int n0, int mhi = -1) {
+template <typename TC, int BM, int BN, int NT, int LDC, bool WAVE = false>
+__device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0, int n0, int mhi = -1,
+                                           int tid = -1) {
   static_assert(BM % 8 == 0, "two halves of whole 4-row chunks");
   if (mhi < 0) mhi = m0 + BM / 2;
+  if (tid < 0) tid = threadIdx.x;
   // vector path: every 4-column chunk is whole and 16-byte (fp32) / 8-byte (bf16) aligned
   const bool vec4 = (g.N % 4 == 0) && (g.ws ? true : (g.ldc % 4 == 0 && ((uintptr_t)g.C % 16) == 0)) &&
                     (!g.aux || (g.ldaux % 4 == 0 && ((uintptr_t)g.aux % 16) == 0)) &&
@@ -495,13 +502,13 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
                     (!g.aux || g.ldaux % 8 == 0) &&
                     (!g.C2 || g.c2_trans || (g.ldc2 % 8 == 0 && ((uintptr_t)g.C2 % 16) == 0));
   const int vec = vec8 ? 8 : (vec4 ? 4 : 0);
-  if (g.ws) { flush_tile_t<-1, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); return; }
+  if (g.ws) { flush_tile_t<-1, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); return; }
   switch (g.epi) {
-    case PH_EPI_BIAS: flush_tile_t<PH_EPI_BIAS, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); break;
-    case PH_EPI_BIAS_RELU: flush_tile_t<PH_EPI_BIAS_RELU, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); break;
-    case PH_EPI_RELU_MASK: flush_tile_t<PH_EPI_RELU_MASK, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); break;
-    case PH_EPI_AXPBY: flush_tile_t<PH_EPI_AXPBY, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); break;
-    default: flush_tile_t<PH_EPI_NONE, TC, BM, BN, NT, LDC>(g, sC, m0, mhi, n0, vec); break;
+    case PH_EPI_BIAS: flush_tile_t<PH_EPI_BIAS, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+    case PH_EPI_BIAS_RELU: flush_tile_t<PH_EPI_BIAS_RELU, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+    case PH_EPI_RELU_MASK: flush_tile_t<PH_EPI_RELU_MASK, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+    case PH_EPI_AXPBY: flush_tile_t<PH_EPI_AXPBY, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+    default: flush_tile_t<PH_EPI_NONE, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
   }
 }
 
@@ -890,49 +897,65 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
   const int lr = lane & 31, lk = (lane >> 5) * 16;
-  auto mfma = [&](floatx16& c, const uint4& a, const uint4& b) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  };
-  auto compute = [&](int st) {
+  // Fragments of one k sub-step (16 of the tile's 32 k; lanes 0-31 take k 0-7 of it, lanes 32-63 k 16-23,
+  // and the second sub-step the k 8 above): A rows of the wave's SM sub-tiles, B rows of its SN.
+  struct Frag { uint4 a[SM]; uint4 b[SN]; };
+  auto rd = [&](Frag& f, int st, int koff) {
     const uint16_t* sa = stages + st * STAGE_EL;
     const uint16_t* sb = sa + A_EL;
-    uint4 a0[SM], a1[SM], b0[SN], b1[SN];
 #pragma unroll
-    for (int i = 0; i < SM; i++) {
-      const int row = wm0 + i * 32 + lr;
-      a0[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(row, lk)]);
-      a1[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(row, lk + 8)]);
-    }
+    for (int i = 0; i < SM; i++) f.a[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(wm0 + i * 32 + lr, koff)]);
 #pragma unroll
-    for (int j = 0; j < SN; j++) {
-      const int row = wn0 + j * 32 + lr;
-      b0[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(row, lk)]);
-      b1[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(row, lk + 8)]);
-    }
+    for (int j = 0; j < SN; j++) f.b[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(wn0 + j * 32 + lr, koff)]);
+  };
+  auto mm = [&](const Frag& f) {
 #pragma unroll
     for (int i = 0; i < SM; i++)
 #pragma unroll
-      for (int j = 0; j < SN; j++) mfma(acc[i][j], a0[i], b0[j]);
-#pragma unroll
-    for (int i = 0; i < SM; i++)
-#pragma unroll
-      for (int j = 0; j < SN; j++) mfma(acc[i][j], a1[i], b1[j]);
+      for (int j = 0; j < SN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
+                                                            __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
   };
 
+  // Software pipeline inside each wavefront: the LDS reads of the next sub-step are issued between the
+  // MFMAs of the current one (one read after each product), so their latency and the LDS port time
+  // overlap the matrix core instead of preceding it. The barrier sits between the two sub-steps of a
+  // k-tile: the reads of kt's second half are done by then, and kt + 1's first half is read after it.
   if (nk > 0) {
     issue(0, kbeg);
     issue(1, kbeg + BK);
-    int st = 0;
+    wait_vm<IA + IB>();  // k-tile 0 has landed (1 may be in flight)
+    barrier_mem();
+    issue(2, kbeg + 2 * BK);
+    Frag X, Y;
+    rd(X, 0, lk);
+    int st = 0;  // stage of k-tile kt
 #pragma unroll 1
-    for (int kt = 0; kt < nk; kt++) {
-      wait_vm<IA + IB>();  // this wave's copies of stage kt have landed (kt + 1's may be in flight)
-      barrier_mem();       // ... and every wave's; all waves are done with stage kt - 1
-      issue(st == 0 ? 2 : st - 1, kbeg + (kt + 2) * BK);
-      compute(st);
+    for (int kt = 0; kt < nk - 1; kt++) {
+      rd(Y, st, lk + 8);   // second sub-step of kt, read while the first is multiplied
+      mm(X);
+      wait_vm<IA + IB>();  // this wave's copies of kt + 1 have landed and its reads of kt are done
+      barrier_mem();       // ... every wave's: the stage of kt is free for kt + 3
+      issue(st, kbeg + (kt + 3) * BK);
       st = st == 2 ? 0 : st + 1;
+      rd(X, st, lk);  // first sub-step of kt + 1, read while the second of kt is multiplied
+      mm(Y);
+      // issue order: products of X with the reads of Y between them, then (after the barrier) the
+      // products of Y with the reads of the next X between them
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int q = 0; q < SM + SN; q++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, SM * SN - (SM + SN), 0);
+      }
     }
-    wait_vm<0>();  // the two copies issued past the end land before the LDS is reused
+    rd(Y, st, lk + 8);
+    mm(X);
+    mm(Y);
+    wait_vm<0>();  // the copies issued past the end land before the LDS is reused
   }
   barrier_mem();
   if constexpr (EPR == BM) {
