@@ -200,6 +200,15 @@ int ph_ns_status(void* stream);
 /* Spin bound of those waits, in polls of about a microsecond (0 restores the default, 2^20). A tiny
  * bound makes the waits give up; it exists so that the failure report can be tested. */
 int ph_ns_set_spin_limit(unsigned polls);
+/* Work placement of that launch. Per-XCD queues (on a device of 8 XCDs of 32 CUs, MI355X): each matrix
+ * runs on the CUs of one XCD, with its signals and intermediate data in that XCD's L2; faster for small
+ * matrices, slower for large ones (32 CUs per matrix). The device-wide queue: signals and data go
+ * through memory. 0 (default): per-XCD queues when every Newton-Schulz phase of every matrix has at
+ * most 32 output tiles of 64x64 (min(rows, cols) <= 256 or so), the device-wide queue otherwise;
+ * 1: always device-wide; 2: per XCD whenever the device has them. All give bit-identical matrices. A
+ * queue with work but no workgroups on its XCD is recorded, and ph_ns_status reports it. No
+ * counterpart in the reference. */
+int ph_ns_set_queues(int mode);
 /* In-place Muon matrix step on fp32 state: M <- mu*M + gscale*G; U = gscale*G + mu*M;
  * W <- (1-lr*wd)*W + lr*sqrt(max(1,rows/cols))*NS(U). */
 int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale, float lr,

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, list] = {
     "ph_scratch_retired": [szptr, szptr],
     "ph_ns_status": [vp],
     "ph_ns_set_spin_limit": [u32],
+    "ph_ns_set_queues": [i32],
     "ph_vtrace": [i32, vp, vp, vp, vp, vp, sz, sz, i32, i32, i32, i32, dbl, dbl, dbl, dbl, vp, vp, vp],
     "ph_adv_normalize": [i32, vp, sz, vp, vp, vp],
     "ph_adv_normalize_noalloc": [i32, vp, sz, vp, vp, vp],

@@ -31,12 +31,27 @@
 // line that is read: nothing needs writing back or invalidating between phases, and operand reads
 // keep the L2.
 //
-// Scheduling: every tile of every phase of every matrix is one work item with a ticket number,
-// ordered by (step, phase, matrix, tile). An item waits only for the items of its matrix in
-// earlier phases, i.e. for smaller tickets. Blocks take tickets from an atomic counter in
-// increasing order, so every item waited on has been taken by a block that is already running:
-// the launch completes for any grid size, without assuming that all blocks are co-resident. The
-// last block to leave resets the counters for the next launch on the stream.
+// Scheduling: every tile of every phase of every matrix is one work item with a ticket number in
+// its matrix's queue, ordered by (step, phase, matrix, tile). An item waits only for the items of
+// its matrix in earlier phases, i.e. for smaller tickets of the same queue. A queue's blocks take its
+// tickets from an atomic counter in increasing order, so every item waited on has been taken by a
+// block that is already running: the launch completes for any grid size, without assuming that all
+// blocks are co-resident. The launch's last block to leave resets the counters for the next launch.
+//
+// Queues: one device-wide queue, with device-coherent (write-through) stores, or, on a device of 8
+// XCDs of 32 CUs (MI355X), one queue per XCD, served by the blocks that run on it (the XCC_ID
+// hardware register): each matrix's items, iterates and products then stay on one XCD and its data
+// moves through that XCD's L2 (plain stores, L2 hits; every line a block reads was written earlier in
+// the launch by a block of the same XCD). Control words are device-scope in both (atomics, and
+// relaxed device-scope loads for polling; many blocks poll one word, and polling with atomics
+// serialises them behind the signal they wait for). A dependent phase costs about 6 us per-XCD
+// against 8 us device-wide, but a matrix has 32 CUs instead of 256. Measured (5 steps): one 64x64 matrix 103 us per-XCD against 139 us
+// device-wide, 128x128 119 against 164, but 512x512 425 against 260 and 1536x512 808 against 303.
+// So per-XCD queues are used when every phase of every matrix fits one XCD (at most 32 tiles), the
+// device-wide queue otherwise. Matrices go to queues by estimated work, largest first, each to the
+// least loaded queue. The launch's last block checks that every queue with work had blocks on its
+// XCD, else it raises a sticky flag that ph_ns_status reports.
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -63,19 +78,38 @@ struct NsMat {
   int rows, cols;
 };
 
-// Control words, each polled or updated one on its own 128-byte line: next ticket, blocks finished,
-// wait limit hit in this launch (+1: ever hit, never cleared), items done per matrix.
-constexpr int kCtlTicket = 0, kCtlOut = 32, kCtlFlag = 64, kCtlDone = 96, kCtlStride = 32;
+constexpr int kNsQueues = 8;  // one work queue per XCD
+constexpr int kXcdCus = 32;   // CUs per XCD
+
+// Control words, each polled or updated on its own 128-byte line (32 words): the launch's blocks
+// finished; the wait limit hit in this launch (kCtlFlag; +1: ever hit, +2: a queue with work had no
+// blocks on its XCD, both never cleared by the kernel); the XCDs that had blocks in this launch (bit
+// mask); per queue its next ticket; per matrix its items done.
+constexpr int kCtlStride = 32;
+constexpr int kCtlOut = 0;
+constexpr int kCtlFlag = kCtlStride;
+constexpr int kCtlSeen = 2 * kCtlStride;
+constexpr int kCtlTicket = 3 * kCtlStride;                    // + kCtlStride * q
+constexpr int kCtlDone = kCtlTicket + kCtlStride * kNsQueues;  // + kCtlStride * matrix
 constexpr int kCtlWords = kCtlDone + kCtlStride * kNsMaxMats;
+
+// One queue's share of a launch: its matrices in ticket order and their item counts per phase.
+struct NsQueue {
+  long n0, nt, n3;  // items of P0, of P1 (= P2) and of P3, summed over the queue's matrices
+  int nmat;
+  unsigned char mat[kNsMaxMats];
+};
+static_assert(kNsMaxMats <= 256, "queue slots are bytes");
 
 struct NsLaunch {
   NsMat mat[kNsMaxMats];
+  NsQueue q[kNsQueues];
   float coef[3 * kNsMaxSteps];
   unsigned* ctl;  // control words (kCtl*)
-  long n0, nt, n3;  // item counts of P0, of P1 (= P2) and of P3, summed over the matrices
-  int nmat, nsteps;
+  int nmat, nsteps, nq;
   float eps;
-  unsigned spin;  // wait bound (polls)
+  unsigned spin;   // wait bound (polls)
+  unsigned qmask;  // queues with work (bit q)
 };
 
 // Buffers of step s start at base + s * stride (x*: the step's input iterate, e*/b*: its E and B').
@@ -127,31 +161,38 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Device-coherent stores (relaxed agent-scope atomic stores: write-through, sc1) for every value
-// another block reads in this launch.
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Stores of every value another block reads in this launch. LOCAL (the reader runs on the same XCD):
+// plain stores, which the write-through L1 passes to the XCD's L2. Otherwise device-coherent stores
+// (relaxed agent-scope atomic stores: write-through to memory, sc1).
+template <bool LOCAL, typename T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  if constexpr (LOCAL) *p = v;
+  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_dev(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+// Control-word atomics and polls, device scope (see the scheduling notes).
+__device__ __forceinline__ unsigned ctl_add(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_dev(uint64_t* p, uint64_t v) {
+__device__ __forceinline__ unsigned ctl_load(unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ctl_store(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Thread 0 waits until `need` items of the matrix are done (relaxed polls: the data they guard was
-// written through and is read for the first time after the wait). The wait is bounded: past the
-// limit it raises the launch's flag, and once the flag is up no further wait blocks, so the launch
-// always drains quickly (with wrong results) instead of hanging.
+// Thread 0 waits until `need` items of the matrix are done (relaxed polls: the data they guard is
+// read for the first time after the wait, from the L2 it was written to, or from memory). The wait
+// is bounded: past the limit it raises the launch's flag, and once the flag is up no further wait
+// blocks, so the launch always drains quickly (with wrong results) instead of hanging.
 __device__ void wait_done(unsigned* cnt, unsigned need, unsigned* flag, unsigned limit) {
   if (threadIdx.x == 0) {
     unsigned spins = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need &&
-           __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+    while (ctl_load(cnt) < need && ctl_load(flag) == 0u) {
       __builtin_amdgcn_s_sleep(2);
       if (++spins > limit) {
-        __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(flag + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sticky record
+        ctl_store(flag, 1u);
+        ctl_store(flag + 1, 1u);  // sticky record
         break;
       }
     }
@@ -159,15 +200,14 @@ __device__ void wait_done(unsigned* cnt, unsigned need, unsigned* flag, unsigned
   __syncthreads();
 }
 
-// Every thread's stores have completed, then the item counts as done. All data read by other
-// blocks was written with device-coherent (write-through) stores, so their completion already
-// makes them visible device-wide: no L2 write-back (an agent-scope release fence) is needed, and
-// none is paid for (it measured 5-15 us per item). The asm's memory clobber keeps the compiler
-// from moving stores past the wait.
+// Every thread's stores have completed, then the item counts as done. A completed store has reached
+// the XCD's L2 (LOCAL: where the readers look) or memory (device-coherent stores), so no L2
+// write-back (an agent-scope release fence) is needed, and none is paid for (it measured 5-15 us
+// per item). The asm's memory clobber keeps the compiler from moving stores past the wait.
 __device__ void signal_done(unsigned* cnt) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) ctl_add(cnt, 1u);
 }
 
 // s = 1/(sqrt(sum of the P0 partials) + eps), summed in the same fixed order by every wavefront.
@@ -294,13 +334,15 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& h, uint16_t& l) {
 
 // Store the 4 consecutive-row values q*4..q*4+3 of this lane as 4 consecutive bf16 of the mirrored
 // row (tile column -> row).
+template <bool LOCAL>
 __device__ __forceinline__ void store_mirror4(uint16_t* dst, const uint16_t (&v)[4]) {
-  st_dev(reinterpret_cast<uint64_t*>(dst), (uint64_t)v[0] | ((uint64_t)v[1] << 16) |
-                                               ((uint64_t)v[2] << 32) | ((uint64_t)v[3] << 48));
+  st_dev<LOCAL>(reinterpret_cast<uint64_t*>(dst), (uint64_t)v[0] | ((uint64_t)v[1] << 16) |
+                                                      ((uint64_t)v[2] << 32) | ((uint64_t)v[3] << 48));
 }
 
 // P0: one 64x64 tile of the wide input into the fp32 / bf16 / transposed bf16 copies, plus the
 // tile's sum of squares (fixed order).
+template <bool LOCAL>
 __device__ void p0_convert(const NsMat& mt, const Geo& g, long r, float* stage) {
   const int ti = (int)(r / g.tw), tj = (int)(r % g.tw);
   const int tid = threadIdx.x;
@@ -322,9 +364,9 @@ __device__ void p0_convert(const NsMat& mt, const Geo& g, long r, float* stage) 
     const float v = stage[a * 65 + b];
     ss += v * v;
     const long o = (long)(ti * kT + a) * g.wp + tj * kT + b;
-    st_dev(&g.xf[o], v);
-    st_dev(&g.xb[o], bf16_rne(v));
-    st_dev(&g.xt[(long)(tj * kT + a) * g.mp + ti * kT + b], bf16_rne(stage[b * 65 + a]));
+    st_dev<LOCAL>(&g.xf[o], v);
+    st_dev<LOCAL>(&g.xb[o], bf16_rne(v));
+    st_dev<LOCAL>(&g.xt[(long)(tj * kT + a) * g.mp + ti * kT + b], bf16_rne(stage[b * 65 + a]));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
@@ -334,51 +376,67 @@ __device__ void p0_convert(const NsMat& mt, const Geo& g, long r, float* stage) 
   if (tid == 0) {
     float t = 0.f;
     for (int w = 0; w < kThreads / 64; w++) t += stage[w];
-    st_dev(&g.part[r], t);
+    st_dev<LOCAL>(&g.part[r], t);
   }
 }
 
+// LOCAL: one queue per XCD (block b serves queue b % kNsQueues); otherwise one device-wide queue.
+template <bool LOCAL>
 __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
   __shared__ __align__(16) uint16_t sA[kGroups][2][kT * kPitch];
   __shared__ __align__(16) uint16_t sB[kGroups][2][kT * kPitch];
   __shared__ unsigned s_ticket;
   static_assert(2 * kGroups * 2 * kT * kPitch * 2 + 16 <= kMaxLdsBytes, "LDS budget");
   unsigned* ctl = L.ctl;
-  const long per = 2 * L.nt + L.n3;
-  const long total = L.n0 + (long)L.nsteps * per;
   const int tid = threadIdx.x;
+  int qi = 0;
+  if constexpr (LOCAL) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    qi = (int)(xcc & 0xfu);
+  }
+  if (tid == 0 && qi < kNsQueues)
+    __hip_atomic_fetch_or(&ctl[kCtlSeen], 1u << qi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (qi >= kNsQueues) qi = -1;  // not a queue's XCD: no work (the last block checks coverage)
+  // the queue's counts as values (binding a reference would move the kernel argument to scratch)
+  const int qc = qi < 0 ? 0 : qi;
+  const long qn0 = L.q[qc].n0, qnt = L.q[qc].nt, qn3 = L.q[qc].n3;
+  const int qnmat = L.q[qc].nmat;
+  const long per = 2 * qnt + qn3;
+  const long total = qi < 0 ? 0 : qn0 + (long)L.nsteps * per;
   for (;;) {
-    if (tid == 0) s_ticket = __hip_atomic_fetch_add(&ctl[kCtlTicket], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) s_ticket = total > 0 ? ctl_add(&ctl[kCtlTicket + kCtlStride * qc], 1u) : 0u;
     __syncthreads();
     const long t = (long)s_ticket;
     __syncthreads();
     if (t >= total) break;
-    // decode (phase p, step s, index r within the phase over all matrices)
+    // decode (phase p, step s, index r within the phase over the queue's matrices)
     int p, s = 0;
     long r;
-    if (t < L.n0) {
+    if (t < qn0) {
       p = 0;
       r = t;
     } else {
-      const long u = t - L.n0;
+      const long u = t - qn0;
       s = (int)(u / per);
       r = u - (long)s * per;
-      if (r < L.nt) p = 1;
-      else if (r < 2 * L.nt) { p = 2; r -= L.nt; }
-      else { p = 3; r -= 2 * L.nt; }
+      if (r < qnt) p = 1;
+      else if (r < 2 * qnt) { p = 2; r -= qnt; }
+      else { p = 3; r -= 2 * qnt; }
     }
     int gi = 0;
     Geo g;
-    for (;; gi++) {
+    for (int k = 0;; k++) {
+      gi = L.q[qc].mat[k];
       ns_layout(L.mat[gi].rows, L.mat[gi].cols, L.nsteps, L.mat[gi].ws, g);
       const long cnt = p == 0 ? g.n0 : (p == 3 ? g.n3 : g.nt);
-      if (r < cnt || gi == L.nmat - 1) break;
+      if (r < cnt || k == qnmat - 1) break;
       r -= cnt;
     }
     const NsMat mt = L.mat[gi];  // a copy: a reference would move the kernel argument to scratch
-    unsigned* done = &ctl[kCtlDone + kCtlStride * gi];
+    unsigned* const done = &ctl[kCtlDone + kCtlStride * gi];
     if (p == 0) {
-      p0_convert(mt, g, r, reinterpret_cast<float*>(&sA[0][0][0]));
+      p0_convert<LOCAL>(mt, g, r, reinterpret_cast<float*>(&sA[0][0][0]));
       signal_done(done);
       continue;
     }
@@ -459,18 +517,18 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
           float val;
           if (p == 1) {
             val = sc * sc * v - (row == col ? 1.f : 0.f);
-            st_dev(&ef[o], val);
+            st_dev<LOCAL>(&ef[o], val);
           } else {
             val = cE * ef[o] + c * v;
           }
           split_bf16(val, h4[e4], l4[e4]);
-          st_dev(&hi[o], h4[e4]);
-          st_dev(&lo[o], l4[e4]);
+          st_dev<LOCAL>(&hi[o], h4[e4]);
+          st_dev<LOCAL>(&lo[o], l4[e4]);
         }
         if (ti != tj) {
           const long om = (long)col * g.mp + row0 + acc_row(4 * q);
-          store_mirror4(hi + om, h4);
-          store_mirror4(lo + om, l4);
+          store_mirror4<LOCAL>(hi + om, h4);
+          store_mirror4<LOCAL>(lo + om, l4);
         }
       }
     } else {
@@ -495,31 +553,35 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
               else mt.x[(long)row * mt.cols + col] = v;
             }
           } else {
-            st_dev(&xfn[o], v);
+            st_dev<LOCAL>(&xfn[o], v);
             x4[e4] = bf16_rne(v);
-            st_dev(&xbn[o], x4[e4]);
+            st_dev<LOCAL>(&xbn[o], x4[e4]);
           }
         }
-        if (!last) store_mirror4(xtn + (long)col * g.mp + row0 + acc_row(4 * q), x4);
+        if (!last) store_mirror4<LOCAL>(xtn + (long)col * g.mp + row0 + acc_row(4 * q), x4);
       }
     }
     signal_done(done);
   }
-  // leave; the last block out resets the counters (every other block has taken its final ticket
-  // and finished its items)
+  // Leave. The launch's last block out (every other block has taken its final ticket and finished
+  // its items) checks that every queue with work had blocks on its XCD and resets the counters.
   if (tid == 0) {
     const unsigned out = __hip_atomic_fetch_add(&ctl[kCtlOut], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (out == gridDim.x - 1) {
-      __hip_atomic_store(&ctl[kCtlTicket], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ctl[kCtlFlag], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int i = 0; i < L.nmat; i++)
-        __hip_atomic_store(&ctl[kCtlDone + kCtlStride * i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((L.qmask & ~ctl_load(&ctl[kCtlSeen])) != 0u) ctl_store(&ctl[kCtlFlag + 2], 1u);
+      ctl_store(&ctl[kCtlSeen], 0u);
+      ctl_store(&ctl[kCtlFlag], 0u);
+      for (int q = 0; q < L.nq; q++) ctl_store(&ctl[kCtlTicket + kCtlStride * q], 0u);
+      for (int i = 0; i < L.nmat; i++) ctl_store(&ctl[kCtlDone + kCtlStride * i], 0u);
       __hip_atomic_store(&ctl[kCtlOut], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
 std::atomic<unsigned> g_spin{kSpinLimit};
+// 0: per-XCD queues where the device has 8 XCDs of 32 CUs and every phase of every matrix fits one
+// XCD's CUs; 1: always one device-wide queue; 2: per-XCD queues whenever the device has them
+std::atomic<int> g_queues{0};
 
 __global__ void k_clear_word(unsigned* w) {
   if (threadIdx.x == 0) *w = 0u;
@@ -553,15 +615,29 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
   unsigned* ctl = (unsigned*)scratch(ctl_slot, kCtlWords * 4);
   if (!ctl) return PH_ERR_NOMEM;
   PH_TRY(ensure_zeroed_words(ctl, kCtlWords, st));
+  // per-XCD queues on a device of kNsQueues XCDs of kXcdCus CUs, for batches whose phases all fit one
+  // XCD (one block per CU, so kXcdCus tiles at a time)
+  const int cus = cu_count();
+  const int mode = g_queues.load(std::memory_order_relaxed);
+  bool local = mode != 1 && cus == kNsQueues * kXcdCus;
+  if (local && mode == 0)
+    for (int j = 0; j < n; j++) {
+      Geo g;
+      ns_layout(rows[j], cols[j], nsteps, nullptr, g);
+      if (g.n3 > kXcdCus || g.nt > kXcdCus) local = false;
+    }
   int i = 0;
   while (i < n) {
     // next group of at most kNsMaxMats non-empty matrices
     NsLaunch L{};
     size_t bytes = 0;
+    long work[kNsMaxMats];
+    long n0[kNsMaxMats], nt[kNsMaxMats], n3[kNsMaxMats];
     int j = i;
     for (; j < n && L.nmat < kNsMaxMats; j++) {
       if ((long)rows[j] * cols[j] == 0) continue;
-      NsMat& m = L.mat[L.nmat++];
+      const int k = L.nmat++;
+      NsMat& m = L.mat[k];
       m.x = X[j];
       m.rows = rows[j];
       m.cols = cols[j];
@@ -569,19 +645,51 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
       const size_t b = ns_layout(rows[j], cols[j], nsteps, nullptr, g);
       m.ws = (unsigned char*)(uintptr_t)bytes;  // offset for now
       bytes += b;
-      L.n0 += g.n0;
-      L.nt += g.nt;
-      L.n3 += g.n3;
+      n0[k] = g.n0;
+      nt[k] = g.nt;
+      n3[k] = g.n3;
+      // tile-chunk products of a step: P1 over w, P2 three over m, P3 two over m
+      const long cw = g.wp / kT, cm = g.mp / kT;
+      work[k] = g.n0 + (long)nsteps * (g.nt * cw + 3 * g.nt * cm + 2 * g.n3 * cm);
     }
     i = j;
     if (L.nmat == 0) continue;
     unsigned char* ws = (unsigned char*)scratch(ws_slot, bytes);
     if (!ws) return PH_ERR_NOMEM;
     for (int k = 0; k < L.nmat; k++) L.mat[k].ws = ws + (uintptr_t)L.mat[k].ws;
-    const long total = L.n0 + (long)nsteps * (2 * L.nt + L.n3);
-    if (total >= (1L << 31)) {
-      set_error("newton_schulz (fused): batch too large");
-      return PH_ERR_UNSUPPORTED;
+    // matrices to queues: largest estimated work first, each to the least loaded queue (ties: the
+    // lower index); a queue's matrices are ticketed in matrix order
+    L.nq = local ? kNsQueues : 1;
+    int qof[kNsMaxMats];
+    {
+      int order[kNsMaxMats];
+      for (int k = 0; k < L.nmat; k++) order[k] = k;
+      for (int a = 1; a < L.nmat; a++)  // stable insertion sort by work, descending
+        for (int b = a; b > 0 && work[order[b]] > work[order[b - 1]]; b--) std::swap(order[b], order[b - 1]);
+      long load[kNsQueues] = {};
+      for (int a = 0; a < L.nmat; a++) {
+        int best = 0;
+        for (int q = 1; q < L.nq; q++)
+          if (load[q] < load[best]) best = q;
+        qof[order[a]] = best;
+        load[best] += work[order[a]];
+      }
+    }
+    long total = 0;
+    for (int k = 0; k < L.nmat; k++) {
+      NsQueue& Q = L.q[qof[k]];
+      Q.mat[Q.nmat++] = (unsigned char)k;
+      Q.n0 += n0[k];
+      Q.nt += nt[k];
+      Q.n3 += n3[k];
+    }
+    for (int q = 0; q < L.nq; q++) {
+      const long tq = L.q[q].n0 + (long)nsteps * (2 * L.q[q].nt + L.q[q].n3);
+      if (tq >= (1L << 31)) {
+        set_error("newton_schulz (fused): batch too large");
+        return PH_ERR_UNSUPPORTED;
+      }
+      total += tq;
     }
     for (int k = 0; k < 3 * nsteps; k++) L.coef[k] = coeffs[k];
     L.ctl = ctl;
@@ -589,10 +697,15 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
     L.eps = eps;
     L.spin = g_spin.load(std::memory_order_relaxed);
     // one block per CU: measured faster than two (half as many blocks polling, and a CU's load
-    // bandwidth goes to one tile at a time)
-    const long cap = cu_count();
-    const unsigned grid = (unsigned)(total < cap ? total : cap);
-    k_ns_fused<<<grid, kThreads, 0, st>>>(L);
+    // bandwidth goes to one tile at a time). Per-XCD queues take every CU (block b serves queue
+    // b % kNsQueues; a queue with no items releases its blocks at once).
+    const long cap = cus;
+    const unsigned grid = local ? (unsigned)cap : (unsigned)(total < cap ? total : cap);
+    L.qmask = 0u;
+    for (int q = 0; q < L.nq; q++)
+      if (L.q[q].nmat > 0) L.qmask |= 1u << q;
+    if (local) k_ns_fused<true><<<grid, kThreads, 0, st>>>(L);
+    else k_ns_fused<false><<<grid, kThreads, 0, st>>>(L);
     PH_LAUNCH_CHECK();
   }
   return PH_OK;
@@ -607,18 +720,33 @@ extern "C" int ph_ns_status(void* stream) {
   PH_CHECK_HIP(hipStreamSynchronize(st));
   unsigned* ctl = (unsigned*)scratch_peek(kSlotNsCtl);
   if (!ctl) return PH_OK;  // no fused launch has run on this device
-  unsigned rec = 0;
-  PH_CHECK_HIP(hipMemcpy(&rec, ctl + kCtlFlag + 1, sizeof(rec), hipMemcpyDeviceToHost));
-  if (rec == 0u) return PH_OK;
-  k_clear_word<<<1, 64, 0, st>>>(ctl + kCtlFlag + 1);
+  unsigned rec[2] = {0u, 0u};
+  PH_CHECK_HIP(hipMemcpy(rec, ctl + kCtlFlag + 1, sizeof(rec), hipMemcpyDeviceToHost));
+  if (rec[0] == 0u && rec[1] == 0u) return PH_OK;
+  if (rec[0]) k_clear_word<<<1, 64, 0, st>>>(ctl + kCtlFlag + 1);
+  if (rec[1]) k_clear_word<<<1, 64, 0, st>>>(ctl + kCtlFlag + 2);
   PH_LAUNCH_CHECK();
   PH_CHECK_HIP(hipStreamSynchronize(st));
-  set_error("newton_schulz (fused): a bounded wait for another workgroup's tiles gave up; the matrices "
-            "written by the launches since the last status check are invalid");
+  if (rec[1])
+    set_error("newton_schulz (fused): a workgroup ran on another XCD than its work queue's (the device does "
+              "not dispatch workgroups to XCDs round-robin); the matrices written by the launches since the "
+              "last status check are invalid; ph_ns_set_queues(1) selects the device-wide queue");
+  else
+    set_error("newton_schulz (fused): a bounded wait for another workgroup's tiles gave up; the matrices "
+              "written by the launches since the last status check are invalid");
   return PH_ERR_HIP;
 }
 
 extern "C" int ph_ns_set_spin_limit(unsigned polls) {
   g_spin.store(polls ? polls : kSpinLimit, std::memory_order_relaxed);
+  return PH_OK;
+}
+
+extern "C" int ph_ns_set_queues(int mode) {
+  if (mode < 0 || mode > 2) {
+    set_error("ph_ns_set_queues: mode must be 0 (by shape), 1 (device-wide) or 2 (per XCD)");
+    return PH_ERR_ARG;
+  }
+  g_queues.store(mode, std::memory_order_relaxed);
   return PH_OK;
 }

@@ -167,6 +167,13 @@ def ns_set_spin_limit(polls=0):
     L.call("ph_ns_set_spin_limit", int(polls))
 
 
+def ns_set_queues(mode=0):
+    """Placement of the fused Newton-Schulz work: 0 by shape (per-XCD queues when every phase of every
+    matrix fits one XCD; the default), 1 one device-wide queue, 2 one queue per XCD. All give
+    bit-identical matrices."""
+    L.call("ph_ns_set_queues", int(mode))
+
+
 def scratch_retired():
     """(count, bytes) of scratch buffers retired by growth and not yet released."""
     n, b = C.c_size_t(0), C.c_size_t(0)

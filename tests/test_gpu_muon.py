@@ -158,6 +158,33 @@ def test_gclip(gpu):
     assert rel(t.cpu().numpy(), ref) < 1e-6
 
 
+@pytest.mark.parametrize("shapes", [CONFIG3, CONFIG3 * 2 + [(1536, 512), (48, 700)], [(1536, 512)], [(64, 64), (512, 128)],
+                                    [(128, 4), (128, 128), (2, 128), (1, 128), (200, 64)]],
+                         ids=["config3", "queues-shared", "one", "two", "small"])
+def test_ns_queue_placements_identical(gpu, shapes):
+    """Per-XCD queues and the device-wide queue give the same matrices bit for bit (same tiles, same
+    per-tile order; only where and how the items synchronise differs), including queues that hold
+    several matrices (14 matrices on 8 queues), tall inputs and a batch with idle queues; no block ran
+    off its queue's XCD."""
+    mats = [rng.normal(0x350 + i, r * c, 0.0, 0.02).reshape(r, c).astype(np.float32)
+            for i, (r, c) in enumerate(shapes)]
+    D.ns_status()
+    out = {}
+    try:
+        for mode in (1, 2):
+            D.ns_set_queues(mode)
+            batch = [torch.from_numpy(m).cuda() for m in mats]
+            D.newton_schulz_batch(batch, coeffs=O.BASELINE_COEFFS, math="bf16")
+            D.ns_status()
+            out[mode] = [b.cpu() for b in batch]
+    finally:
+        D.ns_set_queues(0)
+    for a, b in zip(out[2], out[1]):
+        assert torch.equal(a, b)
+    ref = O.newton_schulz(mats[0].astype(np.float64), O.BASELINE_COEFFS, 1e-7, form=1)
+    assert rel(out[2][0].numpy(), ref) < 1e-2
+
+
 def test_ns_wait_failure_is_reported(gpu):
     """A fused launch whose bounded waits give up (forced from the host with a one-poll bound) still
     ends normally, and ph_ns_status reports it once; with the default bound the record stays clear
