@@ -483,6 +483,16 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
         op.bmask = 2;
       }
     }
+    // The epilogue's fp32 operand (E for P2, X for P3) in accumulator layout, loaded before the k loop
+    // so that its memory latency overlaps the products (k-group 0 runs the epilogue).
+    float pre[16];
+    if (tid < 256 && p >= 2) {
+      const float* src = p == 2 ? g.ef + es : g.xf + xs;
+      const long ld = p == 2 ? g.mp : g.wp;
+      const int c0 = tj * kT + acc_col(), r0 = ti * kT;
+#pragma unroll
+      for (int e = 0; e < 16; e++) pre[e] = src[(long)(r0 + acc_row(e)) * ld + c0];
+    }
     floatx16 acc0, acc1;
     mma_tile(op, sA, sB, acc0, acc1, std::make_integer_sequence<int, kSets>{});
     // fold k-group 1's partial tile into group 0's (fixed order), through LDS
@@ -519,7 +529,7 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
             val = sc * sc * v - (row == col ? 1.f : 0.f);
             st_dev<LOCAL>(&ef[o], val);
           } else {
-            val = cE * ef[o] + c * v;
+            val = cE * pre[e] + c * v;
           }
           split_bf16(val, h4[e4], l4[e4]);
           st_dev<LOCAL>(&hi[o], h4[e4]);
@@ -534,7 +544,6 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
     } else {
       const bool last = s == L.nsteps - 1;
       const float abc = a + b + c;
-      const float* xfc = g.xf + xs;
       float* xfn = g.xf + xs + g.mw;  // next step's input (not touched after the last step)
       uint16_t* xbn = g.xb + xs + g.mw;
       uint16_t* xtn = g.xt + xs + g.mw;
@@ -546,7 +555,7 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
           const int e = 4 * q + e4;
           const int row = row0 + acc_row(e);
           const long o = (long)row * g.wp + col;
-          const float v = sc * (abc * xfc[o] + acc0[e]);
+          const float v = sc * (abc * pre[e] + acc0[e]);
           if (last) {
             if (row < g.m && col < g.w) {
               if (g.tall) mt.x[(long)col * mt.cols + row] = v;
