@@ -86,6 +86,11 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
 }
 __device__ __forceinline__ uint16_t bf16_rne(float a) { return (uint16_t)(bf16x2_rne(a, 0.f) & 0xffffu); }
 
+// Logistic function on the hardware exp2 / reciprocal instructions (a few ulp). exp(-x) overflowing
+// to +inf gives exactly 0. Shared by the MinGRU scans and the GEMM epilogue that applies a gate, so
+// both see the same gate value.
+__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
 // Gradient of the (optionally clipped) value loss 0.5 (v - ret)^2 with respect to v: with vfClip > 0
 // and an old value, the loss is max((v - ret)^2, (clip(v - vold) + vold - ret)^2) / 2
 // (d_vloss_grad, puffercuda.cu:692-700).

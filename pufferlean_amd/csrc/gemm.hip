@@ -42,6 +42,8 @@ struct GemmArgs {
   const float* bias;
   const void* aux;  // same dtype as C
   long ldaux;
+  const void* aux2;  // same dtype as C (kEpiGateSkip)
+  long ldaux2;
   float alpha, beta;
   uint16_t* C2;  // optional bf16 copy of the result
   long ldc2;
@@ -225,6 +227,11 @@ __device__ __forceinline__ void epilogue_store_t(const GemmArgs& g, int row, int
     const float x = g.aux ? to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]) : 0.f;
     v = g.alpha * acc + g.beta * x;
   }
+  if constexpr (EPI == kEpiGateSkip) {
+    const float dh = to_f32(reinterpret_cast<const TC*>(g.aux)[(long)row * g.ldaux + col]);
+    const float p = to_f32(reinterpret_cast<const TC*>(g.aux2)[(long)row * g.ldaux2 + col]);
+    v = acc + dh * (1.f - sigm(p));
+  }
   store_out<TC>(reinterpret_cast<TC*>(g.C) + (long)row * g.ldc + col, v);
   if (g.C2) {
     const long o = g.c2_trans ? (long)col * g.ldc2 + row : (long)row * g.ldc2 + col;
@@ -239,6 +246,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int row, int c
     case PH_EPI_BIAS_RELU: epilogue_store_t<PH_EPI_BIAS_RELU, TC>(g, row, col, acc); break;
     case PH_EPI_RELU_MASK: epilogue_store_t<PH_EPI_RELU_MASK, TC>(g, row, col, acc); break;
     case PH_EPI_AXPBY: epilogue_store_t<PH_EPI_AXPBY, TC>(g, row, col, acc); break;
+    case kEpiGateSkip: epilogue_store_t<kEpiGateSkip, TC>(g, row, col, acc); break;
     default: epilogue_store_t<PH_EPI_NONE, TC>(g, row, col, acc); break;
   }
 }
@@ -275,6 +283,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs& g, const floatx16 (&a
     case PH_EPI_BIAS_RELU: write_tile_t<PH_EPI_BIAS_RELU, TC>(g, acc, r0, c0, lane); break;
     case PH_EPI_RELU_MASK: write_tile_t<PH_EPI_RELU_MASK, TC>(g, acc, r0, c0, lane); break;
     case PH_EPI_AXPBY: write_tile_t<PH_EPI_AXPBY, TC>(g, acc, r0, c0, lane); break;
+    case kEpiGateSkip: write_tile_t<kEpiGateSkip, TC>(g, acc, r0, c0, lane); break;
     default: write_tile_t<PH_EPI_NONE, TC>(g, acc, r0, c0, lane); break;
   }
 }
@@ -374,6 +383,12 @@ __device__ __forceinline__ float4 apply_epi4(const GemmArgs& g, int row, int col
     if (g.aux) x = load4_f32(reinterpret_cast<const TC*>(g.aux) + (long)row * g.ldaux + col);
     v.x = g.alpha * v.x + g.beta * x.x; v.y = g.alpha * v.y + g.beta * x.y;
     v.z = g.alpha * v.z + g.beta * x.z; v.w = g.alpha * v.w + g.beta * x.w;
+  }
+  if constexpr (EPI == kEpiGateSkip) {
+    const float4 dh = load4_f32(reinterpret_cast<const TC*>(g.aux) + (long)row * g.ldaux + col);
+    const float4 p = load4_f32(reinterpret_cast<const TC*>(g.aux2) + (long)row * g.ldaux2 + col);
+    v.x += dh.x * (1.f - sigm(p.x)); v.y += dh.y * (1.f - sigm(p.y));
+    v.z += dh.z * (1.f - sigm(p.z)); v.w += dh.w * (1.f - sigm(p.w));
   }
   return v;
 }
@@ -494,12 +509,13 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
   // vector path: every 4-column chunk is whole and 16-byte (fp32) / 8-byte (bf16) aligned
   const bool vec4 = (g.N % 4 == 0) && (g.ws ? true : (g.ldc % 4 == 0 && ((uintptr_t)g.C % 16) == 0)) &&
                     (!g.aux || (g.ldaux % 4 == 0 && ((uintptr_t)g.aux % 16) == 0)) &&
+                    (!g.aux2 || (g.ldaux2 % 4 == 0 && ((uintptr_t)g.aux2 % 16) == 0)) &&
                     (!g.C2 || ((g.c2_trans ? g.M % 4 : g.ldc2 % 4) == 0 && ((uintptr_t)g.C2 % 8) == 0 &&
                                (g.c2_trans ? g.ldc2 % 4 == 0 : true))) &&
                     (!g.bias || ((uintptr_t)g.bias % 16) == 0);
   // 8-column chunks (bf16 C): every chunk whole and its 16-byte C (and row-major C2) store aligned
   const bool vec8 = vec4 && !g.ws && sizeof(TC) == 2 && g.N % 8 == 0 && g.ldc % 8 == 0 &&
-                    (!g.aux || g.ldaux % 8 == 0) &&
+                    (!g.aux || g.ldaux % 8 == 0) && (!g.aux2 || g.ldaux2 % 8 == 0) &&
                     (!g.C2 || g.c2_trans || (g.ldc2 % 8 == 0 && ((uintptr_t)g.C2 % 16) == 0));
   const int vec = vec8 ? 8 : (vec4 ? 4 : 0);
   if (g.ws) { flush_tile_t<-1, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); return; }
@@ -508,6 +524,7 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
     case PH_EPI_BIAS_RELU: flush_tile_t<PH_EPI_BIAS_RELU, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
     case PH_EPI_RELU_MASK: flush_tile_t<PH_EPI_RELU_MASK, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
     case PH_EPI_AXPBY: flush_tile_t<PH_EPI_AXPBY, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+    case kEpiGateSkip: flush_tile_t<kEpiGateSkip, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
     default: flush_tile_t<PH_EPI_NONE, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
   }
 }
@@ -1351,8 +1368,9 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   PH_REQUIRE(d.math == PH_MATH_BF16 || (d.a_dtype == PH_F32 && d.b_dtype == PH_F32),
              "gemm: fp32 and split-bf16 math need fp32 inputs");
   PH_REQUIRE(d.epi == PH_EPI_NONE || d.epi == PH_EPI_BIAS || d.epi == PH_EPI_BIAS_RELU ||
-                 d.epi == PH_EPI_RELU_MASK || d.epi == PH_EPI_AXPBY,
+                 d.epi == PH_EPI_RELU_MASK || d.epi == PH_EPI_AXPBY || d.epi == kEpiGateSkip,
              "gemm: unknown epilogue %d", d.epi);
+  PH_REQUIRE(d.epi != kEpiGateSkip || (d.aux && d.aux2), "gemm: gate-skip operands missing");
   PH_REQUIRE(!(d.epi == PH_EPI_BIAS || d.epi == PH_EPI_BIAS_RELU) || d.bias, "gemm: bias missing");
   PH_REQUIRE(d.epi != PH_EPI_RELU_MASK || d.aux, "gemm: mask tensor missing");
 
@@ -1376,6 +1394,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   g.A = d.A; g.lda = d.lda; g.B = d.B; g.ldb = d.ldb;
   g.C = d.C; g.ldc = d.ldc; g.c_bf16 = d.c_dtype == PH_BF16;
   g.epi = d.epi; g.bias = d.bias; g.aux = d.aux; g.ldaux = d.ldaux ? d.ldaux : d.ldc;
+  g.aux2 = d.epi == kEpiGateSkip ? d.aux2 : nullptr; g.ldaux2 = d.ldaux2;
   g.alpha = d.alpha; g.beta = d.beta;
   g.C2 = (uint16_t*)d.C2; g.ldc2 = d.ldc2; g.c2_trans = d.c2_trans;
   g.remap = 1;
@@ -1458,6 +1477,7 @@ extern "C" int ph_gemm(int trans_a, int trans_b, int M, int N, int K, int a_dtyp
                        long ldc, int math, int epilogue, const float* bias, const void* aux,
                        long ldaux, float alpha, float beta, void* C2, long ldc2, int c2_trans,
                        int splits, void* stream) {
+  PH_REQUIRE(epilogue >= PH_EPI_NONE && epilogue <= PH_EPI_AXPBY, "gemm: unknown epilogue %d", epilogue);
   PhGemmDesc d{};
   d.trans_a = trans_a; d.trans_b = trans_b; d.M = M; d.N = N; d.K = K;
   d.a_dtype = a_dtype; d.A = A; d.lda = lda; d.b_dtype = b_dtype; d.B = B; d.ldb = ldb;

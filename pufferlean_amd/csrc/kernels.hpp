@@ -49,6 +49,11 @@ int join_lanes(hipStream_t main, int n);  // main waits for everything queued on
 // slot, whose pointer never changes).
 int ensure_zeroed_words(unsigned* words, int n, hipStream_t st);
 
+// Library-internal epilogue (not part of the public PH_EPI_* set): the MinGRU input-gradient skip term,
+// C = acc + aux[row,col] * (1 - sigm(aux2[row,col])), with aux the gradient w.r.t. the layer output and
+// aux2 the proj pre-activations (both of C's dtype).
+constexpr int kEpiGateSkip = 0x100;
+
 struct PhGemmDesc {
   int trans_a, trans_b, M, N, K;
   int a_dtype;
@@ -70,6 +75,8 @@ struct PhGemmDesc {
   int c2_trans;
   int splits;   // <= 0: chosen by shape
   int ws_slot;  // scratch slot of the split-K partials (0: the shared default slot)
+  const void* aux2;  // second epilogue operand (kEpiGateSkip)
+  long ldaux2;
 };
 int gemm(const PhGemmDesc& d, hipStream_t st);
 

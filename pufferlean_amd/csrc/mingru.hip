@@ -21,9 +21,8 @@ namespace {
 constexpr int HP = 32;  // padded head rows
 constexpr unsigned kB = 256;
 
-// Logistic function on the hardware exp2 / reciprocal instructions (a few ulp; the scans are
-// VALU-bound with IEEE exp and division). exp(-x) overflowing to +inf gives exactly 0.
-__device__ __forceinline__ float sigm(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// sigm (common.hpp) uses the hardware exp2 / reciprocal instructions: the scans are VALU-bound with
+// IEEE exp and division.
 __device__ __forceinline__ float gact(float x) { return x >= 0.f ? x + 0.5f : sigm(x); }
 __device__ __forceinline__ float ld(const uint16_t* p) { return bf16_to_f32(*p); }
 __device__ __forceinline__ float ld(const float* p) { return *p; }
@@ -117,14 +116,15 @@ __global__ void __launch_bounds__(256) k_scan_fwd(const TS* __restrict__ cmb, co
 }
 
 // Backward scan of one layer (adjoint of k_scan_fwd), t descending. dhn: gradient w.r.t. this
-// layer's output; writes dy = d(hid,gate,proj) pre-activation gradients and dhx = dhn*(1-hg) (the
-// direct part of the gradient w.r.t. the layer input; the GEMM dy.W adds the rest). o_{t-1} is
-// loaded once and carried as o_t of the next (earlier) step.
+// layer's output; writes dy = d(hid,gate,proj) pre-activation gradients. The direct part of the
+// gradient w.r.t. the layer input, dhn*(1-hg), is not written: the data-gradient GEMM dy.W adds it in
+// its epilogue from dhn and the proj pre-activations. o_{t-1} is loaded once and carried as o_t of
+// the next (earlier) step.
 template <typename TS>
 __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, const TS* __restrict__ oS,
                                                   const TS* __restrict__ hin, const TS* __restrict__ dhn,
-                                                  TS* __restrict__ dy, TS* __restrict__ dhx,
-                                                  const float* __restrict__ done, int B, int H, int T) {
+                                                  TS* __restrict__ dy, const float* __restrict__ done, int B,
+                                                  int H, int T) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int HV = H / 4;
   if (idx >= (long)B * HV || T <= 0) return;
@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
       const int t = t0 - c;
       if (t < 0) break;
       const bool keep_prev = rkeep[c] != 0.f;
-      float vdhx[4], vdg[4], vdz[4], vdp[4];
+      float vdg[4], vdz[4], vdp[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const float hid = el(rh[c], q), gate = el(rg[c], q), proj = el(rp[c], q);
@@ -164,7 +164,6 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
         const float g = hid >= 0.f ? hid + 0.5f : sh;
         const float dhg = dh * (o - hi);
         const float dox = dh * hg + dOn[q];
-        vdhx[q] = dh * (1.f - hg);
         const float dz = dox * (g - prev);
         const float dprev = dox * (1.f - z);
         const float dg = dox * z;
@@ -176,7 +175,6 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
       }
       const long so = (long)t * BH + xo;
       const long yw = (long)t * B3H + yo;
-      st4(dhx + so, vdhx);
       st4(dy + yw, vdg);
       st4(dy + yw + H, vdz);
       st4(dy + yw + 2 * H, vdp);
@@ -419,22 +417,23 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   }
   // layers backward
   TS* dhn = (TS*)b.dh0;
-  TS* dhx = (TS*)b.dh1;
+  TS* dnext = (TS*)b.dh1;  // gradient w.r.t. the layer input, produced by the data-gradient GEMM
   for (int l = L - 1; l >= 0; l--) {
     TS* xl = x + (long)l * TB * H;
     TS* cmb = cmbs + (long)l * TB * 3 * H;
     k_scan_bwd<TS><<<ceil_div((long)d.B * H / 4, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn,
-                                                                 dy, dhx, done, d.B, H, d.T);
+                                                                 dy, done, d.B, H, d.T);
     PH_LAUNCH_CHECK();
     // gW_l = dy^T x_l  -> G
     PhGemmDesc g = gd(1, 0, 3 * H, H, (int)TB, DT, dy, 3 * H, DT, xl, H, PH_F32,
                       G + offW + (long)l * szL, H, MATH);
     PH_TRY(gemm(g, st));
-    // dh_in = dhx + dy W_l   (W_l^T stored [H][3H])
-    PhGemmDesc g2 = gd(0, 1, (int)TB, H, 3 * H, DT, dy, 3 * H, DT, wlt + l * szL, 3 * H, DT, dhx, H, MATH);
-    g2.epi = PH_EPI_AXPBY; g2.alpha = 1.f; g2.beta = 1.f; g2.aux = dhx; g2.ldaux = H;
+    // dh_in = dy W_l + dhn (1 - sigm(proj))   (W_l^T stored [H][3H]; proj = third block of cmb)
+    PhGemmDesc g2 =
+        gd(0, 1, (int)TB, H, 3 * H, DT, dy, 3 * H, DT, wlt + l * szL, 3 * H, DT, dnext, H, MATH);
+    g2.epi = kEpiGateSkip; g2.aux = dhn; g2.ldaux = H; g2.aux2 = cmb + 2 * H; g2.ldaux2 = 3 * H;
     PH_TRY(gemm(g2, st));
-    TS* t = dhn; dhn = dhx; dhx = t;
+    TS* t = dhn; dhn = dnext; dnext = t;
   }
   // encoder backward: gbEnc = colsum(dh), gWEnc = dh^T obs
   if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
