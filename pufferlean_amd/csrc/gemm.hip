@@ -1296,15 +1296,15 @@ __global__ void k_splitk_reduce(GemmArgs g, int splits) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long MN = (long)g.M * g.N;
   if (idx >= MN) return;
-  // eight splits' loads in flight at a time, added in split order
+  // sixteen splits' loads in flight at a time, added in split order
   float s = 0.f;
   int z = 0;
-  for (; z + 8 <= splits; z += 8) {
-    float v[8];
+  for (; z + 16 <= splits; z += 16) {
+    float v[16];
 #pragma unroll
-    for (int q = 0; q < 8; q++) v[q] = g.ws[(long)(z + q) * MN + idx];
+    for (int q = 0; q < 16; q++) v[q] = g.ws[(long)(z + q) * MN + idx];
 #pragma unroll
-    for (int q = 0; q < 8; q++) s += v[q];
+    for (int q = 0; q < 16; q++) s += v[q];
   }
   for (; z < splits; z++) s += g.ws[(long)z * MN + idx];
   epilogue_store<TC>(g, (int)(idx / g.N), (int)(idx % g.N), s);

@@ -222,8 +222,20 @@ __global__ void __launch_bounds__(256) k_sq_part_f64(const double* __restrict__ 
   __shared__ double sh[256];
   const long lo = (long)blockIdx.x * chunk;
   const long hi = lo + chunk < n ? lo + chunk : n;
+  // eight loads in flight at a time, added in index order
   double s = 0.0;
-  for (long i = lo + threadIdx.x; i < hi; i += 256) {
+  long i = lo + threadIdx.x;
+  for (; i + 7 * 256 < hi; i += 8 * 256) {
+    double v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = g[i + q * 256];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const double x = v[q] * sc;
+      s += x * x;
+    }
+  }
+  for (; i < hi; i += 256) {
     const double x = g[i] * sc;
     s += x * x;
   }
@@ -237,10 +249,19 @@ __global__ void __launch_bounds__(256) k_sq_part_f64(const double* __restrict__ 
 }
 __global__ void k_clip_scale_f64(double* __restrict__ g, long n, const double* __restrict__ part, int G,
                                  double maxNorm, double sc) {
+  // one thread sums the partials in order, from LDS: their loads are one round trip per 512
+  __shared__ double sp[512];
   __shared__ double cc;
+  double s = 0.0;
+  for (int b0 = 0; b0 < G; b0 += 512) {
+    const int nb = G - b0 < 512 ? G - b0 : 512;
+    __syncthreads();  // the previous slice has been summed
+    for (int q = threadIdx.x; q < nb; q += blockDim.x) sp[q] = part[b0 + q];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int q = 0; q < nb; q++) s += sp[q];
+  }
   if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int q = 0; q < G; q++) s += part[q];
     const double gn = sqrt(s);
     cc = ((maxNorm > 0.0 && gn > maxNorm) ? maxNorm / gn : 1.0) * sc;
   }

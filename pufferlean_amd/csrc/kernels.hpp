@@ -143,6 +143,14 @@ int muon_fast_batch(const MuonMat* mats, int n, float gscale, float lr, float wd
                     const float* coeffs, int nsteps, int math, hipStream_t st);
 int stepvec_f32(float* b, const float* g, float* m, long n, float gscale, float lr, float wd, float mu,
                 hipStream_t st);
+// stepvec over up to kNsMaxMats vectors in one launch (the same update per element).
+struct StepVec {
+  float* b;
+  const float* g;
+  float* m;
+  long n;
+};
+int stepvec_f32_batch(const StepVec* v, int n, float gscale, float lr, float wd, float mu, hipStream_t st);
 int gclip_f32(float* g, long n, float sc, float maxNorm, hipStream_t st);
 
 int moments_normalize(int dtype, const void* x, size_t n, void* y, void* stats, hipStream_t st);

@@ -71,13 +71,27 @@ static __global__ void __launch_bounds__(256) k_fold_losses(const double* __rest
                                                      float entCoef, double* __restrict__ losses) {
   __shared__ double sh[6][4];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // each sum runs over blocks t, t + 256, ... in order; four blocks' loads are in flight at a time
+  double acc[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  const int bd = blockDim.x;
+  int b = threadIdx.x;
+  for (; b + 3 * bd < G; b += 4 * bd) {
+    double pv[4][6];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int q = 0; q < 6; q++) pv[k][q] = part[(size_t)(b + k * bd) * 6 + q];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int q = 0; q < 6; q++) acc[q] += pv[k][q];
+  }
+  for (; b < G; b += bd)
+#pragma unroll
+    for (int q = 0; q < 6; q++) acc[q] += part[(size_t)b * 6 + q];
   double v[6];
 #pragma unroll
-  for (int q = 0; q < 6; q++) {
-    double acc = 0.0;
-    for (int b = threadIdx.x; b < G; b += blockDim.x) acc += part[(size_t)b * 6 + q];
-    v[q] = wave_sum(acc);
-  }
+  for (int q = 0; q < 6; q++) v[q] = wave_sum(acc[q]);
   if (lane == 0)
 #pragma unroll
     for (int q = 0; q < 6; q++) sh[q][w] = v[q];

@@ -494,12 +494,9 @@ int mingru_muon(const ph_mingru_dims& d, const ph_muon_coefs& m, float* params, 
   for (int l = 0; l < L; l++) mat(offW + l * szL, 3 * H, H);
   mat(offDec, A, H);
   mat(offVal, 1, H);
-  auto vec = [&](long off, long n) {
-    return stepvec_f32(params + off, G + off, mom + off, n, 1.f, m.lr, m.wd, m.mu, st);
-  };
-  PH_TRY(vec(offBEnc, H));
-  PH_TRY(vec(offBDec, A));
-  PH_TRY(vec(offBVal, 1));
+  auto vec = [&](long off, long n) { return StepVec{params + off, G + off, mom + off, n}; };
+  const StepVec vecs[3] = {vec(offBEnc, H), vec(offBDec, A), vec(offBVal, 1)};
+  PH_TRY(stepvec_f32_batch(vecs, 3, 1.f, m.lr, m.wd, m.mu, st));
   return muon_fast_batch(mats, nm, 1.f, m.lr, m.wd, m.mu, m.eps, m.coeffs, m.nsteps, m.math, st);
 }
 

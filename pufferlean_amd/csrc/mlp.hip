@@ -144,12 +144,14 @@ int check_dims(const ph_mlp_dims& d, const char* who) {
 int muon_all(const MlpGeo& g, const ph_muon_coefs& m, float* params, float* mom, float* G, hipStream_t st) {
   PH_TRY(gclip_f32(G, g.P, m.gscale, m.max_grad_norm, st));
   MuonMat mats[kMlpMaxLayers + 1];
+  StepVec vecs[kMlpMaxLayers + 1];
   for (int l = 0; l <= g.L; l++) {
     const int rows = l == g.L ? g.O : g.H, cols = l == 0 ? g.D : g.H;
     mats[l] = MuonMat{params + g.oW[l], G + g.oW[l], mom + g.oW[l], rows, cols};
     const long nb = l == g.L ? g.O : g.H;
-    PH_TRY(stepvec_f32(params + g.ob[l], G + g.ob[l], mom + g.ob[l], nb, 1.f, m.lr, m.wd, m.mu, st));
+    vecs[l] = StepVec{params + g.ob[l], G + g.ob[l], mom + g.ob[l], nb};
   }
+  PH_TRY(stepvec_f32_batch(vecs, g.L + 1, 1.f, m.lr, m.wd, m.mu, st));
   return muon_fast_batch(mats, g.L + 1, 1.f, m.lr, m.wd, m.mu, m.eps, m.coeffs, m.nsteps, m.math, st);
 }
 

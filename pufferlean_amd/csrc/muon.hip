@@ -112,8 +112,17 @@ __global__ void __launch_bounds__(256) k_sumsq_part(const float* __restrict__ x,
                                                     float* __restrict__ part) {
   __shared__ float sh[256];
   const long lo = (long)blockIdx.x * chunk, hi = lo + chunk < n ? lo + chunk : n;
+  // eight loads in flight at a time, added in index order
   float s = 0.f;
-  for (long i = lo + threadIdx.x; i < hi; i += 256) s += x[i] * x[i];
+  long i = lo + threadIdx.x;
+  for (; i + 7 * 256 < hi; i += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = x[i + q * 256];
+#pragma unroll
+    for (int q = 0; q < 8; q++) s += v[q] * v[q];
+  }
+  for (; i < hi; i += 256) s += x[i] * x[i];
   sh[threadIdx.x] = s;
   __syncthreads();
   for (int st = 128; st > 0; st >>= 1) {
@@ -201,15 +210,68 @@ __global__ void k_stepvec_f32(float* __restrict__ b, const float* __restrict__ g
   m[i] = newm;
 }
 
+// The same elementwise updates over up to kNsMaxMats arrays in one launch: the arrays are laid end to
+// end in one index space (start[k] is the first index of array k), so the many small launches of an
+// optimizer step become one. Each element gets exactly the single-array kernel's arithmetic.
+struct EwBatch {
+  int n;
+  long start[kNsMaxMats + 1];
+  float* p[kNsMaxMats];        // nesterov: G; finalize: W; stepvec: b
+  float* q[kNsMaxMats];        // nesterov: M; stepvec: g
+  float* r[kNsMaxMats];        // nesterov: U; finalize: X; stepvec: m
+  float s[kNsMaxMats];         // finalize: the array's update scale
+};
+__device__ __forceinline__ int ew_array(const EwBatch& B, long i) {
+  int k = 0;
+  while (k + 1 < B.n && i >= B.start[k + 1]) k++;
+  return k;
+}
+__global__ void k_nesterov_batch(EwBatch B, float gscale, float mu) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B.start[B.n]) return;
+  const int k = ew_array(B, i);
+  const long j = i - B.start[k];
+  const float gi = B.p[k][j] * gscale;
+  const float m = mu * B.q[k][j] + gi;
+  B.q[k][j] = m;
+  B.r[k][j] = gi + mu * m;
+}
+__global__ void k_finalize_batch(EwBatch B, float c1) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B.start[B.n]) return;
+  const int k = ew_array(B, i);
+  const long j = i - B.start[k];
+  B.p[k][j] = c1 * B.p[k][j] + B.s[k] * B.r[k][j];
+}
+__global__ void k_stepvec_batch(EwBatch B, float gscale, float lr, float wd, float mu) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B.start[B.n]) return;
+  const int k = ew_array(B, i);
+  const long j = i - B.start[k];
+  const float gi = B.q[k][j] * gscale;
+  const float newm = mu * B.r[k][j] + gi;
+  const float upd = gi + mu * newm;
+  B.p[k][j] = B.p[k][j] * (1.f - lr * wd) + lr * upd;
+  B.r[k][j] = newm;
+}
+
 // Global grad-norm clip over a flat fp32 gradient: sumsq in fixed-chunk partials, then scale.
 __global__ void k_gclip_scale(float* __restrict__ g, long n, const float* __restrict__ part, int G,
                               float sc, float maxNorm) {
+  // the partials are summed by one thread in order; the block first stages them in LDS so their loads
+  // are one round trip instead of G dependent ones
+  __shared__ float sp[1024];
   __shared__ float tot;
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-    for (int i = 0; i < G; i++) s += part[i];
-    tot = s;
+  float s = 0.f;
+  for (int b0 = 0; b0 < G; b0 += 1024) {
+    const int nb = G - b0 < 1024 ? G - b0 : 1024;
+    __syncthreads();  // the previous slice has been summed
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) sp[i] = part[b0 + i];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int i = 0; i < nb; i++) s += sp[i];
   }
+  if (threadIdx.x == 0) tot = s;
   __syncthreads();
   const float gn = sqrtf(tot) * fabsf(sc);
   const float cc = ((maxNorm > 0.f && gn > maxNorm) ? maxNorm / gn : 1.f) * sc;
@@ -564,13 +626,24 @@ int muon_fast_batch(const MuonMat* mats, int n, float gscale, float lr, float wd
   if (!U) return PH_ERR_NOMEM;
   float* X[kNsMaxMats];
   int rows[kNsMaxMats], cols[kNsMaxMats];
+  EwBatch nb{}, fb{};
+  nb.n = fb.n = n;
   for (int i = 0; i < n; i++) {
     const long e = (long)mats[i].rows * mats[i].cols;
     X[i] = U + off[i];
     rows[i] = mats[i].rows;
     cols[i] = mats[i].cols;
-    if (e == 0) continue;
-    k_nesterov_f32<<<ceil_div(e, kB), kB, 0, st>>>(mats[i].G, mats[i].M, X[i], e, gscale, mu);
+    nb.start[i + 1] = fb.start[i + 1] = nb.start[i] + e;
+    nb.p[i] = const_cast<float*>(mats[i].G);
+    nb.q[i] = mats[i].M;
+    nb.r[i] = X[i];
+    fb.p[i] = mats[i].W;
+    fb.r[i] = X[i];
+    fb.s[i] = lr * sqrtf(fmaxf(1.f, (float)rows[i] / (float)cols[i]));
+  }
+  const long total = nb.start[n];
+  if (total > 0) {
+    k_nesterov_batch<<<ceil_div(total, kB), kB, 0, st>>>(nb, gscale, mu);
     PH_LAUNCH_CHECK();
   }
   if (math == PH_MATH_F32 || nsteps == 0) {
@@ -579,13 +652,27 @@ int muon_fast_batch(const MuonMat* mats, int n, float gscale, float lr, float wd
   } else {
     PH_TRY(ns_fused(X, rows, cols, n, coeffs, nsteps, eps, kSlotNs, kSlotNsCtl, st));
   }
-  for (int i = 0; i < n; i++) {
-    const long e = (long)rows[i] * cols[i];
-    if (e == 0) continue;
-    const float scale = sqrtf(fmaxf(1.f, (float)rows[i] / (float)cols[i]));
-    k_finalize_f32<<<ceil_div(e, kB), kB, 0, st>>>(mats[i].W, X[i], e, 1.f - lr * wd, lr * scale);
+  if (total > 0) {
+    k_finalize_batch<<<ceil_div(total, kB), kB, 0, st>>>(fb, 1.f - lr * wd);
     PH_LAUNCH_CHECK();
   }
+  return PH_OK;
+}
+
+int stepvec_f32_batch(const StepVec* v, int n, float gscale, float lr, float wd, float mu, hipStream_t st) {
+  PH_REQUIRE(n >= 0 && n <= kNsMaxMats, "stepvec: at most %d vectors per batch", kNsMaxMats);
+  EwBatch b{};
+  b.n = n;
+  for (int i = 0; i < n; i++) {
+    b.start[i + 1] = b.start[i] + v[i].n;
+    b.p[i] = v[i].b;
+    b.q[i] = const_cast<float*>(v[i].g);
+    b.r[i] = v[i].m;
+  }
+  const long total = n > 0 ? b.start[n] : 0;
+  if (total == 0) return PH_OK;
+  k_stepvec_batch<<<ceil_div(total, kB), kB, 0, st>>>(b, gscale, lr, wd, mu);
+  PH_LAUNCH_CHECK();
   return PH_OK;
 }
 

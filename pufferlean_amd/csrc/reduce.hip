@@ -144,8 +144,18 @@ __global__ void __launch_bounds__(256) k_colsum_finish(const float* __restrict__
   const int lc = threadIdx.x & 15, ln = threadIdx.x >> 4;
   const int c = blockIdx.x * 16 + lc;
   float s = 0.f;
-  if (c < J)
-    for (int g = ln; g < G; g += 16) s += part[(long)g * J + c];
+  if (c < J) {
+    // eight loads in flight at a time, added in partial order
+    int g = ln;
+    for (; g + 7 * 16 < G; g += 8 * 16) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) v[q] = part[(long)(g + 16 * q) * J + c];
+#pragma unroll
+      for (int q = 0; q < 8; q++) s += v[q];
+    }
+    for (; g < G; g += 16) s += part[(long)g * J + c];
+  }
   sh[ln][lc] = s;
   __syncthreads();
   for (int w = 8; w > 0; w >>= 1) {
