@@ -1116,14 +1116,16 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
       mm(Y);
       // issue order: products of X with the reads of Y between them, then (after the barrier) the
       // products of Y with the reads of the next X between them
+      constexpr int NP = SM + SN < SM * SN ? SM + SN : SM * SN;  // MFMA / read pairs
 #pragma unroll
       for (int h = 0; h < 2; h++) {
 #pragma unroll
-        for (int q = 0; q < SM + SN; q++) {
+        for (int q = 0; q < NP; q++) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, SM * SN - (SM + SN), 0);
+        if constexpr (SM + SN > NP) __builtin_amdgcn_sched_group_barrier(0x100, SM + SN - NP, 0);
+        if constexpr (SM * SN > NP) __builtin_amdgcn_sched_group_barrier(0x008, SM * SN - NP, 0);
       }
     }
     rd(Y, st, lk + 8);
@@ -1348,6 +1350,9 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
 void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStream_t st) {
   if (bn == 256) {
     dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
+  } else if (!ta && tb && bn == 64) {
+    if (g.c_bf16) k_gemm_nt_dma<256, 64, uint16_t><<<grid, 256, 0, st>>>(g);
+    else k_gemm_nt_dma<256, 64, float><<<grid, 256, 0, st>>>(g);
   } else if (!ta && tb) {
     if (g.c_bf16) k_gemm_nt_dma<256, 128, uint16_t><<<grid, 256, 0, st>>>(g);
     else k_gemm_nt_dma<256, 128, float><<<grid, 256, 0, st>>>(g);
@@ -1535,7 +1540,8 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
   const bool big_ok = d.math == PH_MATH_BF16 && d.a_dtype == PH_BF16 && d.b_dtype == PH_BF16;
   bool small = false, big = big_ok && tiles256x128 >= 512;
-  int big_bn = 128;
+  // NT outputs at most 64 wide (the policy heads): 256x64 tiles, half the wasted columns of 256x128
+  int big_bn = !d.trans_a && d.trans_b && d.N <= 64 ? 64 : 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
     if (d.K >= 4096) {
       // 256x256 splits when both output extents fill the tile and the reduction is long enough to

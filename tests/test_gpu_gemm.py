@@ -265,3 +265,21 @@ def test_gemm_nt_big_tile_epilogue_paths(gpu):
     c_two = D.gemm(ga, gb, trans_b=True, out2=c2).cpu().numpy()
     assert np.array_equal(c_one, c_two)
     assert rel(c2.float().cpu().numpy(), c_one) < 4e-3
+
+
+@pytest.mark.parametrize("N", [64, 40, 32, 17])
+def test_gemm_nt_narrow_output_big_tiles(gpu, N):
+    """NT outputs at most 64 wide with >= 512 row tiles (the policy heads: 262144 x 32) take the
+    256x64 load-to-LDS kernel: ragged M, a K tail, fp32 and bf16 C, the bias epilogue."""
+    M, K = 131080, 264
+    a, b = operands(M, N, K, 0, 1, 340 + N)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = ar.astype(np.float64) @ br.T.astype(np.float64)
+    ga, gb = _bf(a), _bf(b)
+    c = D.gemm(ga, gb, trans_b=True).cpu().numpy()
+    assert rel(c, ref) < 1e-5
+    bias = torch.from_numpy(rng.normal(341, N).astype(np.float32)).cuda()
+    c = D.gemm(ga, gb, trans_b=True, epilogue=L.PH_EPI_BIAS, bias=bias).cpu().numpy()
+    assert rel(c, ref + bias.cpu().numpy()) < 1e-5
+    cb = D.gemm(ga, gb, trans_b=True, out_dtype=torch.bfloat16)
+    assert rel(cb.float().cpu().numpy(), ref) < 4e-3
