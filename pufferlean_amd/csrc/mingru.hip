@@ -241,19 +241,24 @@ __global__ void k_norm_adv(const float* __restrict__ adv, const float* __restric
 }
 
 // fp32 -> bf16 (RNE), 8 elements per thread (n is a multiple of 8: the observation width is)
-__global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y, long n8) {
+// y = bf16(x) over n elements (x 16-byte aligned): 8 per thread, the last partial group element-wise.
+__global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restrict__ y, long n) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n8) return;
-  const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
-  const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
-  reinterpret_cast<uint4*>(y)[i] =
-      make_uint4(bf16x2_rne(a.x, a.y), bf16x2_rne(a.z, a.w), bf16x2_rne(b.x, b.y), bf16x2_rne(b.z, b.w));
+  if (i * 8 >= n) return;
+  if (i * 8 + 8 <= n) {
+    const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+    const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+    reinterpret_cast<uint4*>(y)[i] =
+        make_uint4(bf16x2_rne(a.x, a.y), bf16x2_rne(a.z, a.w), bf16x2_rne(b.x, b.y), bf16x2_rne(b.z, b.w));
+  } else {
+    for (long e = i * 8; e < n; e++) y[e] = bf16_rne(x[e]);
+  }
 }
 
 // Activation and weight-copy buffers hold bf16 (precision 0) or fp32 (precision 1) elements; they
 // are sized for fp32 so one allocation serves both tiers.
 struct Bufs {
-  void *obsb, *x, *cmb, *o, *dy, *dh0, *dh1;
+  void *obsb, *x, *cmb, *o, *dy, *dh0, *dh1, *dlb;
   void *wenc, *wl, *wlt, *wh, *wht;
   float *bh, *logit, *dl, *gh, *gbh, *adv, *advn, *tgt, *newlp, *newval, *stats;
 };
@@ -292,6 +297,7 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
   const size_t o_bh = take(HP * 4);
   const size_t o_logit = take((size_t)TB * HP * 4);
   const size_t o_dl = take((size_t)TB * HP * 4);
+  const size_t o_dlb = take((size_t)TB * HP * 2);
   const size_t o_gh = take((size_t)HP * H * 4);
   const size_t o_gbh = take(HP * 4);
   const size_t o_adv = take((size_t)TB * 4);
@@ -320,7 +326,7 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
     zeroed_a[dev & 15] = d.A;
   }
   b.obsb = base + o_obsb; b.x = base + o_x; b.cmb = base + o_cmb; b.o = base + o_o; b.dy = base + o_dy;
-  b.dh0 = base + o_dh0; b.dh1 = base + o_dh1; b.wenc = base + o_wenc; b.wl = base + o_wl;
+  b.dh0 = base + o_dh0; b.dh1 = base + o_dh1; b.dlb = base + o_dlb; b.wenc = base + o_wenc; b.wl = base + o_wl;
   b.wlt = base + o_wlt; b.wh = base + o_wh; b.wht = base + o_wht;
   b.bh = (float*)(base + o_bh); b.logit = (float*)(base + o_logit); b.dl = (float*)(base + o_dl);
   b.gh = (float*)(base + o_gh); b.gbh = (float*)(base + o_gbh); b.adv = (float*)(base + o_adv);
@@ -370,7 +376,7 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   const void* obsg = obs;
   if (BF) {
     PH_REQUIRE(((uintptr_t)obs % 16) == 0, "mingru: observations must be 16-byte aligned");
-    k_f32_to_bf16_k<<<ceil_div(TB * D / 8, kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D / 8);
+    k_f32_to_bf16_k<<<ceil_div(ceil_div(TB * D, 8), kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D);
     obsg = b.obsb;
   }
   PH_LAUNCH_CHECK();
@@ -405,14 +411,25 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   else
     PH_TRY(ppo_grad(b.logit, HP, b.logit + A, HP, act, advn, ret, oldlp, oldval, TB, A, c.vf_coef,
                     c.ent_coef, c.clip_eps, c.vf_clip, 1, b.dl, HP, b.dl + A, HP, newlp, newval, losses, st));
-  // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh
+  // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh. The bf16 tier's GEMMs round dl to
+  // bf16 on the way in; a bf16 copy made once (the same rounding) lets them read half the bytes and
+  // the data gradient take the load-to-LDS kernel (86 -> 55 us at 262144 rows). The bias gradient
+  // sums fp32 dl.
   {
-    PhGemmDesc g = gd(1, 0, HP, H, (int)TB, PH_F32, b.dl, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
+    const void* dlg = b.dl;
+    int dlt = PH_F32;
+    if (BF) {
+      k_f32_to_bf16_k<<<ceil_div(ceil_div(TB * HP, 8), kB), kB, 0, st>>>(b.dl, (uint16_t*)b.dlb, TB * HP);
+      PH_LAUNCH_CHECK();
+      dlg = b.dlb;
+      dlt = PH_BF16;
+    }
+    PhGemmDesc g = gd(1, 0, HP, H, (int)TB, dlt, dlg, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
     PH_TRY(gemm(g, st));
     PH_TRY(colsum_f32(b.dl, TB, HP, HP, b.gbh, 1.f, 0, st));
     k_head_scatter<<<64, kB, 0, st>>>(b.gh, b.gbh, H, A, G + offDec);
     PH_LAUNCH_CHECK();
-    PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, PH_F32, b.dl, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
+    PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, dlt, dlg, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
     PH_TRY(gemm(g2, st));
   }
   // layers backward
