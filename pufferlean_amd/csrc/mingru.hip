@@ -424,10 +424,16 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
       dlg = b.dlb;
       dlt = PH_BF16;
     }
+    // The head's weight and bias gradients only fill G's head block, which nothing reads before the
+    // join at the end of the backward: they run on library lane 0 (its own split-K slot) beside the
+    // data gradient and the layer backward.
+    PH_TRY(fork_lanes(st, 1));
+    const hipStream_t lane = lane_stream(0);
     PhGemmDesc g = gd(1, 0, HP, H, (int)TB, dlt, dlg, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
-    PH_TRY(gemm(g, st));
-    PH_TRY(colsum_f32(b.dl, TB, HP, HP, b.gbh, 1.f, 0, st));
-    k_head_scatter<<<64, kB, 0, st>>>(b.gh, b.gbh, H, A, G + offDec);
+    g.ws_slot = lane_slots(0).gemm_ws;
+    PH_TRY(gemm(g, lane));
+    PH_TRY(colsum_f32(b.dl, TB, HP, HP, b.gbh, 1.f, 0, lane));
+    k_head_scatter<<<64, kB, 0, lane>>>(b.gh, b.gbh, H, A, G + offDec);
     PH_LAUNCH_CHECK();
     PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, dlt, dlg, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
     PH_TRY(gemm(g2, st));
@@ -452,14 +458,17 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     PH_TRY(gemm(g2, st));
     TS* t = dhn; dhn = dnext; dnext = t;
   }
-  // encoder backward: gbEnc = colsum(dh), gWEnc = dh^T obs
-  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
-  else PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, st));
+  // encoder backward: gbEnc = colsum(dh) on lane 0 (after the head's work queued there) beside
+  // gWEnc = dh^T obs on the main stream; then the main stream waits for the lane
+  PH_TRY(fork_lanes(st, 1));
+  const hipStream_t lane = lane_stream(0);
+  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
+  else PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
   {
     PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, D, PH_F32, G, D, MATH);
     PH_TRY(gemm(g, st));
   }
-  return PH_OK;
+  return join_lanes(st, 1);
 }
 
 }  // namespace
