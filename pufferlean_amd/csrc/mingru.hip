@@ -353,7 +353,7 @@ template <typename TS>
 int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const HeadSizes* heads, const float* params,
                       const float* obs, const int* act, const float* advn, const float* ret,
                       const float* oldlp, const float* oldval, const float* done, float* G,
-                      float* newlp, float* newval, double* losses, hipStream_t st) {
+                      float* newlp, float* newval, double* losses, hipStream_t st, bool join_lane0) {
   constexpr bool BF = sizeof(TS) == 2;
   constexpr int DT = BF ? PH_BF16 : PH_F32;
   constexpr int MATH = BF ? PH_MATH_BF16 : PH_MATH_F32;
@@ -404,7 +404,9 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     g.epi = PH_EPI_BIAS; g.bias = b.bh;
     PH_TRY(gemm(g, st));
   }
-  // fused PPO loss: dlogits into dl[:, :A], dvalue into dl[:, A]
+  // fused PPO loss: dlogits into dl[:, :A], dvalue into dl[:, A]; its advantages and returns may come
+  // from work the caller queued on lane 0
+  if (join_lane0) PH_TRY(join_lanes(st, 1));
   if (heads)
     PH_TRY(ppo_grad_md(b.logit, HP, act, advn, ret, oldlp, oldval, TB, heads->n, heads->K, c.vf_coef, c.ent_coef,
                        c.clip_eps, c.vf_clip, b.dl, HP, newlp, newval, losses, st));
@@ -480,7 +482,7 @@ long mingru_param_count(const ph_mingru_dims& d) {
 int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const HeadSizes* heads, const float* params,
                     const float* obs, const int* act, const float* advn, const float* ret,
                     const float* oldlp, const float* oldval, const float* done, float* G,
-                    float* newlp, float* newval, double* losses, hipStream_t st) {
+                    float* newlp, float* newval, double* losses, hipStream_t st, bool join_lane0) {
   PH_REQUIRE(d.B > 0 && d.T > 0 && d.D > 0 && d.H > 0 && d.L > 0 && d.A > 0, "mingru: empty dims");
   PH_REQUIRE(d.A + 1 <= HP, "mingru: at most %d actions", HP - 1);
   PH_REQUIRE(d.H % 8 == 0 && d.D % 8 == 0, "mingru: hidden and obs sizes must be multiples of 8");
@@ -495,9 +497,9 @@ int mingru_ppo_grad(const ph_mingru_dims& d, const ph_ppo_coefs& c, const HeadSi
   }
   if (d.precision == 1)
     return mingru_ppo_grad_t<float>(d, c, heads, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
-                                    newval, losses, st);
+                                    newval, losses, st, join_lane0);
   return mingru_ppo_grad_t<uint16_t>(d, c, heads, params, obs, act, advn, ret, oldlp, oldval, done, G, newlp,
-                                     newval, losses, st);
+                                     newval, losses, st, join_lane0);
 }
 
 // Clip the summed gradient and apply Muon to every matrix (fp32 master weights), stepvec to biases.
@@ -533,13 +535,16 @@ int mingru_step(const ph_mingru_dims& d, const ph_ppo_coefs& c, const ph_muon_co
   const long TB = (long)d.T * d.B;
   Bufs b;
   PH_TRY(get_bufs(d, b, st));
-  // V-trace (bootstrapped variant, time-major) on the behaviour values; targets = adv + V
+  // V-trace (bootstrapped variant, time-major) on the behaviour values, targets = adv + V, and the
+  // minibatch advantage normalisation: on lane 0 beside the forward pass, which does not need them
+  // (the gradient joins the lane before its loss)
+  PH_TRY(fork_lanes(st, 1));
+  const hipStream_t lane = lane_stream(0);
   PH_TRY(vtrace_f32(rew, oldval, done, logrho, boot, d.B, d.T, 1, 1, logrho != nullptr, 1, c.gamma,
-                    c.lam, c.rho_clip, c.c_clip, b.adv, b.tgt, st));
-  // minibatch advantage normalisation
-  PH_TRY(moments_normalize(PH_F32, b.adv, TB, b.advn, b.stats, st));
+                    c.lam, c.rho_clip, c.c_clip, b.adv, b.tgt, lane));
+  PH_TRY(moments_normalize(PH_F32, b.adv, TB, b.advn, b.stats, lane));
   PH_TRY(mingru_ppo_grad(d, c, nullptr, params, obs, act, b.advn, b.tgt, oldlp, oldval, done, G, b.newlp,
-                         b.newval, losses, st));
+                         b.newval, losses, st, true));
   PH_TRY(mingru_muon(d, m, params, mom, G, st));
   return PH_OK;
 }
@@ -556,7 +561,7 @@ extern "C" int ph_mingru_ppo_grad(const ph_mingru_dims* d, const ph_ppo_coefs* c
                                   float* newlp, float* newval, double* losses, void* stream) {
   PH_REQUIRE(d && c, "ph_mingru_ppo_grad: null config");
   return mingru_ppo_grad(*d, *c, nullptr, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval,
-                         losses, as_stream(stream));
+                         losses, as_stream(stream), false);
 }
 
 extern "C" int ph_mingru_ppo_grad_md(const ph_mingru_dims* d, const ph_ppo_coefs* c, const int* head_sizes,
@@ -573,7 +578,7 @@ extern "C" int ph_mingru_ppo_grad_md(const ph_mingru_dims* d, const ph_ppo_coefs
     hs.n[h] = head_sizes[h];
   }
   return mingru_ppo_grad(*d, *c, &hs, params, obs, act, adv, ret, oldlp, oldval, done, G, newlp, newval, losses,
-                         as_stream(stream));
+                         as_stream(stream), false);
 }
 
 extern "C" int ph_mingru_muon(const ph_mingru_dims* d, const ph_muon_coefs* m, float* params,
