@@ -458,11 +458,18 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
       constexpr int CPR8 = BN / 8, NCH8 = BM * CPR8 / NT, G = NCH8 < 4 ? NCH8 : 4;
       static_assert(NCH8 % G == 0, "chunk groups");
       // The pass's aux operands first: one 16-byte load per chunk and operand, all in flight together
-      // (one load latency per pass instead of one per group).
+      // (one load latency per pass instead of one per group). They become their epilogue terms
+      // before the first store: one counter covers both loads and stores here, so a wait for a load
+      // issued before a store would also wait for that store, a store round trip before every chunk
+      // (measured: the 262144x512x1536 GEMM with an aux operand 549 -> 544 us, 508 without one).
       constexpr bool kX = EPI == PH_EPI_RELU_MASK || EPI == PH_EPI_AXPBY || EPI == kEpiGateSkip;
       constexpr bool kY = EPI == kEpiGateSkip;
-      uint4 xa[kX ? NCH8 : 1], xb[kY ? NCH8 : 1];
+      constexpr bool kAdd = EPI == PH_EPI_AXPBY || EPI == kEpiGateSkip;
+      constexpr bool kMask = EPI == PH_EPI_RELU_MASK;
+      float4 ad[kAdd ? NCH8 : 1][2];  // AXPBY: beta * aux; gate skip: aux * (1 - sigm(aux2))
+      uint32_t mk[kMask ? NCH8 : 1];  // RELU_MASK: bit e set where aux > 0
       if constexpr (kX) {
+        uint4 xa[NCH8], xb[kY ? NCH8 : 1];
         const bool has = EPI != PH_EPI_AXPBY || g.aux;
 #pragma unroll
         for (int q = 0; q < NCH8; q++) {
@@ -474,6 +481,35 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
           if constexpr (kY) {
             const uint16_t* pb = reinterpret_cast<const uint16_t*>(g.aux2) + (long)row * g.ldaux2 + col;
             xb[q] = in ? *reinterpret_cast<const uint4*>(pb) : make_uint4(0u, 0u, 0u, 0u);
+          }
+        }
+        // Wait for them here, before any store of the pass (the compiler would otherwise sink the
+        // terms, and its waits, to the chunks' stores): s_waitcnt vmcnt(0), other counters unchanged.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+#pragma unroll
+        for (int q = 0; q < NCH8; q++) {
+          const float4 x[2] = {cvt4(EpiRaw4<uint16_t>{make_uint2(xa[q].x, xa[q].y)}),
+                               cvt4(EpiRaw4<uint16_t>{make_uint2(xa[q].z, xa[q].w)})};
+          if constexpr (kMask) {
+            uint32_t m = 0u;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+              m |= (x[h].x > 0.f ? 1u : 0u) << (4 * h) | (x[h].y > 0.f ? 2u : 0u) << (4 * h) |
+                   (x[h].z > 0.f ? 4u : 0u) << (4 * h) | (x[h].w > 0.f ? 8u : 0u) << (4 * h);
+            mk[q] = m;
+          }
+          if constexpr (EPI == PH_EPI_AXPBY) {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+              ad[q][h] = make_float4(g.beta * x[h].x, g.beta * x[h].y, g.beta * x[h].z, g.beta * x[h].w);
+          }
+          if constexpr (kY) {
+            const float4 pp[2] = {cvt4(EpiRaw4<uint16_t>{make_uint2(xb[q].x, xb[q].y)}),
+                                  cvt4(EpiRaw4<uint16_t>{make_uint2(xb[q].z, xb[q].w)})};
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+              ad[q][h] = make_float4(x[h].x * (1.f - sigm(pp[h].x)), x[h].y * (1.f - sigm(pp[h].y)),
+                                     x[h].z * (1.f - sigm(pp[h].z)), x[h].w * (1.f - sigm(pp[h].w)));
           }
         }
       }
@@ -507,14 +543,6 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
               op[q][1] = epi_load4<EPI, TC>(g, row, col + 4);
             }
           }
-          if constexpr (kX) {
-            op[q][0].x.v = make_uint2(xa[q0 + q].x, xa[q0 + q].y);
-            op[q][1].x.v = make_uint2(xa[q0 + q].z, xa[q0 + q].w);
-          }
-          if constexpr (kY) {
-            op[q][0].y.v = make_uint2(xb[q0 + q].x, xb[q0 + q].y);
-            op[q][1].y.v = make_uint2(xb[q0 + q].z, xb[q0 + q].w);
-          }
           const float* src = &sC[lr * LDC + lc];
           v[q][0] = *reinterpret_cast<const float4*>(src);
           v[q][1] = *reinterpret_cast<const float4*>(src + 4);
@@ -525,8 +553,22 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
           const int lr = c / CPR8, lc = (c % CPR8) * 8;
           const int row = grow(lr), col = n0 + lc;
           if (row >= g.M || col >= g.N) continue;
-          const float4 a = epi_apply4<EPI, TC>(g, v[q][0], op[q][0]);
-          const float4 b = epi_apply4<EPI, TC>(g, v[q][1], op[q][1]);
+          float4 a, b;
+          if constexpr (kAdd) {
+            // AXPBY: alpha * acc + beta * aux; gate skip: acc + its term
+            const float al = EPI == PH_EPI_AXPBY ? g.alpha : 1.f;
+            const float4 u = v[q][0], w = v[q][1], t0 = ad[q0 + q][0], t1 = ad[q0 + q][1];
+            a = make_float4(al * u.x + t0.x, al * u.y + t0.y, al * u.z + t0.z, al * u.w + t0.w);
+            b = make_float4(al * w.x + t1.x, al * w.y + t1.y, al * w.z + t1.z, al * w.w + t1.w);
+          } else if constexpr (kMask) {
+            const uint32_t m = mk[q0 + q];
+            const float4 u = v[q][0], w = v[q][1];
+            a = make_float4(m & 1u ? u.x : 0.f, m & 2u ? u.y : 0.f, m & 4u ? u.z : 0.f, m & 8u ? u.w : 0.f);
+            b = make_float4(m & 16u ? w.x : 0.f, m & 32u ? w.y : 0.f, m & 64u ? w.z : 0.f, m & 128u ? w.w : 0.f);
+          } else {
+            a = epi_apply4<EPI, TC>(g, v[q][0], op[q][0]);
+            b = epi_apply4<EPI, TC>(g, v[q][1], op[q][1]);
+          }
           store8(reinterpret_cast<uint16_t*>(g.C) + (long)row * g.ldc + col, a, b);
           if (g.C2 && !g.c2_trans) store8(g.C2 + (long)row * g.ldc2 + col, a, b);
           if (g.C2 && g.c2_trans) {
