@@ -660,7 +660,7 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
 
 // Chunk width of the flush: 8 (bf16 C, 8-column chunks), 4 (4-column chunks) or 0 (element stores).
 template <typename TC>
-__device__ __forceinline__ int flush_vec(const GemmArgs& g) {
+__host__ __device__ __forceinline__ int flush_vec(const GemmArgs& g) {
   // vector path: every 4-column chunk is whole and 16-byte (fp32) / 8-byte (bf16) aligned
   const bool vec4 = (g.N % 4 == 0) && (g.ws ? true : (g.ldc % 4 == 0 && ((uintptr_t)g.C % 16) == 0)) &&
                     (!g.aux || (g.ldaux % 4 == 0 && ((uintptr_t)g.aux % 16) == 0)) &&
@@ -690,6 +690,81 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
     case PH_EPI_AXPBY: flush_tile_t<PH_EPI_AXPBY, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
     case kEpiGateSkip: flush_tile_t<kEpiGateSkip, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
     default: flush_tile_t<PH_EPI_NONE, TC, BM, BN, NT, LDC, WAVE>(g, sC, m0, mhi, n0, vec, tid); break;
+  }
+}
+
+// bf16 C with no aux operand (EPI NONE / BIAS / BIAS_RELU, no second output, no split-K partials, the
+// 8-column path): the accumulators are rounded to bf16 in registers (bias and ReLU applied first, the
+// same arithmetic as the fp32-staged flush) and the whole BM x BN tile is staged once, as bf16: half
+// the LDS bytes of the fp32 staging passes, which share the LDS with the other block's k loop.
+// Adjacent lanes hold adjacent columns: for each pair of rows they swap one value (DPP), so each lane
+// writes two columns of one row as one 4-byte store. Rows are 2 BN bytes with no padding; the 16-byte
+// chunks of odd rows are XOR-swizzled by 4 so the two rows a half-wavefront writes use different banks.
+__host__ __device__ __forceinline__ bool stage_bf16_ok(const GemmArgs& g, int vec) {
+  return g.c_bf16 && !g.ws && !g.C2 && vec == 8 &&
+         (g.epi == PH_EPI_NONE || g.epi == PH_EPI_BIAS || g.epi == PH_EPI_BIAS_RELU);
+}
+__device__ __forceinline__ int sbf_word(int row, int col, int BN) {
+  const int ch = (col >> 3) ^ ((row & 1) << 2);
+  return row * (BN / 2) + ch * 4 + ((col & 7) >> 1);
+}
+template <int EPI, int BN, int SM, int SN>
+__device__ __forceinline__ void stage_bf16(const GemmArgs& g, uint32_t* sT, const floatx16 (&acc)[SM][SN],
+                                           int wm0, int wn0, int n0, int lane) {
+  const bool odd = lane & 1;
+  const int hrow = (lane >> 5) * 4;
+#pragma unroll
+  for (int j = 0; j < SN; j++) {
+    const int c = wn0 + j * 32 + (lane & 31);
+    float bj = 0.f;
+    if constexpr (EPI != PH_EPI_NONE) bj = n0 + c < g.N ? g.bias[n0 + c] : 0.f;
+    const int ce = c & ~1;
+#pragma unroll
+    for (int i = 0; i < SM; i++)
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int r0 = 2 * k, r1 = r0 + 1;
+        float v0 = acc[i][j][r0], v1 = acc[i][j][r1];
+        if constexpr (EPI != PH_EPI_NONE) {
+          v0 += bj;
+          v1 += bj;
+        }
+        if constexpr (EPI == PH_EPI_BIAS_RELU) {
+          v0 = fmaxf(v0, 0.f);
+          v1 = fmaxf(v1, 0.f);
+        }
+        // even lane: (own r0, odd neighbour's r0) at row r0; odd lane: (even neighbour's r1, own r1) at row r1
+        const float x = odd ? v0 : v1;
+        const int xi = __builtin_bit_cast(int, x);
+        // the value of lane ^ 1 (DPP quad permutation 1, 0, 3, 2)
+        const float y = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(xi, 0xB1, 0xF, 0xF, false));
+        const uint32_t w = odd ? pack_bf16x2(y, v1) : pack_bf16x2(v0, y);
+        const int row = wm0 + i * 32 + 8 * (r0 >> 2) + hrow + (r0 & 3) + (odd ? 1 : 0);
+        sT[sbf_word(row, ce, BN)] = w;
+      }
+  }
+}
+// Writes the staged bf16 tile: one 16-byte LDS read and one 16-byte nontemporal store per chunk.
+template <int BM, int BN, int NT>
+__device__ __forceinline__ void flush_bf16(const GemmArgs& g, const uint32_t* sT, int m0, int n0, int tid) {
+  constexpr int CPR = BN / 8, NCH = BM * CPR / NT, G = 8;
+  static_assert(NCH * NT == BM * CPR && NCH % G == 0, "bf16 flush chunks");
+#pragma unroll
+  for (int q0 = 0; q0 < NCH; q0 += G) {
+    u32x4_t v[G];
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+      const int c = tid + (q0 + q) * NT, row = c / CPR, ch = c % CPR;
+      v[q] = *reinterpret_cast<const u32x4_t*>(&sT[sbf_word(row, ch * 8, BN)]);
+    }
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+      const int c = tid + (q0 + q) * NT, row = m0 + c / CPR, col = n0 + (c % CPR) * 8;
+      if (row < g.M && col < g.N) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(g.C) + (long)row * g.ldc + col;
+        __builtin_nontemporal_store(v[q], reinterpret_cast<u32x4_t*>(dst));
+      }
+    }
   }
 }
 
@@ -1029,7 +1104,9 @@ __device__ __forceinline__ void copy_to_lds(gptr<uint16_t> src, const uint16_t* 
 #pragma clang diagnostic pop
 }
 
-template <int BM, int BN, typename TC>
+// S16: the launch takes the bf16-staged epilogue (stage_bf16_ok, decided on the host), so each
+// instantiation carries one epilogue and its registers.
+template <int BM, int BN, typename TC, bool S16 = false>
 __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
   constexpr int BK = 32, NT = 256, NSTG = 3;
   using Lay = LdsLayout<BK>;
@@ -1176,7 +1253,15 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
     wait_vm<0>();  // the copies issued past the end land before the LDS is reused
   }
   barrier_mem();
-  if constexpr (EPR == BM) {
+  if constexpr (S16) {
+    static_assert(sizeof(TC) == 2 && BM * BN * 2 <= (PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES), "bf16 staging");
+    uint32_t* sT = reinterpret_cast<uint32_t*>(smem);
+    if (g.epi == PH_EPI_NONE) stage_bf16<PH_EPI_NONE, BN>(g, sT, acc, wm0, wn0, n0, lane);
+    else if (g.epi == PH_EPI_BIAS) stage_bf16<PH_EPI_BIAS, BN>(g, sT, acc, wm0, wn0, n0, lane);
+    else stage_bf16<PH_EPI_BIAS_RELU, BN>(g, sT, acc, wm0, wn0, n0, lane);
+    lds_barrier();
+    flush_bf16<BM, BN, NT>(g, sT, m0, n0, tid);
+  } else if constexpr (EPR == BM) {
     stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
     lds_barrier();
     flush_tile<TC, BM, BN, NT, LDC>(g, sC, m0, n0);
@@ -1390,13 +1475,16 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
 // transposed weight copy) copies its tiles through the load-to-LDS path instead (bit-identical, about
 // 5 % faster on the policy shapes).
 void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStream_t st) {
+  const bool s16 = g.c_bf16 && stage_bf16_ok(g, flush_vec<uint16_t>(g));
   if (bn == 256) {
     dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
   } else if (!ta && tb && bn == 64) {
-    if (g.c_bf16) k_gemm_nt_dma<256, 64, uint16_t><<<grid, 256, 0, st>>>(g);
+    if (s16) k_gemm_nt_dma<256, 64, uint16_t, true><<<grid, 256, 0, st>>>(g);
+    else if (g.c_bf16) k_gemm_nt_dma<256, 64, uint16_t><<<grid, 256, 0, st>>>(g);
     else k_gemm_nt_dma<256, 64, float><<<grid, 256, 0, st>>>(g);
   } else if (!ta && tb) {
-    if (g.c_bf16) k_gemm_nt_dma<256, 128, uint16_t><<<grid, 256, 0, st>>>(g);
+    if (s16) k_gemm_nt_dma<256, 128, uint16_t, true><<<grid, 256, 0, st>>>(g);
+    else if (g.c_bf16) k_gemm_nt_dma<256, 128, uint16_t><<<grid, 256, 0, st>>>(g);
     else k_gemm_nt_dma<256, 128, float><<<grid, 256, 0, st>>>(g);
   } else {
     dispatch_bf16_t<256, 128, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);

@@ -283,3 +283,27 @@ def test_gemm_nt_narrow_output_big_tiles(gpu, N):
     assert rel(c, ref + bias.cpu().numpy()) < 1e-5
     cb = D.gemm(ga, gb, trans_b=True, out_dtype=torch.bfloat16)
     assert rel(cb.float().cpu().numpy(), ref) < 4e-3
+
+
+@pytest.mark.parametrize("M,N", [(4136, 4104), (131080, 64)])
+def test_gemm_nt_bf16_staging_matches_fp32_staging(gpu, M, N):
+    """bf16 C with no aux operand (NONE / BIAS / BIAS_RELU) rounds the accumulators in registers and
+    stages the tile once as bf16; a second output forces the fp32 staging passes. Both give the same
+    bits (ragged M and N, a K tail), and both match the f64 product."""
+    K = 264
+    a, b = operands(M, N, K, 0, 1, 350 + N)
+    ar, br = bf16_round(a), bf16_round(b)
+    ref = ar.astype(np.float64) @ br.T.astype(np.float64)
+    ga, gb = _bf(a), _bf(b)
+    bias = torch.from_numpy(rng.normal(351, N).astype(np.float32)).cuda()
+    for epi in (L.PH_EPI_NONE, L.PH_EPI_BIAS, L.PH_EPI_BIAS_RELU):
+        bb = None if epi == L.PH_EPI_NONE else bias
+        c16 = D.gemm(ga, gb, trans_b=True, out_dtype=torch.bfloat16, epilogue=epi, bias=bb)
+        two = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        c32 = D.gemm(ga, gb, trans_b=True, out_dtype=torch.bfloat16, epilogue=epi, bias=bb, out2=two)
+        assert torch.equal(c16, c32), epi
+        assert torch.equal(two, c32), epi
+        r = ref if bb is None else ref + bias.cpu().numpy()
+        if epi == L.PH_EPI_BIAS_RELU:
+            r = np.maximum(r, 0.0)
+        assert rel(c16.float().cpu().numpy(), r) < 4e-3
