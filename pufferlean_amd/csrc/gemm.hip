@@ -699,13 +699,19 @@ __device__ __forceinline__ void flush_tile(const GemmArgs& g, float* sC, int m0,
 // the LDS bytes of the fp32 staging passes, which share the LDS with the other block's k loop.
 // Adjacent lanes hold adjacent columns: for each pair of rows they swap one value (DPP), so each lane
 // writes two columns of one row as one 4-byte store. Rows are 2 BN bytes with no padding; the 16-byte
-// chunks of odd rows are XOR-swizzled by 4 so the two rows a half-wavefront writes use different banks.
+// chunks are XOR-swizzled by row (sbf_word) so the four rows one store instruction writes use
+// different banks.
 __host__ __device__ __forceinline__ bool stage_bf16_ok(const GemmArgs& g, int vec) {
   return g.c_bf16 && !g.ws && !g.C2 && vec == 8 &&
          (g.epi == PH_EPI_NONE || g.epi == PH_EPI_BIAS || g.epi == PH_EPI_BIAS_RELU);
 }
+// One staging store instruction writes rows R, R + 1 (half-wavefront 0) and R + 4, R + 5 (half 1),
+// 32 columns (4 chunks) each; the 64 LDS banks see each row's chunks at a different 16-bank offset.
+// 16 chunks per row (BN 128, rows 64 words): chunk ^ 4 (row bit 0) ^ 8 (row bit 2). 8 chunks per row
+// (rows 32 words, so odd rows already sit 32 banks on): chunk ^ 4 when row bits 0 and 2 differ.
 __device__ __forceinline__ int sbf_word(int row, int col, int BN) {
-  const int ch = (col >> 3) ^ ((row & 1) << 2);
+  const int sw = BN >= 128 ? ((row & 1) << 2) | (((row >> 2) & 1) << 3) : (((row ^ (row >> 2)) & 1) << 2);
+  const int ch = (col >> 3) ^ sw;
   return row * (BN / 2) + ch * 4 + ((col & 7) >> 1);
 }
 template <int EPI, int BN, int SM, int SN>
