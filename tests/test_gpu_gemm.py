@@ -307,3 +307,24 @@ def test_gemm_nt_bf16_staging_matches_fp32_staging(gpu, M, N):
         if epi == L.PH_EPI_BIAS_RELU:
             r = np.maximum(r, 0.0)
         assert rel(c16.float().cpu().numpy(), r) < 4e-3
+
+
+@pytest.mark.parametrize("M,N,K", [(520, 264, 86024), (1536, 512, 45056), (2048, 2056, 512),
+                                   (300, 132, 1032)])
+def test_gemm_tn_matches_nt_on_transposed_copies(gpu, M, N, K):
+    """The TN form (both operands m/n-contiguous: the weight gradients) transposes 4 x 8 register
+    chunks into LDS; the NT form on transposed copies of the same operands runs the same tiles, LDS
+    contents and MFMA order, so the two give the same bits. Split-K over 256x256 tiles (with a K
+    tail), the weight-gradient shape's split count, 128x128 tiles with a ragged N, and a padded
+    unaligned shape; the first also against the f64 product."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M + N + K)
+    aT = torch.randn(K, M, device="cuda", generator=g).bfloat16()
+    b = torch.randn(K, N, device="cuda", generator=g).bfloat16()
+    c_tn = D.gemm(aT, b, trans_a=True)
+    c_nt = D.gemm(aT.t().contiguous(), b.t().contiguous(), trans_b=True)
+    assert torch.equal(c_tn, c_nt)
+    assert torch.equal(D.gemm(aT, b, trans_a=True), c_tn)  # deterministic split-K fold
+    if M == 520:
+        ref = aT.double().t() @ b.double()
+        assert float((c_tn.double() - ref).norm() / ref.norm()) < 1e-5
