@@ -828,7 +828,8 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
 
   // Prefetch depth: NSETS register sets of k-tiles in flight. Two measured best on the policy shapes
   // (a depth of four made the 256x128 forward 37 % slower: the longer unrolled body costs more than
-  // the added latency cover).
+  // the added latency cover; three or four made the split-K weight gradients 512x128x262144 and
+  // 32x512x262144 at 128x128 tiles 4-14 % slower).
   constexpr int NSETS = 2;
   Raw8<TIA> ra[NSETS][CA];
   Raw8<TIB> rb[NSETS][CB];
