@@ -328,3 +328,18 @@ def test_gemm_tn_matches_nt_on_transposed_copies(gpu, M, N, K):
     if M == 520:
         ref = aT.double().t() @ b.double()
         assert float((c_tn.double() - ref).norm() / ref.norm()) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 128, 131072), (512, 128, 262144)])
+def test_gemm_split_k_tiles_of_a_split_on_one_xcd(gpu, M, N, K):
+    """Weight-gradient reductions long enough for 64 / 128 splits of 2048 (a multiple of 8 splits,
+    each at least 2048 of k) place every tile of one split on one XCD; the split index and tile come
+    from that placement. Against the f64 product of the same bf16 operands, twice (same bits)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M + K)
+    aT = torch.randn(K, M, device="cuda", generator=g).bfloat16()
+    b = torch.randn(K, N, device="cuda", generator=g).bfloat16()
+    c = D.gemm(aT, b, trans_a=True)
+    ref = aT.double().t() @ b.double()
+    assert float((c.double() - ref).norm() / ref.norm()) < 1e-5
+    assert torch.equal(D.gemm(aT, b, trans_a=True), c)
