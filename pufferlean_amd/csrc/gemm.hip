@@ -49,9 +49,9 @@ struct GemmArgs {
   long ldc2;
   int c2_trans;
   int kps;       // k per split
-  float* ws;     // split-K partials [splits][M][N]
+  float* ws;     // split-K partials [splits][M][N] (inside a kernel: this block's split)
   int remap;     // XCD-aware tile order
-  int split_xcd; // all tiles of one k-split on one XCD (splits a multiple of 8)
+  int split_xcd; // 1: all tiles of one k-split on one XCD; 2: each half of a split's tiles on one XCD
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return bf16x2_rne(a, b); }
@@ -198,14 +198,21 @@ __device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...
 }
 
 // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2), so blocks whose linear
-// ids differ by a multiple of 8 run on one XCD, whatever XCD a launch starts on.
-// With split_xcd (a multiple of 8 splits, each a long k range) every tile of one split goes to one XCD:
-// the tiles all read the same k rows of the shared operand, which are then fetched into one L2 instead
-// of up to four (measured on 512x128x262144 at 128 splits: 94 -> 85 us). Short splits keep the plain
-// order: there the tiles of a split reading the same rows at once on one XCD made 512x128x16384 at 32
-// splits slower (17 -> 22 us).
+// ids differ by a multiple of 8 run on one XCD, whatever XCD a launch starts on. The tiles of one
+// k-split all read the same k rows of the operands; placed on one XCD, those rows are fetched into one
+// L2 instead of several. Only long splits (>= 2048 of k) are placed: where the tiles of a split read
+// the same rows at once through one L2, short splits got slower (512x128x16384 at 32 splits: 17 ->
+// 22 us).
+//  split_xcd 1 (a multiple of 8 splits): every tile of a split on one XCD (512x128x262144 at 128
+//    splits: 94 -> 85 us).
+//  split_xcd 2 (a multiple of 4 splits, an even tile count): the first and the second half of a
+//    split's tiles (in tile order) each on one XCD (1536x512x262144 at 256x256 tiles: 508 us at 21
+//    splits unplaced, 512 at 20 unplaced, 494 at 20 placed).
 __device__ __forceinline__ bool split_remap(const GemmArgs& g) {
-  return g.split_xcd && gridDim.z > 1 && (gridDim.z & 7) == 0;
+  if (gridDim.z <= 1) return false;
+  if (g.split_xcd == 1) return (gridDim.z & 7) == 0;
+  if (g.split_xcd == 2) return (gridDim.z & 3) == 0 && (gridDim.x & 1) == 0;
+  return false;
 }
 // (k-split, tile id) of this block
 __device__ __forceinline__ void block_split_tile(const GemmArgs& g, int& z, int& t) {
@@ -214,8 +221,16 @@ __device__ __forceinline__ void block_split_tile(const GemmArgs& g, int& z, int&
   if (split_remap(g)) {
     const int nt = gridDim.x;
     const int L = t + nt * z, slot = L >> 3;
-    z = (L & 7) * ((int)gridDim.z >> 3) + slot / nt;
-    t = slot % nt;
+    if (g.split_xcd == 1) {
+      z = (L & 7) * ((int)gridDim.z >> 3) + slot / nt;
+      t = slot % nt;
+    } else {
+      // half-split groups of nt/2 tiles; XCD x takes groups [x * ng, (x + 1) * ng)
+      const int half = nt >> 1, ng = (int)gridDim.z >> 2;
+      const int grp = (L & 7) * ng + slot / half;
+      z = grp >> 1;
+      t = (grp & 1) * half + slot % half;
+    }
   }
 }
 __device__ __forceinline__ int split_of(const GemmArgs& g) {
@@ -295,7 +310,7 @@ __device__ __forceinline__ void write_tile_t(const GemmArgs& g, const floatx16 (
         const int row = r0 + i * 32 + 8 * (r >> 2) + hrow + (r & 3);
         const int col = c0 + j * 32 + lr;
         if constexpr (EPI < 0) {
-          if (row < g.M && col < g.N) g.ws[((long)split_of(g) * g.M + row) * g.N + col] = acc[i][j][r];
+          if (row < g.M && col < g.N) g.ws[(long)row * g.N + col] = acc[i][j][r];
         } else {
           epilogue_store_t<EPI, TC>(g, row, col, acc[i][j][r]);
         }
@@ -647,7 +662,7 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
         const int row = grow(lr), col = n0 + lc;
         if (row >= g.M || col >= g.N) continue;
         if constexpr (EPI < 0) {
-          store4(g.ws + ((long)split_of(g) * g.M + row) * g.N + col, v[q]);
+          store4(g.ws + (long)row * g.N + col, v[q]);
         } else {
           const float4 w = epi_apply4<EPI, TC>(g, v[q], op[u]);
           store4(reinterpret_cast<TC*>(g.C) + (long)row * g.ldc + col, w);
@@ -664,7 +679,7 @@ __device__ __forceinline__ void flush_tile_t(const GemmArgs& g, float* sC, int m
       const int row = grow(lr), col = n0 + lc;
       if (row >= g.M || col >= g.N) continue;
       const float e = sC[lr * LDC + lc];
-      if constexpr (EPI < 0) g.ws[((long)split_of(g) * g.M + row) * g.N + col] = e;
+      if constexpr (EPI < 0) g.ws[(long)row * g.N + col] = e;
       else epilogue_store_t<EPI, TC>(g, row, col, e);
     }
   }
@@ -847,7 +862,9 @@ __global__ void __launch_bounds__(WGM * WGN * 64) k_gemm_bf16(GemmArgs g) {
   int bm, bn;
   tile_coords(g, tm, tn, bm, bn);
   const int m0 = bm * BM, n0 = bn * BN;
-  const int kbeg = split_of(g) * g.kps;
+  const int zs = split_of(g);
+  const int kbeg = zs * g.kps;
+  if (g.ws) g.ws += (long)zs * g.M * g.N;  // this split's partials
   const int kend = min(g.K, kbeg + g.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
@@ -1168,7 +1185,9 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
   int bm, bn;
   tile_coords(g, tm, tn, bm, bn);
   const int m0 = bm * BM, n0 = bn * BN;
-  const int kbeg = split_of(g) * g.kps;
+  const int zs = split_of(g);
+  const int kbeg = zs * g.kps;
+  if (g.ws) g.ws += (long)zs * g.M * g.N;  // this split's partials
   const int kend = min(g.K, kbeg + g.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
   const gptr<uint16_t> A = (gptr<uint16_t>)g.A;
@@ -1345,7 +1364,9 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
   int bm, bn;
   tile_coords(g, tm, tn, bm, bn);
   const int m0 = bm * BM, n0 = bn * BN;
-  const int kbeg = split_of(g) * g.kps;
+  const int zs = split_of(g);
+  const int kbeg = zs * g.kps;
+  if (g.ws) g.ws += (long)zs * g.M * g.N;  // this split's partials
   const int kend = min(g.K, kbeg + g.kps);
   const int nk = (kend - kbeg + BK - 1) / BK;
   const float* A = reinterpret_cast<const float*>(g.A);
@@ -1704,7 +1725,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   const long tiles128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
   const bool big_ok = d.math == PH_MATH_BF16 && d.a_dtype == PH_BF16 && d.b_dtype == PH_BF16;
-  bool small = false, big = big_ok && tiles256x128 >= 512;
+  bool small = false, big = big_ok && tiles256x128 >= 512, halves = false;
   // NT outputs at most 64 wide (the policy heads): 256x64 tiles, half the wasted columns of 256x128
   int big_bn = !d.trans_a && d.trans_b && d.N <= 64 ? 64 : 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
@@ -1713,7 +1734,11 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
       // give every one of the 256 resident blocks >= 2048 of k; else 128x128 splits of >= 512
       big = big_ok && d.M >= 256 && d.N >= 256 && d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
       big_bn = 256;
-      const long want = big ? 256 / tiles256 : 512 / tiles128;
+      long want = big ? 256 / tiles256 : 512 / tiles128;
+      // 256x256 tiles in an even count of at least 6: a multiple of 4 splits, so each half of a
+      // split's tiles can run on one XCD (split_xcd 2 below)
+      halves = big && tiles256 % 2 == 0 && tiles256 >= 6 && want >= 4;
+      if (halves) want &= ~3L;
       const long maxs = d.K / (big ? 2048 : 512);
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
@@ -1732,7 +1757,10 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   splits = kps > 0 ? (d.K + kps - 1) / kps : 1;
   if (splits < 1) splits = 1;
   g.kps = kps > 0 ? kps : BK;
-  g.split_xcd = splits % 8 == 0 && g.kps >= 2048;
+  if (splits > 1 && g.kps >= 2048) {
+    if (halves && splits % 4 == 0) g.split_xcd = 2;
+    else if (splits % 8 == 0) g.split_xcd = 1;
+  }
   if (splits > 1) {
     g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
