@@ -51,7 +51,7 @@ struct GemmArgs {
   int kps;       // k per split
   float* ws;     // split-K partials [splits][M][N] (inside a kernel: this block's split)
   int remap;     // XCD-aware tile order
-  int split_xcd; // 1: all tiles of one k-split on one XCD; 2: each half of a split's tiles on one XCD
+  int split_xcd; // all tiles of one k-split on one XCD (a multiple of 8 splits)
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return bf16x2_rne(a, b); }
@@ -203,16 +203,12 @@ __device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...
 // L2 instead of several. Only long splits (>= 2048 of k) are placed: where the tiles of a split read
 // the same rows at once through one L2, short splits got slower (512x128x16384 at 32 splits: 17 ->
 // 22 us).
-//  split_xcd 1 (a multiple of 8 splits): every tile of a split on one XCD (512x128x262144 at 128
-//    splits: 94 -> 85 us).
-//  split_xcd 2 (a multiple of 4 splits, an even tile count): the first and the second half of a
-//    split's tiles (in tile order) each on one XCD (1536x512x262144 at 256x256 tiles: 508 us at 21
-//    splits unplaced, 512 at 20 unplaced, 494 at 20 placed).
+// With split_xcd (a multiple of 8 splits) every tile of a split runs on one XCD (512x128x262144 at
+// 128 splits: 94 -> 82 us standalone, 103 -> 99 us inside the MinGRU step). Placing each half of the
+// 12 tiles of a 1536x512x262144 split on one XCD (20 splits instead of 21) was faster standalone (520
+// -> 502 us) but slower inside the step (466 -> 484 us), where the operands arrive from HBM.
 __device__ __forceinline__ bool split_remap(const GemmArgs& g) {
-  if (gridDim.z <= 1) return false;
-  if (g.split_xcd == 1) return (gridDim.z & 7) == 0;
-  if (g.split_xcd == 2) return (gridDim.z & 3) == 0 && (gridDim.x & 1) == 0;
-  return false;
+  return g.split_xcd && gridDim.z > 1 && (gridDim.z & 7) == 0;
 }
 // (k-split, tile id) of this block
 __device__ __forceinline__ void block_split_tile(const GemmArgs& g, int& z, int& t) {
@@ -221,16 +217,8 @@ __device__ __forceinline__ void block_split_tile(const GemmArgs& g, int& z, int&
   if (split_remap(g)) {
     const int nt = gridDim.x;
     const int L = t + nt * z, slot = L >> 3;
-    if (g.split_xcd == 1) {
-      z = (L & 7) * ((int)gridDim.z >> 3) + slot / nt;
-      t = slot % nt;
-    } else {
-      // half-split groups of nt/2 tiles; XCD x takes groups [x * ng, (x + 1) * ng)
-      const int half = nt >> 1, ng = (int)gridDim.z >> 2;
-      const int grp = (L & 7) * ng + slot / half;
-      z = grp >> 1;
-      t = (grp & 1) * half + slot % half;
-    }
+    z = (L & 7) * ((int)gridDim.z >> 3) + slot / nt;
+    t = slot % nt;
   }
 }
 __device__ __forceinline__ int split_of(const GemmArgs& g) {
@@ -1725,7 +1713,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   const long tiles128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
   const bool big_ok = d.math == PH_MATH_BF16 && d.a_dtype == PH_BF16 && d.b_dtype == PH_BF16;
-  bool small = false, big = big_ok && tiles256x128 >= 512, halves = false;
+  bool small = false, big = big_ok && tiles256x128 >= 512;
   // NT outputs at most 64 wide (the policy heads): 256x64 tiles, half the wasted columns of 256x128
   int big_bn = !d.trans_a && d.trans_b && d.N <= 64 ? 64 : 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
@@ -1734,11 +1722,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
       // give every one of the 256 resident blocks >= 2048 of k; else 128x128 splits of >= 512
       big = big_ok && d.M >= 256 && d.N >= 256 && d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
       big_bn = 256;
-      long want = big ? 256 / tiles256 : 512 / tiles128;
-      // 256x256 tiles in an even count of at least 6: a multiple of 4 splits, so each half of a
-      // split's tiles can run on one XCD (split_xcd 2 below)
-      halves = big && tiles256 % 2 == 0 && tiles256 >= 6 && want >= 4;
-      if (halves) want &= ~3L;
+      const long want = big ? 256 / tiles256 : 512 / tiles128;
       const long maxs = d.K / (big ? 2048 : 512);
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
@@ -1757,10 +1741,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   splits = kps > 0 ? (d.K + kps - 1) / kps : 1;
   if (splits < 1) splits = 1;
   g.kps = kps > 0 ? kps : BK;
-  if (splits > 1 && g.kps >= 2048) {
-    if (halves && splits % 4 == 0) g.split_xcd = 2;
-    else if (splits % 8 == 0) g.split_xcd = 1;
-  }
+  g.split_xcd = splits % 8 == 0 && g.kps >= 2048;
   if (splits > 1) {
     g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
