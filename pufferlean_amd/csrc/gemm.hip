@@ -51,7 +51,7 @@ struct GemmArgs {
   int kps;       // k per split
   float* ws;     // split-K partials [splits][M][N] (inside a kernel: this block's split)
   int remap;     // XCD-aware tile order
-  int split_xcd; // all tiles of one k-split on one XCD (a multiple of 8 splits)
+  int split_xcd; // the tiles of one k-split on one XCD
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return bf16x2_rne(a, b); }
@@ -199,26 +199,25 @@ __device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, I...
 
 // Blocks are dispatched round-robin over the 8 XCDs (each with its own L2), so blocks whose linear
 // ids differ by a multiple of 8 run on one XCD, whatever XCD a launch starts on. The tiles of one
-// k-split all read the same k rows of the operands; placed on one XCD, those rows are fetched into one
-// L2 instead of several. Only long splits (>= 2048 of k) are placed: where the tiles of a split read
-// the same rows at once through one L2, short splits got slower (512x128x16384 at 32 splits: 17 ->
-// 22 us).
-// With split_xcd (a multiple of 8 splits) every tile of a split runs on one XCD (512x128x262144 at
-// 128 splits: 94 -> 82 us standalone, 103 -> 99 us inside the MinGRU step). Placing each half of the
-// 12 tiles of a 1536x512x262144 split on one XCD (20 splits instead of 21) was faster standalone (520
-// -> 502 us) but slower inside the step (466 -> 484 us), where the operands arrive from HBM.
-__device__ __forceinline__ bool split_remap(const GemmArgs& g) {
-  return g.split_xcd && gridDim.z > 1 && (gridDim.z & 7) == 0;
-}
+// k-split all read the same k rows of the operands. With split_xcd each XCD takes a contiguous range
+// of (split, tile) ids, so a split's tiles run on one XCD (two where a range boundary cuts the split)
+// and its rows are fetched into one L2 instead of several. Only long splits (>= 2048 of k) are
+// placed: where the tiles of a split read the same rows at once through one L2, short splits got
+// slower (512x128x16384 at 32 splits: 17 -> 22 us). 512x128x262144 at 128 splits: 94 -> 82 us
+// standalone, 103 -> 99 us inside the MinGRU step; 1536x512x262144 at 21 splits of 12 tiles: ~1 %
+// inside the step.
+__device__ __forceinline__ bool split_remap(const GemmArgs& g) { return g.split_xcd && gridDim.z > 1; }
 // (k-split, tile id) of this block
 __device__ __forceinline__ void block_split_tile(const GemmArgs& g, int& z, int& t) {
   z = blockIdx.z;
   t = blockIdx.x;
   if (split_remap(g)) {
-    const int nt = gridDim.x;
-    const int L = t + nt * z, slot = L >> 3;
-    z = (L & 7) * ((int)gridDim.z >> 3) + slot / nt;
-    t = slot % nt;
+    const int nt = gridDim.x, nb = nt * (int)gridDim.z;
+    const int L = t + nt * z, x = L & 7;
+    // XCD x holds ids [x * (nb / 8) + min(x, nb % 8), ...) in dispatch order
+    const int v = x * (nb >> 3) + min(x, nb & 7) + (L >> 3);
+    z = v / nt;
+    t = v % nt;
   }
 }
 __device__ __forceinline__ int split_of(const GemmArgs& g) {
@@ -1741,7 +1740,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   splits = kps > 0 ? (d.K + kps - 1) / kps : 1;
   if (splits < 1) splits = 1;
   g.kps = kps > 0 ? kps : BK;
-  g.split_xcd = splits % 8 == 0 && g.kps >= 2048;
+  g.split_xcd = splits > 1 && g.kps >= 2048;
   if (splits > 1) {
     g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
