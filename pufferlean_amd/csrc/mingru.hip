@@ -232,6 +232,36 @@ __global__ void k_head_scatter(const float* __restrict__ gh, const float* __rest
   }
 }
 
+// bf16 copy of the observations [rows][D] (D a multiple of 8, x 16-byte aligned) with row pitch
+// D + 8: columns D..D+7 hold 1, 0, ..., 0. The encoder's weight-gradient product dh^T [obs | 1 | 0]
+// then carries the bias gradient (the column sums of dh) in its column D.
+__global__ void k_obs_bf16_ones(const float* __restrict__ x, uint16_t* __restrict__ y, long rows, int D) {
+  const int cpr = D / 8 + 1;  // 8-element chunks per row of y
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cpr) return;
+  const long r = i / cpr;
+  const int c = (int)(i - r * cpr);
+  uint4 v = make_uint4(0x3F80u, 0u, 0u, 0u);  // bf16 1.0, then zeros
+  if (c < D / 8) {
+    const float4 a = reinterpret_cast<const float4*>(x + r * D)[2 * c];
+    const float4 b = reinterpret_cast<const float4*>(x + r * D)[2 * c + 1];
+    v = make_uint4(bf16x2_rne(a.x, a.y), bf16x2_rne(a.z, a.w), bf16x2_rne(b.x, b.y), bf16x2_rne(b.z, b.w));
+  }
+  reinterpret_cast<uint4*>(y + r * (D + 8))[c] = v;
+}
+
+// [H][D + 8] product of the encoder backward -> gWEnc (H x D) and gbEnc (column D)
+__global__ void k_enc_scatter(const float* __restrict__ ge, int H, int D, float* __restrict__ gW,
+                              float* __restrict__ gb) {
+  const long n = (long)H * (D + 1);
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const int h = (int)(i / (D + 1)), d = (int)(i - (long)h * (D + 1));
+    const float v = ge[(long)h * (D + 8) + d];
+    if (d < D) gW[(long)h * D + d] = v;
+    else gb[h] = v;
+  }
+}
+
 // V-trace outputs -> the minibatch columns the loss reads: ret = adv + V (already the target),
 // advantage normalised with the minibatch mean/std (stats[0], stats[1] = std + 1e-8).
 __global__ void k_norm_adv(const float* __restrict__ adv, const float* __restrict__ stats, long n,
@@ -260,7 +290,7 @@ __global__ void k_f32_to_bf16_k(const float* __restrict__ x, uint16_t* __restric
 struct Bufs {
   void *obsb, *x, *cmb, *o, *dy, *dh0, *dh1, *dlb;
   void *wenc, *wl, *wlt, *wh, *wht;
-  float *bh, *logit, *dl, *gh, *gbh, *adv, *advn, *tgt, *newlp, *newval, *stats;
+  float *bh, *logit, *dl, *gh, *gbh, *genc, *adv, *advn, *tgt, *newlp, *newval, *stats;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -282,7 +312,7 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
   const size_t es = d.precision == 1 ? 4 : 2;
-  const size_t o_obsb = take((size_t)TB * d.D * 2);
+  const size_t o_obsb = take((size_t)TB * (d.D + 8) * 2);  // pitch D + 8 (a ones column)
   const size_t o_x = take((size_t)(L + 1) * TB * H * es);
   const size_t o_cmb = take((size_t)L * TB * 3 * H * es);
   const size_t o_o = take((size_t)L * TB * H * es);
@@ -300,6 +330,7 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
   const size_t o_dlb = take((size_t)TB * HP * 2);
   const size_t o_gh = take((size_t)HP * H * 4);
   const size_t o_gbh = take(HP * 4);
+  const size_t o_genc = take((size_t)H * (d.D + 8) * 4);
   const size_t o_adv = take((size_t)TB * 4);
   const size_t o_advn = take((size_t)TB * 4);
   const size_t o_tgt = take((size_t)TB * 4);
@@ -329,7 +360,8 @@ int get_bufs(const ph_mingru_dims& d, Bufs& b, hipStream_t st) {
   b.dh0 = base + o_dh0; b.dh1 = base + o_dh1; b.dlb = base + o_dlb; b.wenc = base + o_wenc; b.wl = base + o_wl;
   b.wlt = base + o_wlt; b.wh = base + o_wh; b.wht = base + o_wht;
   b.bh = (float*)(base + o_bh); b.logit = (float*)(base + o_logit); b.dl = (float*)(base + o_dl);
-  b.gh = (float*)(base + o_gh); b.gbh = (float*)(base + o_gbh); b.adv = (float*)(base + o_adv);
+  b.gh = (float*)(base + o_gh); b.gbh = (float*)(base + o_gbh);
+  b.genc = (float*)(base + o_genc); b.adv = (float*)(base + o_adv);
   b.advn = (float*)(base + o_advn); b.tgt = (float*)(base + o_tgt); b.newlp = (float*)(base + o_newlp);
   b.newval = (float*)(base + o_newval); b.stats = (float*)(base + o_stats);
   return PH_OK;
@@ -376,14 +408,15 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   const void* obsg = obs;
   if (BF) {
     PH_REQUIRE(((uintptr_t)obs % 16) == 0, "mingru: observations must be 16-byte aligned");
-    k_f32_to_bf16_k<<<ceil_div(ceil_div(TB * D, 8), kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB * D);
+    k_obs_bf16_ones<<<ceil_div(TB * (D / 8 + 1), kB), kB, 0, st>>>(obs, (uint16_t*)b.obsb, TB, D);
     obsg = b.obsb;
   }
+  const long ldo = BF ? D + 8 : D;  // row pitch of the observations the GEMMs read
   PH_LAUNCH_CHECK();
 
   // encoder: x0 = obs W_enc^T + b_enc
   {
-    PhGemmDesc g = gd(0, 1, (int)TB, H, D, DT, obsg, D, DT, b.wenc, D, DT, x, H, MATH);
+    PhGemmDesc g = gd(0, 1, (int)TB, H, D, DT, obsg, ldo, DT, b.wenc, D, DT, x, H, MATH);
     g.epi = PH_EPI_BIAS; g.bias = params + offBEnc;
     PH_TRY(gemm(g, st));
   }
@@ -460,14 +493,22 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     PH_TRY(gemm(g2, st));
     TS* t = dhn; dhn = dnext; dnext = t;
   }
-  // encoder backward: gbEnc = colsum(dh) on lane 0 (after the head's work queued there) beside
-  // gWEnc = dh^T obs on the main stream; then the main stream waits for the lane
+  // encoder backward. bf16: one product dh^T [obs | 1 | 0] gives gWEnc and, in its column D, gbEnc
+  // (one pass over dh); then the main stream waits for the head's work on lane 0.
+  if (BF) {
+    PhGemmDesc g = gd(1, 0, H, D + 8, (int)TB, DT, dhn, H, DT, obsg, ldo, PH_F32, b.genc, D + 8, MATH);
+    PH_TRY(gemm(g, st));
+    k_enc_scatter<<<ceil_div((long)H * (D + 1), kB), kB, 0, st>>>(b.genc, H, D, G, G + offBEnc);
+    PH_LAUNCH_CHECK();
+    return join_lanes(st, 1);
+  }
+  // fp32: gbEnc = colsum(dh) on lane 0 (after the head's work queued there) beside gWEnc = dh^T obs
+  // on the main stream; then the main stream waits for the lane
   PH_TRY(fork_lanes(st, 1));
   const hipStream_t lane = lane_stream(0);
-  if (BF) PH_TRY(colsum_bf16((const uint16_t*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
-  else PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
+  PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
   {
-    PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, D, PH_F32, G, D, MATH);
+    PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, ldo, PH_F32, G, D, MATH);
     PH_TRY(gemm(g, st));
   }
   return join_lanes(st, 1);
