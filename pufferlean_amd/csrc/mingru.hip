@@ -14,6 +14,7 @@
 // head GEMM has an aligned reduction; padded rows stay zero.
 #include "common.hpp"
 #include "kernels.hpp"
+#include <type_traits>
 
 namespace ph {
 namespace {
@@ -178,6 +179,105 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
       st4(dy + yw, vdg);
       st4(dy + yw + H, vdz);
       st4(dy + yw + 2 * H, vdp);
+      ocur = rpo[c];
+    }
+  }
+}
+
+// Backward scan of the top layer (bf16 tier) with the head's data gradient folded in. dh = dl[:, :nh] Wh
+// is formed per step from the bf16 loss-gradient row of the segment (dlb [TB][HP]) and the head
+// weights Wh [HP][H] held in LDS, instead of being read from a separate GEMM's output; besides dy the
+// kernel writes the gate-skip term dh (1 - sigm(proj)), which the data-gradient GEMM adds with its
+// AXPBY epilogue. H is a multiple of 256, so the H/4 lanes of a segment fill whole wavefronts and the
+// loss-gradient row is read with wavefront-uniform (scalar) loads; NW is the number of its 32-bit words
+// loaded per step (nh <= 2 NW) and CH the steps loaded ahead. The per-step arithmetic of the recurrence
+// is that of k_scan_bwd.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <int NW, int CH>
+__global__ void __launch_bounds__(256) k_scan_bwd_top(const uint16_t* __restrict__ cmb, const uint16_t* __restrict__ oS,
+                                                      const uint16_t* __restrict__ hin,
+                                                      const uint16_t* __restrict__ dlb,
+                                                      const uint16_t* __restrict__ wh, int nh,
+                                                      uint16_t* __restrict__ dy, uint16_t* __restrict__ skip,
+                                                      const float* __restrict__ done, int B, int H, int T) {
+  // Wh row pairs: swp[p * H + j] = Wh[2p][j] | Wh[2p + 1][j] << 16 for p < NW (Wh has HP >= 2 NW rows,
+  // zero past nh, as are dl's columns past nh, so pairs past nh add nothing)
+  extern __shared__ uint32_t swp[];
+  const int HV = H / 4;
+  for (int i = threadIdx.x; i < NW * H; i += blockDim.x) {
+    const int pr = i / H, jj = i - pr * H;
+    swp[i] = (uint32_t)wh[(long)(2 * pr) * H + jj] | ((uint32_t)wh[(long)(2 * pr + 1) * H + jj] << 16);
+  }
+  __syncthreads();  // the only barrier: every thread reaches it before the bounds check
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)B * HV || T <= 0) return;
+  const int b = __builtin_amdgcn_readfirstlane((int)(idx / HV));  // one segment per wavefront
+  const int j = (int)(idx % HV) * 4;
+  const long BH = (long)B * H, B3H = (long)B * 3 * H;
+  const long xo = (long)b * H + j, yo = (long)b * 3 * H + j;
+  const uint4* wj = reinterpret_cast<const uint4*>(swp + j);  // + p * H / 4 for pair p
+  float dOn[4] = {0.f, 0.f, 0.f, 0.f};
+  Raw4<uint16_t> ocur = ld4(oS + (long)(T - 1) * BH + xo);
+  for (int t0 = T - 1; t0 >= 0; t0 -= CH) {
+    Raw4<uint16_t> rh[CH], rg[CH], rp[CH], rx[CH], rpo[CH];
+    uint32_t rl[CH][NW];
+    float rkeep[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+      const int t = t0 - c >= 0 ? t0 - c : 0;  // clamped: a step before 0 is loaded, not used
+      const int tp = t > 0 ? t - 1 : 0;
+      const uint16_t* yt = cmb + (long)t * B3H + yo;
+      rh[c] = ld4(yt);
+      rg[c] = ld4(yt + H);
+      rp[c] = ld4(yt + 2 * H);
+      rx[c] = ld4(hin + (long)t * BH + xo);
+      rpo[c] = ld4(oS + (long)tp * BH + xo);
+      const uint32_t* lr = reinterpret_cast<const uint32_t*>(dlb + ((long)t * B + b) * HP);
+#pragma unroll
+      for (int w = 0; w < NW; w++) rl[c][w] = lr[w];
+      rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+      const int t = t0 - c;
+      if (t < 0) break;
+      // dh = dl Wh[:, j..j+3]: packed bf16 pair products, pairs ascending
+      float dhv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int pr = 0; pr < NW; pr++) {
+        const bf16x2_t dp = __builtin_bit_cast(bf16x2_t, rl[c][pr]);
+        const uint4 w = wj[pr * HV];
+        dhv[0] = __builtin_amdgcn_fdot2_f32_bf16(dp, __builtin_bit_cast(bf16x2_t, w.x), dhv[0], false);
+        dhv[1] = __builtin_amdgcn_fdot2_f32_bf16(dp, __builtin_bit_cast(bf16x2_t, w.y), dhv[1], false);
+        dhv[2] = __builtin_amdgcn_fdot2_f32_bf16(dp, __builtin_bit_cast(bf16x2_t, w.z), dhv[2], false);
+        dhv[3] = __builtin_amdgcn_fdot2_f32_bf16(dp, __builtin_bit_cast(bf16x2_t, w.w), dhv[3], false);
+      }
+      const bool keep_prev = rkeep[c] != 0.f;
+      float vdg[4], vdz[4], vdp[4], vsk[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float hid = el(rh[c], q), gate = el(rg[c], q), proj = el(rp[c], q);
+        const float o = el(ocur, q), hi = el(rx[c], q), dh = dhv[q];
+        const float prev = keep_prev ? el(rpo[c], q) : 0.f;
+        const float z = sigm(gate), hg = sigm(proj), sh = sigm(hid);
+        const float g = hid >= 0.f ? hid + 0.5f : sh;
+        const float dhg = dh * (o - hi);
+        const float dox = dh * hg + dOn[q];
+        const float dz = dox * (g - prev);
+        const float dprev = dox * (1.f - z);
+        const float dg = dox * z;
+        const float sg = hid >= 0.f ? 1.f : sh * (1.f - sh);
+        vdg[q] = dg * sg;
+        vdz[q] = dz * z * (1.f - z);
+        vdp[q] = dhg * hg * (1.f - hg);
+        vsk[q] = dh * (1.f - hg);
+        dOn[q] = keep_prev ? dprev : 0.f;
+      }
+      const long yw = (long)t * B3H + yo;
+      st4(dy + yw, vdg);
+      st4(dy + yw + H, vdz);
+      st4(dy + yw + 2 * H, vdp);
+      st4(skip + (long)t * BH + xo, vsk);
       ocur = rpo[c];
     }
   }
@@ -446,6 +546,13 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   else
     PH_TRY(ppo_grad(b.logit, HP, b.logit + A, HP, act, advn, ret, oldlp, oldval, TB, A, c.vf_coef,
                     c.ent_coef, c.clip_eps, c.vf_clip, 1, b.dl, HP, b.dl + A, HP, newlp, newval, losses, st));
+  // bf16 tier with H a multiple of 256: the top layer's backward scan forms dh_L = dl Wh itself from the
+  // bf16 copy of dl and Wh in LDS (no dh_L GEMM and no dh_L round trip through memory) and writes the
+  // gate-skip term, which its data-gradient GEMM adds as a plain AXPBY operand
+  const int nh = A + 1;
+  // (at most 18 head rows: the 9 words of a loss-gradient row per step, 4 steps ahead, fit the scalar
+  // registers without spilling)
+  const bool top_fused = BF && H % 256 == 0 && nh <= 18 && 9L * H * 4 <= 65536;
   // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh. The bf16 tier's GEMMs round dl to
   // bf16 on the way in; a bf16 copy made once (the same rounding) lets them read half the bytes and
   // the data gradient take the load-to-LDS kernel (86 -> 55 us at 262144 rows). The bias gradient
@@ -470,8 +577,10 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     PH_TRY(colsum_f32(b.dl, TB, HP, HP, b.gbh, 1.f, 0, lane));
     k_head_scatter<<<64, kB, 0, lane>>>(b.gh, b.gbh, H, A, G + offDec);
     PH_LAUNCH_CHECK();
-    PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, dlt, dlg, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
-    PH_TRY(gemm(g2, st));
+    if (!top_fused) {
+      PhGemmDesc g2 = gd(0, 1, (int)TB, H, HP, dlt, dlg, HP, DT, b.wht, HP, DT, b.dh0, H, MATH);
+      PH_TRY(gemm(g2, st));
+    }
   }
   // layers backward
   TS* dhn = (TS*)b.dh0;
@@ -479,8 +588,23 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   for (int l = L - 1; l >= 0; l--) {
     TS* xl = x + (long)l * TB * H;
     TS* cmb = cmbs + (long)l * TB * 3 * H;
-    k_scan_bwd<TS><<<ceil_div((long)d.B * H / 4, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn,
-                                                                 dy, done, d.B, H, d.T);
+    const bool fused = top_fused && l == L - 1;  // dhn then receives the gate-skip term
+    if constexpr (std::is_same_v<TS, uint16_t>) {
+      if (fused) {
+        const unsigned grid = ceil_div((long)d.B * H / 4, kB);
+        const size_t lds = (size_t)(nh <= 16 ? 8 : 9) * H * 4;
+        const uint16_t* os_l = os + (long)l * TB * H;
+        if (nh <= 16)
+          k_scan_bwd_top<8, kScanCh><<<grid, kB, lds, st>>>(cmb, os_l, xl, (const uint16_t*)b.dlb,
+                                                            (const uint16_t*)b.wh, nh, dy, dhn, done, d.B, H, d.T);
+        else
+          k_scan_bwd_top<9, kScanCh><<<grid, kB, lds, st>>>(cmb, os_l, xl, (const uint16_t*)b.dlb,
+                                                            (const uint16_t*)b.wh, nh, dy, dhn, done, d.B, H, d.T);
+      }
+    }
+    if (!fused)
+      k_scan_bwd<TS><<<ceil_div((long)d.B * H / 4, kB), kB, 0, st>>>(cmb, os + (long)l * TB * H, xl, dhn, dy, done,
+                                                                   d.B, H, d.T);
     PH_LAUNCH_CHECK();
     // gW_l = dy^T x_l  -> G
     PhGemmDesc g = gd(1, 0, 3 * H, H, (int)TB, DT, dy, 3 * H, DT, xl, H, PH_F32,
@@ -489,7 +613,11 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     // dh_in = dy W_l + dhn (1 - sigm(proj))   (W_l^T stored [H][3H]; proj = third block of cmb)
     PhGemmDesc g2 =
         gd(0, 1, (int)TB, H, 3 * H, DT, dy, 3 * H, DT, wlt + l * szL, 3 * H, DT, dnext, H, MATH);
-    g2.epi = kEpiGateSkip; g2.aux = dhn; g2.ldaux = H; g2.aux2 = cmb + 2 * H; g2.ldaux2 = 3 * H;
+    if (fused) {
+      g2.epi = PH_EPI_AXPBY; g2.aux = dhn; g2.ldaux = H; g2.beta = 1.f;  // + dh (1 - sigm(proj)) from the scan
+    } else {
+      g2.epi = kEpiGateSkip; g2.aux = dhn; g2.ldaux = H; g2.aux2 = cmb + 2 * H; g2.ldaux2 = 3 * H;
+    }
     PH_TRY(gemm(g2, st));
     TS* t = dhn; dhn = dnext; dnext = t;
   }
