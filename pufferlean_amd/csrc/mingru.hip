@@ -186,7 +186,8 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
 
 // Backward scan of the top layer (bf16 tier) with the head's data gradient folded in. dh = dl[:, :nh] Wh
 // is formed per step from the bf16 loss-gradient row of the segment (dlb [TB][HP]) and the head
-// weights Wh [HP][H] held in LDS, instead of being read from a separate GEMM's output; besides dy the
+// weights Wh [HP][H] (staged in LDS as row pairs; a thread's pairs stay in its registers across the
+// steps) with packed bf16 dot products, instead of being read from a separate GEMM's output; besides dy the
 // kernel writes the gate-skip term dh (1 - sigm(proj)), which the data-gradient GEMM adds with its
 // AXPBY epilogue. H is a multiple of 256, so the H/4 lanes of a segment fill whole wavefronts and the
 // loss-gradient row is read with wavefront-uniform (scalar) loads; NW is the number of its 32-bit words
