@@ -91,6 +91,26 @@ def test_grad_vs_sequential_oracle(gpu, dims, vfclip, precision):
     assert rel(nv.cpu().numpy().reshape(T, B), rnv) < min(tol, 1e-2)
 
 
+@pytest.mark.parametrize("A", [5, 17])
+def test_grad_top_scan_forms_head_gradient(gpu, A):
+    """bf16 tier with H a multiple of 256: the top layer's backward scan forms the head's data gradient
+    dl.Wh itself (8 loss-gradient words a step for up to 16 head rows, 9 for 17-18) and writes the
+    gate-skip term that the top data gradient adds. Against the sequential oracle at the bf16-tier
+    tolerance; B = 3 leaves a whole idle wavefront in the last workgroup."""
+    B, T, D_, H, L = 3, 12, 8, 256, 2
+    p = init_params(D_, H, L, A, 0x700 + A)
+    obs, act, adv, ret, old, ov, done = make_batch(B, T, D_, A, 0x710 + A)
+    ref, rnlp, rnv = oracle_grad(p, obs, act, adv, ret, old, ov, done, T, B, H, D_, L, A, 0.2)
+    cfg = D.MinGRUConfig(B, T, D_, H, L, A, vf_clip=0.2, precision="bf16")
+    G, nlp, nv = D.mingru_ppo_grad(cfg, cuda32(p), cuda32(obs), torch.from_numpy(act.astype(np.int32)).cuda(),
+                                   cuda32(adv), cuda32(ret), cuda32(old), cuda32(ov), cuda32(done))
+    g = G.cpu().numpy()
+    assert np.isfinite(g).all()
+    assert rel(g, ref) < TOL["bf16"], rel(g, ref)
+    assert rel(nlp.cpu().numpy().reshape(T, B), rnlp) < 1e-2
+    assert rel(nv.cpu().numpy().reshape(T, B), rnv) < 1e-2
+
+
 def test_grad_blocks_match_per_tensor(gpu):
     # every parameter block (encoder, each layer, heads, biases) within tolerance on its own (fp32 tier)
     B, T, D_, H, L, A = 8, 16, 8, 16, 2, 5
