@@ -554,10 +554,10 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   // (at most 18 head rows: the 9 words of a loss-gradient row per step, 4 steps ahead, fit the scalar
   // registers without spilling)
   const bool top_fused = BF && H % 256 == 0 && nh <= 18 && 9L * H * 4 <= 65536;
-  // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh. The bf16 tier's GEMMs round dl to
-  // bf16 on the way in; a bf16 copy made once (the same rounding) lets them read half the bytes and
-  // the data gradient take the load-to-LDS kernel (86 -> 55 us at 262144 rows). The bias gradient
-  // sums fp32 dl.
+  // head backward: gh = dl^T x_L; gbh = colsum(dl); dh_L = dl Wh (by a GEMM, or inside the top layer's
+  // backward scan). The bf16 tier rounds dl to bf16 on the way into these products; a bf16 copy made
+  // once (the same rounding) lets them read half the bytes and the data-gradient GEMM take the
+  // load-to-LDS kernel (86 -> 55 us at 262144 rows). The bias gradient sums fp32 dl.
   {
     const void* dlg = b.dl;
     int dlt = PH_F32;
@@ -569,7 +569,7 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     }
     // The head's weight and bias gradients only fill G's head block, which nothing reads before the
     // join at the end of the backward: they run on library lane 0 (its own split-K slot) beside the
-    // data gradient and the layer backward.
+    // layer backward (and the head's data-gradient GEMM where it runs).
     PH_TRY(fork_lanes(st, 1));
     const hipStream_t lane = lane_stream(0);
     PhGemmDesc g = gd(1, 0, HP, H, (int)TB, dlt, dlg, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
