@@ -1712,7 +1712,7 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   const long tiles128 = (long)((d.M + 127) / 128) * ((d.N + 127) / 128);
   const long tiles64 = (long)((d.M + 63) / 64) * ((d.N + 63) / 64);
   const bool big_ok = d.math == PH_MATH_BF16 && d.a_dtype == PH_BF16 && d.b_dtype == PH_BF16;
-  bool small = false, big = big_ok && tiles256x128 >= 512;
+  bool small = false, big = big_ok && tiles256x128 >= 512, wide_n = false;
   // NT outputs at most 64 wide (the policy heads): 256x64 tiles, half the wasted columns of 256x128
   int big_bn = !d.trans_a && d.trans_b && d.N <= 64 ? 64 : 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
@@ -1721,7 +1721,12 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
       // give every one of the 256 resident blocks >= 2048 of k; else 128x128 splits of >= 512
       big = big_ok && d.M >= 256 && d.N >= 256 && d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
       big_bn = 256;
-      const long want = big ? 256 / tiles256 : 512 / tiles128;
+      // TN bf16 products 129..256 wide (the encoder's weight gradient with its bias column): 128x256
+      // tiles, one block per CU, so each split reads its rows of A once (512x136x262144: 120 -> 109 us
+      // against two 128-wide column tiles)
+      wide_n = !big && d.trans_a && !d.trans_b && big_ok && d.N > 128 && d.N <= 256;
+      const long tw = (long)((d.M + 127) / 128);
+      const long want = big ? 256 / tiles256 : (wide_n ? 256 / tw : 512 / tiles128);
       const long maxs = d.K / (big ? 2048 : 512);
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
@@ -1745,11 +1750,13 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
     g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
   }
-  const int bm = big ? 256 : (small ? 64 : 128), bn = big ? big_bn : bm;
+  const int bm = big ? 256 : (small ? 64 : 128), bn = big ? big_bn : (wide_n ? 256 : bm);
   const unsigned tiles = (unsigned)(((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn));
   dim3 grid(tiles, 1, splits);
   if (big) {
     dispatch_big(g, bn, d.trans_a, d.trans_b, grid, st);
+  } else if (wide_n) {
+    launch_bf16<128, 256, 32, true, false, uint16_t, uint16_t>(g, grid, st);
   } else if (d.math == PH_MATH_BF16) {
     if (small) dispatch_bf16<64, 64>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);
     else dispatch_bf16<128, 128>(g, d.a_dtype, d.b_dtype, d.trans_a, d.trans_b, grid, st);

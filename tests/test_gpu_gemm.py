@@ -343,3 +343,18 @@ def test_gemm_split_k_tiles_of_a_split_on_one_xcd(gpu, M, N, K):
     ref = aT.double().t() @ b.double()
     assert float((c.double() - ref).norm() / ref.norm()) < 1e-5
     assert torch.equal(D.gemm(aT, b, trans_a=True), c)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 136, 262144), (300, 200, 8200), (136, 256, 65536)])
+def test_gemm_tn_split_k_128x256_tiles(gpu, M, N, K):
+    """TN bf16 split-K products 129..256 wide take 128x256 tiles, one block per CU (the encoder's
+    weight and bias gradients over the observation copy with its ones column: 512 x 136). Ragged M
+    and N and a K tail; against the f64 product of the same bf16 operands, twice (same bits)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M * N + K)
+    aT = torch.randn(K, M, device="cuda", generator=g).bfloat16()
+    b = torch.randn(K, N, device="cuda", generator=g).bfloat16()
+    c = D.gemm(aT, b, trans_a=True)
+    ref = aT.double().t() @ b.double()
+    assert float((c.double() - ref).norm() / ref.norm()) < 1e-5
+    assert torch.equal(D.gemm(aT, b, trans_a=True), c)
