@@ -169,9 +169,10 @@ def bench_ppo_step(steps, warmup, eager=False):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     finite = bool(torch.isfinite(p).all().item())
+    ns_valid = ns_ok()
     rows = B5 * T5
     out = {"ms": round(ms, 4), "samples_per_s": round(rows / (ms * 1e-3), 1), "rows": rows,
-           "params": cfg.P, "graph": graph is not None, "finite": finite,
+           "params": cfg.P, "graph": graph is not None, "finite": finite, "ns_ok": ns_valid,
            "losses": [round(float(x), 5) for x in losses.cpu().tolist()]}
     # dominant kernel: the layer-forward GEMM (x_l W_l^T, 262144 x 1536 x 512, bf16 in/out), timed
     # as 3 warm-up + 10 launches after the step loop
@@ -185,6 +186,19 @@ def bench_ppo_step(steps, warmup, eager=False):
                               "tflops": round(tf, 1), "flops": flops,
                               "hbm_bytes": 2.0 * (rows * H5 + rows * 3 * H5 + 3 * H5 * H5)}
     return out
+
+
+def ns_ok():
+    """False if a fused Newton-Schulz launch since the last check gave up a bounded wait or left a work
+    queue without blocks on its XCD: its matrices, and every update that used them, are invalid. The
+    library keeps that record on the device; reading it synchronises and clears it."""
+    from pufferlean_amd import device as D
+    try:
+        D.ns_status()
+        return True
+    except Exception as e:  # noqa: BLE001 - the library's error text is the report
+        print(f"# newton-schulz status: {e}", file=sys.stderr, flush=True)
+        return False
 
 
 def time_graph(fn, steps, warmup):
@@ -266,7 +280,7 @@ def bench_ns(steps, warmup):
     flops = sum(5 * (4 * min(r, c) ** 2 * max(r, c) + 2 * min(r, c) ** 3) for r, c in shapes)
     tf = flops / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-            "flops": flops, "matrices": len(shapes), "us_eager": round(ms_eager * 1e3, 1)}
+            "flops": flops, "matrices": len(shapes), "us_eager": round(ms_eager * 1e3, 1), "ns_ok": ns_ok()}
 
 
 def bench_vtrace(steps, warmup):
@@ -819,9 +833,11 @@ def main():
     if args.only in ("all", "cartpole"):
         comps["cartpole"] = bench_cartpole(args.steps, args.warmup)
         print("# cartpole done", file=sys.stderr, flush=True)
+    # a step whose Newton-Schulz gave up has no valid figure: no value is printed for it
+    valid = head is not None and head["finite"] and head["ns_ok"]
     line = {
         "metric": METRIC,
-        "value": head["samples_per_s"] if head else None,
+        "value": head["samples_per_s"] if valid else None,
         "unit": "samples/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": head["ms"] if head else None,
@@ -841,6 +857,10 @@ def main():
                             "algorithmic_bytes": dk["hbm_bytes"]}
         line["step"] = {k: v for k, v in head.items() if k != "dominant_kernel"}
     line["components"] = comps
+    if head is not None and not valid:
+        line["error"] = "the timed step produced invalid weights (non-finite, or a Newton-Schulz launch gave up)"
+    if "ns" in comps and not comps["ns"]["ns_ok"]:
+        comps["ns"]["us"] = comps["ns"]["tflops"] = comps["ns"]["frac"] = None
     if not args.no_cpu_baseline:
         nt = cpu_threads()
         if head:
@@ -848,7 +868,7 @@ def main():
             print("# cpu baseline ppo done", file=sys.stderr, flush=True)
         line["cpu_baselines"] = cpu_baselines(args.only)
     print(json.dumps(line))
-    return 0
+    return 0 if (head is None or valid) else 1
 
 
 if __name__ == "__main__":

@@ -195,7 +195,11 @@ int ph_newton_schulz_batch(float* const* X, const int* rows, const int* cols, in
  * a bounded spin, for the tiles of earlier phases computed by other workgroups. A wait that reaches
  * its bound lets the launch finish with invalid matrices and records the failure on the device.
  * ph_ns_status synchronises `stream`, reads and clears that record, and returns PH_ERR_HIP (with a
- * message) when a launch since the last check gave up; PH_OK otherwise. */
+ * message) when a launch since the last check gave up; PH_OK otherwise. Callers of the entries above
+ * in bf16 math poll it, e.g. once per update (the weights of an update whose launch gave up are
+ * invalid, though usually still finite). These launches share one set of control words per device:
+ * two of them must not overlap in time on different streams of one device (order them on one
+ * stream). */
 int ph_ns_status(void* stream);
 /* Spin bound of those waits, in polls of about a microsecond (0 restores the default, 2^20). A tiny
  * bound makes the waits give up; it exists so that the failure report can be tested. */

@@ -44,6 +44,33 @@ inline LaneSlots lane_slots(int lane) {
 hipStream_t lane_stream(int lane);
 int fork_lanes(hipStream_t main, int n);  // lanes 0..n-1 wait for work queued so far on main
 int join_lanes(hipStream_t main, int n);  // main waits for everything queued on lanes 0..n-1
+// join_lanes on an error path: the error message already set is kept whatever the join returns.
+void join_lanes_on_exit(hipStream_t main, int n);
+
+// Joins lanes 0..n-1 back into `main` on every exit of the scope that forked them, error returns
+// included: an unjoined fork invalidates a stream capture, and in eager mode later work on `main`
+// would not wait for the lanes' writes. join() joins now (its status is the caller's); the destructor
+// joins whatever is still forked and keeps the error message already set.
+struct LaneJoin {
+  hipStream_t main;
+  int n = 0;
+  explicit LaneJoin(hipStream_t m) : main(m) {}
+  int fork(int k) {
+    if (k > n) n = k;  // lanes that waited before a failure are joined as well
+    return fork_lanes(main, k);
+  }
+  int join() {
+    const int k = n;
+    n = 0;
+    return join_lanes(main, k);
+  }
+  void joined() { n = 0; }  // a callee joined them
+  ~LaneJoin() {
+    if (n) join_lanes_on_exit(main, n);
+  }
+  LaneJoin(const LaneJoin&) = delete;
+  LaneJoin& operator=(const LaneJoin&) = delete;
+};
 
 // Zero a block of n words once per pointer (fill kernel, no memset node; for a fixed-size scratch
 // slot, whose pointer never changes).

@@ -494,6 +494,7 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
   const int H = d.H, D = d.D, L = d.L, A = d.A;
   Bufs b;
   PH_TRY(get_bufs(d, b, st));
+  LaneJoin lanes(st);  // lane 0 (head and fp32 encoder bias gradients) is joined on every exit
   TS* x = (TS*)b.x;
   TS* cmbs = (TS*)b.cmb;
   TS* os = (TS*)b.o;
@@ -570,7 +571,7 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     // The head's weight and bias gradients only fill G's head block, which nothing reads before the
     // join at the end of the backward: they run on library lane 0 (its own split-K slot) beside the
     // layer backward (and the head's data-gradient GEMM where it runs).
-    PH_TRY(fork_lanes(st, 1));
+    PH_TRY(lanes.fork(1));
     const hipStream_t lane = lane_stream(0);
     PhGemmDesc g = gd(1, 0, HP, H, (int)TB, dlt, dlg, HP, DT, xL, H, PH_F32, b.gh, H, MATH);
     g.ws_slot = lane_slots(0).gemm_ws;
@@ -629,18 +630,18 @@ int mingru_ppo_grad_t(const ph_mingru_dims& d, const ph_ppo_coefs& c, const Head
     PH_TRY(gemm(g, st));
     k_enc_scatter<<<ceil_div((long)H * (D + 1), kB), kB, 0, st>>>(b.genc, H, D, G, G + offBEnc);
     PH_LAUNCH_CHECK();
-    return join_lanes(st, 1);
+    return lanes.join();
   }
   // fp32: gbEnc = colsum(dh) on lane 0 (after the head's work queued there) beside gWEnc = dh^T obs
   // on the main stream; then the main stream waits for the lane
-  PH_TRY(fork_lanes(st, 1));
+  PH_TRY(lanes.fork(1));
   const hipStream_t lane = lane_stream(0);
   PH_TRY(colsum_f32((const float*)dhn, TB, H, H, G + offBEnc, 1.f, 0, lane));
   {
     PhGemmDesc g = gd(1, 0, H, D, (int)TB, DT, dhn, H, DT, obsg, ldo, PH_F32, G, D, MATH);
     PH_TRY(gemm(g, st));
   }
-  return join_lanes(st, 1);
+  return lanes.join();
 }
 
 }  // namespace
@@ -708,13 +709,15 @@ int mingru_step(const ph_mingru_dims& d, const ph_ppo_coefs& c, const ph_muon_co
   // V-trace (bootstrapped variant, time-major) on the behaviour values, targets = adv + V, and the
   // minibatch advantage normalisation: on lane 0 beside the forward pass, which does not need them
   // (the gradient joins the lane before its loss)
-  PH_TRY(fork_lanes(st, 1));
+  LaneJoin lanes(st);
+  PH_TRY(lanes.fork(1));
   const hipStream_t lane = lane_stream(0);
   PH_TRY(vtrace_f32(rew, oldval, done, logrho, boot, d.B, d.T, 1, 1, logrho != nullptr, 1, c.gamma,
                     c.lam, c.rho_clip, c.c_clip, b.adv, b.tgt, lane));
   PH_TRY(moments_normalize(PH_F32, b.adv, TB, b.advn, b.stats, lane));
   PH_TRY(mingru_ppo_grad(d, c, nullptr, params, obs, act, b.advn, b.tgt, oldlp, oldval, done, G, b.newlp,
                          b.newval, losses, st, true));
+  lanes.joined();  // the gradient joined lane 0 before its loss
   PH_TRY(mingru_muon(d, m, params, mom, G, st));
   return PH_OK;
 }

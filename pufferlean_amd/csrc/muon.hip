@@ -743,13 +743,14 @@ extern "C" int ph_newton_schulz_batch(float* const* X, const int* rows, const in
   // fp32 MFMA: matrix i runs on stream lane i % kLanes with that lane's scratch; the lanes fork
   // from and join back into `stream`.
   const int nl = n < kLanes ? n : kLanes;
-  PH_TRY(fork_lanes(st, nl));
+  LaneJoin lanes(st);
+  PH_TRY(lanes.fork(nl));
   for (int i = 0; i < n; i++) {
     const LaneSlots sl = lane_slots(i % kLanes);
     PH_TRY(newton_schulz_fast(X[i], rows[i], cols[i], coeffs, nsteps, eps, math, sl.ns, sl.gemm_ws,
                               lane_stream(i % kLanes)));
   }
-  return join_lanes(st, nl);
+  return lanes.join();
 }
 
 extern "C" int ph_muon_mat(float* W, const float* G, float* M, int rows, int cols, float gscale,

@@ -13,15 +13,21 @@
 // precision the shifted form roughly halves the error against an f64 iterate.
 //
 // Phases (each a list of 64x64 output tiles):
-//   P0  raw input -> fp32, bf16 and transposed-bf16 wide copies; per-tile sums of squares
+//   P0  raw input -> fp32, bf16 and transposed hi/lo bf16 wide copies; per-tile sums of squares
 //   P1  E = s^2 XX^T - I       lower-triangle tiles (E is symmetric). Writes E in fp32 for the
 //                              tile and its hi/lo bf16 halves (E = Eh + El) for the tile and its
 //                              mirror, so later phases read whole rows
 //   P2  B' = (b+2c)E + cE^2    lower-triangle tiles; E^2 = Eh Eh^T + Eh El^T + El Eh^T (three
 //                              products, one k loop over the concatenated operands). Writes the
 //                              hi/lo bf16 halves of B' (tile and mirror)
-//   P3  X' = s((a+b+c)X + B'X) all tiles; B'X = Bh X + Bl X. Writes fp32, bf16 and transposed
-//                              bf16 copies of X', or the caller's matrix after the last step
+//   P3  X' = s((a+b+c)X + B'X) all tiles; B'X = Bh Xh + Bh Xl + Bl Xh with X = Xh + Xl its hi/lo
+//                              bf16 halves (three products, one k loop). Writes fp32, bf16 and
+//                              transposed hi/lo bf16 copies of X', or the caller's matrix after
+//                              the last step
+// The lo half of X matters on real gradients: B' is O(1) while small singular values are still
+// growing, and 5 steps amplify an error along a small singular direction up to a^5 ~ 480-fold, so
+// B' times the bf16 rounding of X alone left 1.4-2.5e-2 on the MinGRU step's 1536x512 and 16x512
+// momenta (an emulation of this arithmetic reproduces the measured errors); with it, <= 3e-3.
 // s = 1/(||X||_F + eps) at step 0 (the copies hold the raw input), 1 afterwards. Zero padding is
 // exact: padded rows/columns of X stay zero, and E's padded diagonal (-1) only meets zeros of X.
 //
@@ -119,7 +125,7 @@ struct Geo {
   long n0, nt, n3;
   long mw, mm;  // per-step strides (elements) of the wide and the square buffers
   float *xf, *ef, *part;
-  uint16_t *xb, *xt, *eh, *el, *bh, *bl;
+  uint16_t *xb, *xt, *xtl, *eh, *el, *bh, *bl;
 };
 
 // Geometry and scratch layout of one matrix for nsteps steps; returns the scratch bytes it needs.
@@ -147,6 +153,7 @@ __host__ __device__ inline size_t ns_layout(int rows, int cols, int nsteps, unsi
   g.ef = (float*)take(4 * mm * ns);
   g.xb = (uint16_t*)take(2 * mw * ns);
   g.xt = (uint16_t*)take(2 * mw * ns);
+  g.xtl = (uint16_t*)take(2 * mw * ns);
   g.eh = (uint16_t*)take(2 * mm * ns);
   g.el = (uint16_t*)take(2 * mm * ns);
   g.bh = (uint16_t*)take(2 * mm * ns);
@@ -366,7 +373,11 @@ __device__ void p0_convert(const NsMat& mt, const Geo& g, long r, float* stage) 
     const long o = (long)(ti * kT + a) * g.wp + tj * kT + b;
     st_dev<LOCAL>(&g.xf[o], v);
     st_dev<LOCAL>(&g.xb[o], bf16_rne(v));
-    st_dev<LOCAL>(&g.xt[(long)(tj * kT + a) * g.mp + ti * kT + b], bf16_rne(stage[b * 65 + a]));
+    uint16_t th, tl;
+    split_bf16(stage[b * 65 + a], th, tl);
+    const long ot = (long)(tj * kT + a) * g.mp + ti * kT + b;
+    st_dev<LOCAL>(&g.xt[ot], th);
+    st_dev<LOCAL>(&g.xtl[ot], tl);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
@@ -450,16 +461,16 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
     if (p == 3) {
       ti = (int)(r / g.tw);
       tj = (int)(r % g.tw);
-      op.nseg = 2;
+      op.nseg = 3;
       op.ld = g.mp;
       op.K = g.mp;
-      // A segments (Bh, Bl) rows ti; B segments (X^T, X^T) rows tj
+      // A segments (Bh, Bh, Bl) rows ti; B segments (Xh^T, Xl^T, Xh^T) rows tj
       op.a = g.bh + es + (long)ti * kT * g.mp;
       op.da = g.bl - g.bh;
-      op.amask = 2;
+      op.amask = 4;
       op.b = g.xt + xs + (long)tj * kT * g.mp;
-      op.db = 0;
-      op.bmask = 0;
+      op.db = g.xtl - g.xt;
+      op.bmask = 2;
     } else {
       tri_coords(r, ti, tj);
       if (p == 1) {
@@ -547,9 +558,10 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
       float* xfn = g.xf + xs + g.mw;  // next step's input (not touched after the last step)
       uint16_t* xbn = g.xb + xs + g.mw;
       uint16_t* xtn = g.xt + xs + g.mw;
+      uint16_t* xtln = g.xtl + xs + g.mw;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        uint16_t x4[4];
+        uint16_t x4[4], l4[4];
 #pragma unroll
         for (int e4 = 0; e4 < 4; e4++) {
           const int e = 4 * q + e4;
@@ -563,11 +575,15 @@ __global__ void __launch_bounds__(kThreads) k_ns_fused(const NsLaunch L) {
             }
           } else {
             st_dev<LOCAL>(&xfn[o], v);
-            x4[e4] = bf16_rne(v);
+            split_bf16(v, x4[e4], l4[e4]);
             st_dev<LOCAL>(&xbn[o], x4[e4]);
           }
         }
-        if (!last) store_mirror4<LOCAL>(xtn + (long)col * g.mp + row0 + acc_row(4 * q), x4);
+        if (!last) {
+          const long om = (long)col * g.mp + row0 + acc_row(4 * q);
+          store_mirror4<LOCAL>(xtn + om, x4);
+          store_mirror4<LOCAL>(xtln + om, l4);
+        }
       }
     }
     signal_done(done);
@@ -657,9 +673,9 @@ int ns_fused(float* const* X, const int* rows, const int* cols, int n, const flo
       n0[k] = g.n0;
       nt[k] = g.nt;
       n3[k] = g.n3;
-      // tile-chunk products of a step: P1 over w, P2 three over m, P3 two over m
+      // tile-chunk products of a step: P1 over w, P2 three over m, P3 three over m
       const long cw = g.wp / kT, cm = g.mp / kT;
-      work[k] = g.n0 + (long)nsteps * (g.nt * cw + 3 * g.nt * cm + 2 * g.n3 * cm);
+      work[k] = g.n0 + (long)nsteps * (g.nt * cw + 3 * g.nt * cm + 3 * g.n3 * cm);
     }
     i = j;
     if (L.nmat == 0) continue;

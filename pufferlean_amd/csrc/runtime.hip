@@ -1,5 +1,6 @@
 // Library runtime: error channel, per-device growable buffers, device query.
 #include <cstdarg>
+#include <cstdio>
 #include <mutex>
 #include <set>
 
@@ -187,6 +188,12 @@ int join_lanes(hipStream_t main, int n) {
     PH_CHECK_HIP(hipStreamWaitEvent(main, ev, 0));
   }
   return PH_OK;
+}
+
+void join_lanes_on_exit(hipStream_t main, int n) {
+  char saved[sizeof(g_err)];
+  snprintf(saved, sizeof(saved), "%s", g_err);
+  if (join_lanes(main, n) != PH_OK) set_error("%s", saved);
 }
 
 }  // namespace ph

@@ -106,3 +106,50 @@ def test_captured_gemm_survives_scratch_growth(gpu):
     del graph
     D.release_scratch()
     assert D.scratch_retired() == (0, 0)
+
+
+def test_step_error_after_fork_joins_lane(gpu):
+    """An argument error found after the step forked its lane 0 (V-trace and the normalisation already
+    queued there; the gradient then rejects 40 logits, more than the padded head holds) still joins the
+    lane: a capture around the failing call ends cleanly and the library's error is what surfaces, and
+    the stream's later work is unaffected."""
+    from pufferlean_amd._lib import PufferHipError
+    B, T, Dm, H, L = 16, 8, 8, 32, 1
+    n = B * T
+    obs = _t(rng.normal(0x940, n * Dm)).view(T, B, Dm)
+    old = _t(rng.normal(0x941, n, -2.0, 0.1)).view(T, B)
+    val = _t(rng.normal(0x942, n)).view(T, B)
+    rew = _t(rng.normal(0x943, n)).view(T, B)
+    done = _t(rng.bernoulli(0x944, n, 0.05)).view(T, B)
+    logrho = _t(rng.normal(0x945, n, 0.0, 0.1)).view(T, B)
+    boot = _t(rng.normal(0x946, B))
+
+    cfgs = {A: D.MinGRUConfig(B, T, Dm, H, L, A, gscale=1.0 / n, precision="bf16", math="bf16") for A in (5, 40)}
+    acts = {A: _t(rng.randint(0x947, n, A), np.int32).view(T, B) for A in (5, 40)}
+    gs = {A: torch.zeros(cfgs[A].P, device="cuda") for A in (5, 40)}
+
+    def step(A, p, m):  # no allocation or host copy: it also runs under capture
+        D.mingru_step(cfgs[A], p, m, obs, acts[A], old, val, rew, done, logrho, boot, G=gs[A])
+
+    good, bad_P = cfgs[5], cfgs[40].P
+    p0 = rng.normal(0x948, good.P) * 0.1
+    ref_p, ref_m = _t(p0), torch.zeros(good.P, device="cuda")
+    step(5, ref_p, ref_m)
+    torch.cuda.synchronize()
+    with pytest.raises(PufferHipError, match="at most"):  # eager: sizes the buffers, fails after the fork
+        step(40, _t(np.zeros(bad_P)), torch.zeros(bad_P, device="cuda"))
+    torch.cuda.synchronize()
+    pb, mb = _t(np.zeros(bad_P)), torch.zeros(bad_P, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with pytest.raises(PufferHipError, match="at most"):
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                step(40, pb, mb)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    p, m = _t(p0), torch.zeros(good.P, device="cuda")
+    step(5, p, m)
+    torch.cuda.synchronize()
+    assert torch.equal(p, ref_p) and torch.equal(m, ref_m)

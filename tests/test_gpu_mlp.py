@@ -145,6 +145,35 @@ def test_cartpole_update_vs_oracle_chain(gpu):
     assert np.all(np.isfinite(p.cpu().numpy()))
 
 
+def test_cartpole_update_bf16_vs_oracle_chain(gpu):
+    """The bf16 tier of the CartPole-sized update (bf16 MFMA products and bf16 hidden activations, fp32
+    master weights, fp32 Newton-Schulz): per matrix and per bias, the new momentum and the weight change
+    within 2e-2 relative Frobenius of the f64 oracle chain, and the whole gradient within 2e-2 (the bar of
+    the two-hidden-layer bf16 gradient)."""
+    w = cartpole()
+    print(f"cartpole update bf16 N={w['N']} obs {w['Dm']} -> {w['H']} x {w['L']} -> {w['A']}+1", flush=True)
+    g_ref, p_ref, m_ref = oracle_update(w)
+    cfg = D.MLPConfig(w["N"], w["Dm"], w["H"], w["L"], w["A"], math="bf16", muon_math="f32")
+    p = t32(w["p"]); m = torch.zeros(cfg.P, device="cuda")
+    G = D.mlp_update(cfg, w["T"], p, m, t32(w["obs"]), t32(w["act"], np.int32), t32(w["behav"]), t32(w["rew"]),
+                     t32(w["done"]))
+    torch.cuda.synchronize()
+    g, newp, newm = G.cpu().numpy(), p.cpu().numpy(), m.cpu().numpy()
+    assert rel(g, g_ref) < 2e-2, rel(g, g_ref)
+    mats, vecs = matrices(w["Dm"], w["H"], w["L"], w["A"])
+    errs = {}
+    for off, r, cc in mats:
+        s = slice(off, off + r * cc)
+        errs[f"W{r}x{cc}@{off}"] = (rel(newm[s], m_ref[s]), rel(newp[s] - w["p"][s], p_ref[s] - w["p"][s]))
+    for off, k in vecs:
+        s = slice(off, off + k)
+        errs[f"b{k}@{off}"] = (rel(newm[s], m_ref[s]), rel(newp[s] - w["p"][s], p_ref[s] - w["p"][s]))
+    print({k: (f"{a:.2e}", f"{b:.2e}") for k, (a, b) in errs.items()}, flush=True)
+    for name, (em, eu) in errs.items():
+        assert em < 2e-2, (name, "momentum", em)
+        assert eu < 2e-2, (name, "update", eu)
+
+
 def test_cartpole_update_graph_replay(gpu):
     """The update is stream work only: a captured update replays bit-identically to the eager one."""
     w = cartpole(0xCB00)

@@ -32,6 +32,40 @@ def _run(fn, dtype, x, with_stats):
     return out, stats
 
 
+def test_noalloc_under_graph_capture(gpu):
+    """Captured in a HIP graph, first as the process's first call of the entry (its per-device address
+    lookup then happens inside the capture; this test is the file's first), then again after eager
+    calls: every replay, with eager work and synchronisations between replays, equals the allocating
+    entry's eager result bit for bit."""
+    ref, na = _fns()
+    n = 300_001
+    x = torch.from_numpy(rng.normal(75, n, 0.3, 1.7)).float().to(gpu)
+    o_ref, s_ref = _run(ref, torch.float32, x, True)
+    for attempt in range(2):
+        out = torch.empty_like(x)
+        stats = torch.zeros(2, device=gpu)
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                _lib.check(na(_lib.PH_F32, x.data_ptr(), n, out.data_ptr(), stats.data_ptr(), s.cuda_stream),
+                           "ph_adv_normalize_noalloc")
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for k in range(3):
+            out.zero_()
+            stats.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            _ = (torch.ones(1000, device=gpu) * 2).sum().item()
+            assert torch.equal(out, o_ref), (attempt, k)
+            assert torch.equal(stats, s_ref), (attempt, k)
+        if attempt == 0:
+            _run(na, torch.float32, x, True)  # eager calls between the two captures
+            _run(na, torch.float32, x[:4097], False)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_noalloc_matches_allocating_entry(gpu, dtype):
     ref, na = _fns()
