@@ -174,18 +174,57 @@ def bench_ppo_step(steps, warmup, eager=False):
     out = {"ms": round(ms, 4), "samples_per_s": round(rows / (ms * 1e-3), 1), "rows": rows,
            "params": cfg.P, "graph": graph is not None, "finite": finite, "ns_ok": ns_valid,
            "losses": [round(float(x), 5) for x in losses.cpu().tolist()]}
-    # dominant kernel: the layer-forward GEMM (x_l W_l^T, 262144 x 1536 x 512, bf16 in/out), timed
-    # as 3 warm-up + 10 launches after the step loop
-    x = torch.randn(rows, H5, device="cuda").bfloat16()
-    w = (torch.randn(3 * H5, H5, device="cuda") / 22.6).bfloat16()
-    y = torch.empty(rows, 3 * H5, device="cuda", dtype=torch.bfloat16)
-    gms = time_loop(lambda: D.gemm(x, w, trans_b=True, out=y), 10, 3)
-    flops = 2.0 * rows * 3 * H5 * H5
-    tf = flops / (gms * 1e-3) / 1e12
-    out["dominant_kernel"] = {"name": "k_gemm_nt_dma (layer forward 262144x1536x512, bf16)", "us": round(gms * 1e3, 1),
-                              "tflops": round(tf, 1), "flops": flops,
-                              "hbm_bytes": 2.0 * (rows * H5 + rows * 3 * H5 + 3 * H5 * H5)}
+    out["dominant_kernel"] = dominant_kernel()
     return out
+
+
+DGRAD_SETS = 3  # operand sets the dominant-kernel loop rotates through (2.4 GB of dy: not cache-resident)
+
+
+def dgrad_operands(sets=DGRAD_SETS):
+    """The step's data-gradient product of one layer as the step runs it: dh_in = dy W_l + skip, with dy
+    [262144 x 1536] bf16, the transposed weight copy W_l^T [512 x 1536] bf16 (an NT product over k = 1536)
+    and the gate-skip term the top layer's backward scan writes, added by the AXPBY epilogue into dh_in
+    [262144 x 512] bf16. `sets` independent operand sets, so a loop over them reads dy from HBM."""
+    import torch
+    rows = B5 * T5
+    ops = []
+    for _ in range(sets):
+        dy = (torch.randn(rows, 3 * H5, device="cuda") * 0.1).bfloat16()
+        wt = (torch.randn(H5, 3 * H5, device="cuda") / 39.2).bfloat16()
+        skip = (torch.randn(rows, H5, device="cuda") * 0.1).bfloat16()
+        out = torch.empty(rows, H5, device="cuda", dtype=torch.bfloat16)
+        ops.append((dy, wt, skip, out))
+    return ops
+
+
+def dgrad_launch(op):
+    from pufferlean_amd import _lib as L
+    from pufferlean_amd import device as D
+    dy, wt, skip, out = op
+    D.gemm(dy, wt, trans_b=True, out=out, epilogue=L.PH_EPI_AXPBY, aux=skip, alpha=1.0, beta=1.0)
+
+
+def dominant_kernel():
+    """The data-gradient GEMM (the step's largest kernel family: two launches per step), timed with HIP
+    events on the stream it runs on over 30 launches that rotate through three operand sets, after 0.25 s
+    of warm-up launches."""
+    import torch
+    rows = B5 * T5
+    ops = dgrad_operands()
+    it = [0]
+
+    def fn():
+        dgrad_launch(ops[it[0] % len(ops)])
+        it[0] += 1
+    gms = time_loop(fn, 30, 6)
+    flops = 2.0 * rows * H5 * 3 * H5
+    tf = flops / (gms * 1e-3) / 1e12
+    del ops
+    torch.cuda.empty_cache()
+    return {"name": "k_gemm_nt_dma (data gradient 262144x512x1536, bf16, AXPBY epilogue)", "us": round(gms * 1e3, 1),
+            "tflops": round(tf, 1), "flops": flops,
+            "hbm_bytes": 2.0 * (rows * 3 * H5 + H5 * 3 * H5 + 2 * rows * H5)}
 
 
 def ns_ok():
@@ -542,26 +581,22 @@ def bench_heads(steps, warmup):
 
 def traffic_kernels():
     """Launches for the two HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE):
-    the dominant kernel (layer-forward GEMM) 3 times, then a plain 512 MiB device copy 3 times, whose
-    known byte count scales the counters."""
+    the dominant kernel (the data-gradient GEMM, one operand set per launch) 3 times, then a plain
+    512 MiB device copy 3 times, whose known byte count scales the counters."""
     import torch
-    from pufferlean_amd import device as D
-    rows = B5 * T5
-    x = torch.randn(rows, H5, device="cuda").bfloat16()
-    w = (torch.randn(3 * H5, H5, device="cuda") / 22.6).bfloat16()
-    y = torch.empty(rows, 3 * H5, device="cuda", dtype=torch.bfloat16)
-    for _ in range(3):
-        D.gemm(x, w, trans_b=True, out=y)
+    ops = dgrad_operands()
+    for op in ops:
+        dgrad_launch(op)
     torch.cuda.synchronize()
     a = torch.ones(1 << 28, device="cuda", dtype=torch.bfloat16)
     b = torch.empty_like(a)
     for _ in range(3):
         b.copy_(a)
     torch.cuda.synchronize()
-    return {"gemm": [rows, 3 * H5, H5], "copy_bytes": 2 * a.numel()}
+    return {"gemm": [B5 * T5, H5, 3 * H5], "copy_bytes": 2 * a.numel()}
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_layer_fwd_262144x1536x512_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_dgrad_262144x512x1536_traffic.json")
 
 
 def measured_traffic():
@@ -595,16 +630,25 @@ def cpu_model():
     return "unknown"
 
 
-def _median_time(fn, budget_s, min_reps=3, max_reps=11):
+WARMUPS, REPS = 3, 10  # CPU baselines: median of REPS timed runs after WARMUPS untimed ones
+
+
+def _median_time(fn, budget_s, reps=REPS, warmups=WARMUPS, min_reps=3):
+    """Median wall time of fn() over `reps` runs after `warmups` untimed ones. A leg whose runs are too
+    long for `budget_s` stops after at least `min_reps` and says so: returns (median, timing record)."""
     import statistics
-    fn()  # warm-up
+    for _ in range(warmups):
+        fn()
     ts = []
     t_start = time.perf_counter()
-    while len(ts) < max_reps and (len(ts) < min_reps or time.perf_counter() - t_start < budget_s):
+    while len(ts) < reps and (len(ts) < min_reps or time.perf_counter() - t_start < budget_s):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-    return statistics.median(ts), len(ts)
+    rec = {"reps": len(ts), "warmups": warmups}
+    if len(ts) < reps:
+        rec["budget_limited"] = f"{len(ts)} of {reps} reps within the {budget_s:.0f} s budget of this leg"
+    return statistics.median(ts), rec
 
 
 def _oracle():
@@ -613,7 +657,7 @@ def _oracle():
     return O
 
 
-def cpu_baseline_gemm(nt, budget_s=8.0):
+def cpu_baseline_gemm(nt, budget_s=15.0):
     """Config 2 on the oracle's blocked f64 GEMM over nt threads (the reference's CPU GEMMs are OpenBLAS
     dgemm): GFLOP/s per form."""
     import numpy as np
@@ -629,14 +673,14 @@ def cpu_baseline_gemm(nt, budget_s=8.0):
              "wgrad": lambda: O.lib().orc_gemm_blocked(1, 0, N, K, M, O.P(dY), N, O.P(X), K, O.P(C3), K, nt)}
     out = {}
     for name, fn in forms.items():
-        t, reps = _median_time(fn, budget_s / 3)
-        out[name] = {"value": round(2.0 * M * N * K / t / 1e9, 2), "unit": "GFLOP/s", "ms": round(t * 1e3, 1),
-                     "reps": reps}
+        t, rec = _median_time(fn, budget_s / 3)
+        out[name] = dict({"value": round(2.0 * M * N * K / t / 1e9, 2), "unit": "GFLOP/s", "ms": round(t * 1e3, 1)},
+                         **rec)
     return {"forms": out, "cores": nt, "kind": "port",
             "sample": "the whole 16384x512x512 product per form, f64, blocked and packed, OpenMP"}
 
 
-def cpu_baseline_ns(nt, budget_s=12.0):
+def cpu_baseline_ns(nt, budget_s=25.0):
     """Config 3: the oracle's Newton-Schulz (the reference's naive f64 products) on the six matrices over
     nt threads, and on one thread for one step of one 512x512 matrix, scaled to the batch by flops."""
     import numpy as np
@@ -647,19 +691,18 @@ def cpu_baseline_ns(nt, budget_s=12.0):
     flops = sum(5 * (4 * min(r, c) ** 2 * max(r, c) + 2 * min(r, c) ** 3) for r, c in shapes)
     old = O.lib().orc_set_threads(nt)
     try:
-        t_mt, reps = _median_time(lambda: [O.newton_schulz(m, O.BASELINE_COEFFS, 1e-7, form=1) for m in mats],
-                                  budget_s * 0.6, min_reps=2, max_reps=5)
+        t_mt, rec = _median_time(lambda: [O.newton_schulz(m, O.BASELINE_COEFFS, 1e-7, form=1) for m in mats],
+                                 budget_s * 0.6)
     finally:
         O.lib().orc_set_threads(old)
     one = mats[0]
-    t_1, reps1 = _median_time(lambda: O.newton_schulz(one, O.BASELINE_COEFFS[:1], 1e-7, form=1), budget_s * 0.4,
-                              min_reps=2, max_reps=5)
+    t_1, rec1 = _median_time(lambda: O.newton_schulz(one, O.BASELINE_COEFFS[:1], 1e-7, form=1), budget_s * 0.4)
     f1 = 4 * 512 ** 3 + 2 * 512 ** 3
-    return {"value": round(flops / t_mt / 1e9, 2), "unit": "GFLOP/s", "us": round(t_mt * 1e6, 1), "cores": nt,
-            "reps": reps, "single_thread": {"value": round(f1 / t_1 / 1e9, 3), "unit": "GFLOP/s",
-                                            "batch_us_scaled": round(t_1 * flops / f1 * 1e6, 1), "reps": reps1},
-            "kind": "port", "sample": "all six matrices x 5 steps on nt threads; one step of one 512x512 "
-                                      "matrix on one thread, scaled to the batch's flops"}
+    return dict({"value": round(flops / t_mt / 1e9, 2), "unit": "GFLOP/s", "us": round(t_mt * 1e6, 1),
+                 "cores": nt, "single_thread": dict({"value": round(f1 / t_1 / 1e9, 3), "unit": "GFLOP/s",
+                                                     "batch_us_scaled": round(t_1 * flops / f1 * 1e6, 1)}, **rec1),
+                 "kind": "port", "sample": "all six matrices x 5 steps on nt threads; one step of one 512x512 "
+                                           "matrix on one thread, scaled to the batch's flops"}, **rec)
 
 
 def cpu_baseline_vtrace(nt, budget_s=3.0):
@@ -677,16 +720,17 @@ def cpu_baseline_vtrace(nt, budget_s=3.0):
     adv = np.zeros(n, np.float32); tgt = np.zeros(n, np.float32)
     args = lambda: (O.P(rew), O.P(val), O.P(done), O.P(lr), O.P(boot), B, T, 1, 1, 1, 1, 0.99, 0.95, 1.0, 1.0,
                     O.P(adv), O.P(tgt))
-    t1, r1 = _median_time(lambda: O.lib().orc_vtrace_f32(*args()), budget_s / 2, min_reps=5, max_reps=21)
-    tm, rm = _median_time(lambda: O.lib().orc_vtrace_f32_mt(*args(), nt), budget_s / 2, min_reps=5, max_reps=21)
+    t1, r1 = _median_time(lambda: O.lib().orc_vtrace_f32(*args()), budget_s / 2, reps=21)
+    tm, rm = _median_time(lambda: O.lib().orc_vtrace_f32_mt(*args(), nt), budget_s / 2, reps=21)
     by = 24.0 * n + 4.0 * B
-    return {"value": round(by / tm / 1e9, 2), "unit": "GB/s", "us": round(tm * 1e6, 1), "cores": nt, "reps": rm,
-            "single_thread": {"value": round(by / t1 / 1e9, 2), "unit": "GB/s", "us": round(t1 * 1e6, 1),
-                              "reps": r1},
-            "kind": "port", "sample": "the whole 4096 x 64 fp32 scan (bootstrapped variant, log-ratio input)"}
+    return dict({"value": round(by / tm / 1e9, 2), "unit": "GB/s", "us": round(tm * 1e6, 1), "cores": nt,
+                 "single_thread": dict({"value": round(by / t1 / 1e9, 2), "unit": "GB/s", "us": round(t1 * 1e6, 1)},
+                                       **r1),
+                 "kind": "port", "sample": "the whole 4096 x 64 fp32 scan (bootstrapped variant, log-ratio input)"},
+                **rm)
 
 
-def cpu_baseline_cartpole(nt, budget_s=12.0):
+def cpu_baseline_cartpole(nt, budget_s=20.0):
     """Config 1: the whole CartPole update on the oracle (f64): forward, V-trace, normalisation, the
     gradient of the 4->128->128->3 MLP, Muon on the three matrices; GEMMs and NS products on nt threads."""
     import numpy as np
@@ -719,58 +763,75 @@ def cpu_baseline_cartpole(nt, budget_s=12.0):
 
     old = O.lib().orc_set_threads(nt)
     try:
-        t, reps = _median_time(update, budget_s, min_reps=3, max_reps=11)
+        t, rec = _median_time(update, budget_s)
     finally:
         O.lib().orc_set_threads(old)
-    return {"value": round(N / t, 1), "unit": "samples/s", "ms": round(t * 1e3, 1), "cores": nt, "reps": reps,
-            "kind": "port", "sample": "the whole 65,536-row update (two forwards: V-trace inputs, then the "
-                                      "gradient's), f64"}
+    return dict({"value": round(N / t, 1), "unit": "samples/s", "ms": round(t * 1e3, 1), "cores": nt,
+                 "kind": "port", "sample": "the whole 65,536-row update (two forwards: V-trace inputs, then the "
+                                           "gradient's), f64"}, **rec)
 
 
-def cpu_baseline_ppo(nt, budget_s=20.0):
-    """Config 5 (the headline): the oracle's single-sequence MinGRU PPO gradient (f64, the reference CPU
-    path's algorithm) over a sample of segments spread on nt threads, scaled to the 4096 segments, plus
-    Muon (f64 Newton-Schulz, nt threads) on the five matrices; samples/s = 262,144 / (gradient + Muon)."""
+def cpu_baseline_ppo(nt, budget_s=40.0):
+    """Config 5 (the headline) on the oracle, in the trainer's order: V-trace (bootstrapped, time-major, log
+    ratios) and the advantage normalisation over all 262,144 rows, then the single-sequence MinGRU PPO
+    gradient (f64, the reference CPU path's algorithm) over a sample of segments spread on nt threads and
+    scaled to the 4096 segments, the grad-norm clip, and Muon (f64 Newton-Schulz, nt threads) on the five
+    matrices. samples/s = 262,144 / (V-trace + normalisation + scaled gradient + clip + Muon)."""
     import numpy as np
     O = _oracle()
     params, cols = mingru_inputs(B5, T5, D5, H5, L5, A5)
     P = params.size
+    n = B5 * T5
+    rew, val, done, logrho = (O.f64(cols[k]) for k in ("rew", "val", "done", "logrho"))
+    boot = O.f64(cols["boot"])
+    adv = np.zeros(n)
+
+    def vtrace_norm():
+        a, tg = O.vtrace(rew, val, done, logrho, boot, B5, T5, variant=1, time_major=True, rho_is_log=True)
+        O.lib().orc_adv_normalize(O.P(a), n, O.P(adv))
+        return tg
+
+    t_v, rec_v = _median_time(vtrace_norm, budget_s * 0.1)
+    tgt = vtrace_norm().reshape(T5, B5)
     S = min(B5, 4 * nt)
-    obs = cols["obs"].reshape(T5, B5, D5)[:, :S, :]
-    pick = lambda k: O.f64(cols[k].reshape(T5, B5)[:, :S])
-    act, rew, val, old_, done = (pick(k) for k in ("act", "rew", "val", "old", "done"))
+    obs = O.f64(cols["obs"].reshape(T5, B5, D5)[:, :S, :])
+    pick = lambda x: O.f64(x.reshape(T5, B5)[:, :S])
+    act, old_, vals, term, advs, tgts = (pick(x) for x in (cols["act"], cols["old"], val, done, adv, tgt))
     out = np.zeros(P + 2 * T5 * S)
     grad = lambda: O.lib().orc_mingru_ppo_grad_batch(
-        O.P(params), O.P(O.f64(obs)), O.P(act), O.P(rew), O.P(val), O.P(old_), O.P(done), O.P(val), S, T5, H5,
+        O.P(params), O.P(obs), O.P(act), O.P(advs), O.P(tgts), O.P(old_), O.P(term), O.P(vals), S, T5, H5,
         D5, L5, A5, 0.5, 0.01, 0.2, 0.0, O.P(out), nt)
-    t_g, reps = _median_time(grad, budget_s * 0.6, min_reps=2, max_reps=5)
+    t_g, rec_g = _median_time(grad, budget_s * 0.4)
     cf = O.coeffs_array(O.BASELINE_COEFFS)
     szE, szL = H5 * D5, 3 * H5 * H5
     mats = [(0, H5, D5)] + [(szE + H5 + l * szL, 3 * H5, H5) for l in range(L5)]
     offDec = szE + H5 + L5 * szL
     mats += [(offDec, A5, H5), (offDec + A5 * H5 + A5, 1, H5)]
-    g = out[:P] / (B5 * T5)
+    g = out[:P].copy()
 
-    def muon():
+    def clip_muon():
+        gc = g.copy()
+        O.lib().orc_gclip(O.P(gc), P, 1.0 / n, 0.5)
         for off, r, c in mats:
             k = r * c
             a = np.zeros(k); b = np.zeros(k)
-            O.lib().orc_muon_mat(r, c, O.P(params[off:off + k].copy()), O.P(g[off:off + k].copy()),
+            O.lib().orc_muon_mat(r, c, O.P(params[off:off + k].copy()), O.P(gc[off:off + k].copy()),
                                  O.P(np.zeros(k)), O.P(a), O.P(b), 1.0, 0.015, 0.0, 0.95, 1e-7, O.P(cf), 5, 1)
 
     old = O.lib().orc_set_threads(nt)
     try:
-        t0 = time.perf_counter()
-        muon()
-        t_m = time.perf_counter() - t0
+        t_m, rec_m = _median_time(clip_muon, budget_s * 0.5)
     finally:
         O.lib().orc_set_threads(old)
-    t_step = t_g * B5 / S + t_m
-    return {"value": round(B5 * T5 / t_step, 1), "unit": "samples/s", "cores": nt, "kind": "port",
-            "sample": f"gradient of {S} of 4096 segments x 64 steps on {nt} threads (median of {reps}), scaled to "
-                      f"4096, plus one Muon pass over the 5 matrices (f64 Newton-Schulz, {nt} threads, "
-                      f"{t_m:.2f} s); step {t_step:.1f} s",
-            "gradient_s_per_segment": round(t_g / S, 4), "muon_s": round(t_m, 2)}
+    t_step = t_v + t_g * B5 / S + t_m
+    return {"value": round(n / t_step, 1), "unit": "samples/s", "cores": nt, "kind": "port",
+            "sample": f"V-trace + normalisation over all 4096 segments; gradient over {S} of 4096 segments "
+                      f"({100.0 * S / B5:.1f} %) x 64 steps on {nt} threads, scaled to 4096; clip + Muon on "
+                      f"the 5 matrices ({nt} threads); step {t_step:.1f} s",
+            "sampled_fraction": round(S / B5, 5),
+            "vtrace_norm_s": round(t_v, 4), "vtrace_norm_timing": rec_v,
+            "gradient_s_per_segment": round(t_g / S, 4), "gradient_timing": rec_g,
+            "muon_s": round(t_m, 3), "muon_timing": rec_m}
 
 
 def cpu_baselines(only):
