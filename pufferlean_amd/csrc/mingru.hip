@@ -84,22 +84,26 @@ __global__ void __launch_bounds__(256) k_scan_fwd(const TS* __restrict__ cmb, co
   const long BH = (long)B * H, B3H = (long)B * 3 * H;
   const long xo = (long)b * H + j, yo = (long)b * 3 * H + j;
   float state[4] = {0.f, 0.f, 0.f, 0.f};
+  // rolling prefetch: set c holds step t0 + c; after step t is computed its set is refilled with step
+  // t + kScanCh, so kScanCh - 1 steps stay in flight while one is computed
+  Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh];
+  float rd[kScanCh];
+  auto load = [&](int c, int t) __attribute__((always_inline)) {
+    const TS* yt = cmb + (long)t * B3H + yo;
+    rh[c] = ld4(yt);
+    rg[c] = ld4(yt + H);
+    rp[c] = ld4(yt + 2 * H);
+    rx[c] = ld4(hin + (long)t * BH + xo);
+    rd[c] = done[(long)t * B + b];
+  };
+#pragma unroll
+  for (int c = 0; c < kScanCh; c++)
+    if (c < T) load(c, c);
   for (int t0 = 0; t0 < T; t0 += kScanCh) {
-    Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh];
-    float rd[kScanCh];
 #pragma unroll
     for (int c = 0; c < kScanCh; c++) {
-      const int t = t0 + c < T ? t0 + c : T - 1;  // clamped: a step past T is loaded, not used
-      const TS* yt = cmb + (long)t * B3H + yo;
-      rh[c] = ld4(yt);
-      rg[c] = ld4(yt + H);
-      rp[c] = ld4(yt + 2 * H);
-      rx[c] = ld4(hin + (long)t * BH + xo);
-      rd[c] = done[(long)t * B + b];
-    }
-#pragma unroll
-    for (int c = 0; c < kScanCh; c++) {
-      if (t0 + c >= T) break;
+      const int t = t0 + c;
+      if (t >= T) break;
       float hv[4], ov[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -109,9 +113,10 @@ __global__ void __launch_bounds__(256) k_scan_fwd(const TS* __restrict__ cmb, co
         ov[q] = o;
         state[q] = rd[c] != 0.f ? 0.f : o;
       }
-      const long so = (long)(t0 + c) * BH + xo;
+      const long so = (long)t * BH + xo;
       st4(hout + so, hv);
       st4(oS + so, ov);
+      if (t + kScanCh < T) load(c, t + kScanCh);  // t is uniform: no lane loads past the end
     }
   }
 }
@@ -134,22 +139,25 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
   const long xo = (long)b * H + j, yo = (long)b * 3 * H + j;
   float dOn[4] = {0.f, 0.f, 0.f, 0.f};
   Raw4<TS> ocur = ld4(oS + (long)(T - 1) * BH + xo);
-  for (int t0 = T - 1; t0 >= 0; t0 -= kScanCh) {
-    Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh], rdh[kScanCh], rpo[kScanCh];
-    float rkeep[kScanCh];
+  // rolling prefetch (t descending): set c holds step t0 - c and is refilled with step t - kScanCh
+  // once step t is computed
+  Raw4<TS> rh[kScanCh], rg[kScanCh], rp[kScanCh], rx[kScanCh], rdh[kScanCh], rpo[kScanCh];
+  float rkeep[kScanCh];
+  auto load = [&](int c, int t) __attribute__((always_inline)) {
+    const int tp = t > 0 ? t - 1 : 0;
+    const TS* yt = cmb + (long)t * B3H + yo;
+    rh[c] = ld4(yt);
+    rg[c] = ld4(yt + H);
+    rp[c] = ld4(yt + 2 * H);
+    rx[c] = ld4(hin + (long)t * BH + xo);
+    rdh[c] = ld4(dhn + (long)t * BH + xo);
+    rpo[c] = ld4(oS + (long)tp * BH + xo);
+    rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
+  };
 #pragma unroll
-    for (int c = 0; c < kScanCh; c++) {
-      const int t = t0 - c >= 0 ? t0 - c : 0;  // clamped: a step before 0 is loaded, not used
-      const int tp = t > 0 ? t - 1 : 0;
-      const TS* yt = cmb + (long)t * B3H + yo;
-      rh[c] = ld4(yt);
-      rg[c] = ld4(yt + H);
-      rp[c] = ld4(yt + 2 * H);
-      rx[c] = ld4(hin + (long)t * BH + xo);
-      rdh[c] = ld4(dhn + (long)t * BH + xo);
-      rpo[c] = ld4(oS + (long)tp * BH + xo);
-      rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
-    }
+  for (int c = 0; c < kScanCh; c++)
+    if (T - 1 - c >= 0) load(c, T - 1 - c);
+  for (int t0 = T - 1; t0 >= 0; t0 -= kScanCh) {
 #pragma unroll
     for (int c = 0; c < kScanCh; c++) {
       const int t = t0 - c;
@@ -174,12 +182,12 @@ __global__ void __launch_bounds__(256) k_scan_bwd(const TS* __restrict__ cmb, co
         vdp[q] = dhg * hg * (1.f - hg);
         dOn[q] = keep_prev ? dprev : 0.f;
       }
-      const long so = (long)t * BH + xo;
       const long yw = (long)t * B3H + yo;
       st4(dy + yw, vdg);
       st4(dy + yw + H, vdz);
       st4(dy + yw + 2 * H, vdp);
       ocur = rpo[c];
+      if (t - kScanCh >= 0) load(c, t - kScanCh);  // t is uniform: no lane loads before step 0
     }
   }
 }
@@ -219,25 +227,28 @@ __global__ void __launch_bounds__(256) k_scan_bwd_top(const uint16_t* __restrict
   const uint4* wj = reinterpret_cast<const uint4*>(swp + j);  // + p * H / 4 for pair p
   float dOn[4] = {0.f, 0.f, 0.f, 0.f};
   Raw4<uint16_t> ocur = ld4(oS + (long)(T - 1) * BH + xo);
+  // rolling prefetch (t descending): set c holds step t0 - c and is refilled with step t - CH once
+  // step t is computed
+  Raw4<uint16_t> rh[CH], rg[CH], rp[CH], rx[CH], rpo[CH];
+  uint32_t rl[CH][NW];
+  float rkeep[CH];
+  auto load = [&](int c, int t) __attribute__((always_inline)) {
+    const int tp = t > 0 ? t - 1 : 0;
+    const uint16_t* yt = cmb + (long)t * B3H + yo;
+    rh[c] = ld4(yt);
+    rg[c] = ld4(yt + H);
+    rp[c] = ld4(yt + 2 * H);
+    rx[c] = ld4(hin + (long)t * BH + xo);
+    rpo[c] = ld4(oS + (long)tp * BH + xo);
+    const uint32_t* lr = reinterpret_cast<const uint32_t*>(dlb + ((long)t * B + b) * HP);
+#pragma unroll
+    for (int w = 0; w < NW; w++) rl[c][w] = lr[w];
+    rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
+  };
+#pragma unroll
+  for (int c = 0; c < CH; c++)
+    if (T - 1 - c >= 0) load(c, T - 1 - c);
   for (int t0 = T - 1; t0 >= 0; t0 -= CH) {
-    Raw4<uint16_t> rh[CH], rg[CH], rp[CH], rx[CH], rpo[CH];
-    uint32_t rl[CH][NW];
-    float rkeep[CH];
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-      const int t = t0 - c >= 0 ? t0 - c : 0;  // clamped: a step before 0 is loaded, not used
-      const int tp = t > 0 ? t - 1 : 0;
-      const uint16_t* yt = cmb + (long)t * B3H + yo;
-      rh[c] = ld4(yt);
-      rg[c] = ld4(yt + H);
-      rp[c] = ld4(yt + 2 * H);
-      rx[c] = ld4(hin + (long)t * BH + xo);
-      rpo[c] = ld4(oS + (long)tp * BH + xo);
-      const uint32_t* lr = reinterpret_cast<const uint32_t*>(dlb + ((long)t * B + b) * HP);
-#pragma unroll
-      for (int w = 0; w < NW; w++) rl[c][w] = lr[w];
-      rkeep[c] = (t > 0 && done[(long)tp * B + b] == 0.f) ? 1.f : 0.f;
-    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
       const int t = t0 - c;
@@ -280,6 +291,7 @@ __global__ void __launch_bounds__(256) k_scan_bwd_top(const uint16_t* __restrict
       st4(dy + yw + 2 * H, vdp);
       st4(skip + (long)t * BH + xo, vsk);
       ocur = rpo[c];
+      if (t - CH >= 0) load(c, t - CH);  // t is uniform: no lane loads before step 0
     }
   }
 }

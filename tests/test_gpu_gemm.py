@@ -358,3 +358,36 @@ def test_gemm_tn_split_k_128x256_tiles(gpu, M, N, K):
     ref = aT.double().t() @ b.double()
     assert float((c.double() - ref).norm() / ref.norm()) < 1e-5
     assert torch.equal(D.gemm(aT, b, trans_a=True), c)
+
+
+@pytest.mark.parametrize("epi", ["none", "none_f32", "bias", "bias_relu", "axpby"])
+def test_gemm_long_k_nt_pingpong(gpu, epi):
+    """NT bf16 products with k >= 1024 and both output extents multiples of 256 (the MinGRU data gradient's
+    form) take the ping-pong 256x256 kernel: each epilogue against the f64 product of the bf16-rounded
+    operands on sampled rows (one bf16 output rounding: 4e-3; fp32 output: 1e-5)."""
+    M, N, K = 32768, 512, 1536
+    rs = np.random.default_rng(0xF00 + len(epi))
+    a = rs.standard_normal((M, K), dtype=np.float32)
+    b = (rs.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    ga, gb = torch.from_numpy(a).cuda().bfloat16(), torch.from_numpy(b).cuda().bfloat16()
+    ar, br = bf16_round(a), bf16_round(b)
+    rows = np.sort(rs.choice(M, 384, replace=False))
+    ref = O.gemm(0, 1, ar[rows], br, len(rows), N, K, threads=8)
+    bias = torch.from_numpy(rs.standard_normal(N).astype(np.float32)).cuda()
+    aux = torch.from_numpy(rs.standard_normal((M, N)).astype(np.float32)).cuda().bfloat16()
+    kw = dict(trans_b=True, out_dtype=torch.float32 if epi == "none_f32" else torch.bfloat16)
+    if epi == "bias":
+        kw.update(epilogue=L.PH_EPI_BIAS, bias=bias)
+        ref = ref + bias.cpu().numpy()
+    elif epi == "bias_relu":
+        kw.update(epilogue=L.PH_EPI_BIAS_RELU, bias=bias)
+        ref = np.maximum(ref + bias.cpu().numpy(), 0.0)
+    elif epi == "axpby":
+        kw.update(epilogue=L.PH_EPI_AXPBY, aux=aux, alpha=0.75, beta=1.5)
+        ref = 0.75 * ref + 1.5 * aux.float().cpu().numpy()[rows]
+    c = D.gemm(ga, gb, **kw).float().cpu().numpy()
+    assert np.isfinite(c).all()
+    assert rel(c[rows], ref) < (1e-5 if epi == "none_f32" else 4e-3), rel(c[rows], ref)
+    if epi == "bias_relu":  # zeros exactly where the product is <= 0 (up to fp32 accumulation at ~0)
+        diff = (c[rows] == 0) != (ref <= 0)
+        assert np.all(np.abs(ref[diff]) < 1e-4)
