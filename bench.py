@@ -382,8 +382,11 @@ def bench_cartpole(steps, warmup):
     N = CP_B * CP_T
     out = {"rows": N, "envs": CP_B, "horizon": CP_T, "net": f"{CP_D}->{CP_H}x{CP_L}->{CP_A}+1"}
     flops_fwd = 2.0 * N * (CP_D * CP_H + (CP_L - 1) * CP_H * CP_H + CP_H * (CP_A + 1))
-    for name, math_ in (("f32", "f32"), ("bf16", "bf16")):
-        cfg = D.MLPConfig(N, CP_D, CP_H, CP_L, CP_A, math=math_, muon_math="f32")
+    # fp32 tier: fp32 products and fp32-MFMA Newton-Schulz; bf16 tier: bf16 products, and the three
+    # matrices' Newton-Schulz in one fused bf16 launch ("bf16_ns_f32": the bf16 products with the fp32
+    # Newton-Schulz)
+    for name, math_, mm in (("f32", "f32", "f32"), ("bf16", "bf16", "bf16"), ("bf16_ns_f32", "bf16", "f32")):
+        cfg = D.MLPConfig(N, CP_D, CP_H, CP_L, CP_A, math=math_, muon_math=mm)
         p0 = _t(params)
         obs = _t(c["obs"]).view(N, CP_D)
         act = _t(c["act"], np.int32)
@@ -397,7 +400,8 @@ def bench_cartpole(steps, warmup):
         ms = time_graph(lambda: D.mlp_update(cfg, CP_T, p, mom, obs, act, behav, rew, done, G=G), steps, warmup)
         tf = 3.0 * flops_fwd / (ms * 1e-3) / 1e12
         out[name] = {"us": round(ms * 1e3, 1), "samples_per_s": round(N / (ms * 1e-3), 1),
-                     "gemm_tflops": round(tf, 2), "finite": bool(torch.isfinite(p).all().item())}
+                     "gemm_tflops": round(tf, 2), "finite": bool(torch.isfinite(p).all().item()),
+                     "ns_ok": ns_ok()}
     out["gemm_flops"] = 3.0 * flops_fwd
     return out
 

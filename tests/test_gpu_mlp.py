@@ -145,15 +145,17 @@ def test_cartpole_update_vs_oracle_chain(gpu):
     assert np.all(np.isfinite(p.cpu().numpy()))
 
 
-def test_cartpole_update_bf16_vs_oracle_chain(gpu):
+@pytest.mark.parametrize("muon_math", ["f32", "bf16"])
+def test_cartpole_update_bf16_vs_oracle_chain(gpu, muon_math):
     """The bf16 tier of the CartPole-sized update (bf16 MFMA products and bf16 hidden activations, fp32
-    master weights, fp32 Newton-Schulz): per matrix and per bias, the new momentum and the weight change
-    within 2e-2 relative Frobenius of the f64 oracle chain, and the whole gradient within 2e-2 (the bar of
-    the two-hidden-layer bf16 gradient)."""
+    master weights; Newton-Schulz in fp32 MFMA, or in the fused bf16 launch with hi/lo split products):
+    per matrix and per bias, the new momentum and the weight change within 2e-2 relative Frobenius of the
+    f64 oracle chain, and the whole gradient within 2e-2 (the bar of the two-hidden-layer bf16 gradient)."""
     w = cartpole()
-    print(f"cartpole update bf16 N={w['N']} obs {w['Dm']} -> {w['H']} x {w['L']} -> {w['A']}+1", flush=True)
+    print(f"cartpole update bf16 (NS {muon_math}) N={w['N']} obs {w['Dm']} -> {w['H']} x {w['L']} -> {w['A']}+1",
+          flush=True)
     g_ref, p_ref, m_ref = oracle_update(w)
-    cfg = D.MLPConfig(w["N"], w["Dm"], w["H"], w["L"], w["A"], math="bf16", muon_math="f32")
+    cfg = D.MLPConfig(w["N"], w["Dm"], w["H"], w["L"], w["A"], math="bf16", muon_math=muon_math)
     p = t32(w["p"]); m = torch.zeros(cfg.P, device="cuda")
     G = D.mlp_update(cfg, w["T"], p, m, t32(w["obs"]), t32(w["act"], np.int32), t32(w["behav"]), t32(w["rew"]),
                      t32(w["done"]))
@@ -172,6 +174,8 @@ def test_cartpole_update_bf16_vs_oracle_chain(gpu):
     for name, (em, eu) in errs.items():
         assert em < 2e-2, (name, "momentum", em)
         assert eu < 2e-2, (name, "update", eu)
+    if muon_math == "bf16":
+        D.ns_status()
 
 
 def test_cartpole_update_graph_replay(gpu):
