@@ -1906,8 +1906,11 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
       // tiles, one block per CU, so each split reads its rows of A once (512x136x262144: 120 -> 109 us
       // against two 128-wide column tiles)
       wide_n = !big && d.trans_a && !d.trans_b && big_ok && d.N > 128 && d.N <= 256;
+      // 128x128 splits: two resident blocks per CU (512 blocks) for small outputs, one (256 blocks)
+      // once the output has >= 16 tiles (512x512x16384: 32 -> 16 splits, 31.8 -> 26.4 us: half the
+      // fp32 partials to write and fold)
       const long tw = (long)((d.M + 127) / 128);
-      const long want = big ? 256 / tiles256 : (wide_n ? 256 / tw : 512 / tiles128);
+      const long want = big ? 256 / tiles256 : (wide_n ? 256 / tw : (tiles128 >= 16 ? 256 : 512) / tiles128);
       const long maxs = d.K / (big ? 2048 : 512);
       splits = (int)(want < maxs ? want : maxs);
       if (splits < 1) splits = 1;
