@@ -37,6 +37,19 @@ DRIVER = textwrap.dedent(r"""
       size_t n = t.release([](void* p) { live.erase(p); std::free(p); });
       CHECK(n == 1 && t.retired.empty() && t.retired_bytes == 0 && live.count(a) == 0);
       CHECK(live.count(b) == 1 && t.peek(3) == b);     // current buffers survive a release
+      // a process whose shape grows step by step: every growth retires the previous buffer, all of
+      // them stay allocated until a release, and a release frees exactly the retired ones
+      size_t want = 5120, kept = 0;
+      for (int i = 0; i < 10; i++) {
+        kept += t.bytes[3];
+        want += 4096;
+        CHECK(t.get(3, want, alloc) != nullptr && t.bytes[3] >= want);
+      }
+      CHECK(t.retired.size() == 10 && t.retired_bytes == kept);
+      CHECK(live.size() == 12);                        // 10 retired + slots 3 and 5 current
+      CHECK(t.release([](void* p) { live.erase(p); std::free(p); }) == 10);
+      CHECK(live.size() == 2 && t.retired.empty() && t.retired_bytes == 0);
+      CHECK(t.get(3, want * 2, alloc) != nullptr && t.retired.size() == 1);  // the next growth retires one
       std::printf(fails ? "failed\n" : "ok\n");
       return fails ? 1 : 0;
     }
