@@ -222,7 +222,7 @@ def dominant_kernel():
     tf = flops / (gms * 1e-3) / 1e12
     del ops
     torch.cuda.empty_cache()
-    return {"name": "k_gemm_nt_pp (data gradient 262144x512x1536, bf16, AXPBY epilogue)", "us": round(gms * 1e3, 1),
+    return {"name": "k_gemm_nt_dma (data gradient 262144x512x1536, bf16, AXPBY epilogue)", "us": round(gms * 1e3, 1),
             "tflops": round(tf, 1), "flops": flops,
             "hbm_bytes": 2.0 * (rows * 3 * H5 + H5 * 3 * H5 + 2 * rows * H5)}
 

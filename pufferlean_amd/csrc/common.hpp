@@ -48,10 +48,6 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // footprints (a single workgroup may hold up to 160 KB on gfx950) stay out until a form using them
 // has been shown sound.
 constexpr int kMaxLdsBytes = 80 * 1024;
-// The one kernel that holds a CU alone (k_gemm_nt_pp: 128 KB, one 512-thread block per CU) asserts
-// against the device's limit instead; it has run bit-identical to the 80 KB kernel it replaces on the
-// data-gradient shapes, with every launch completing.
-constexpr int kMaxLdsBytesOneBlock = 160 * 1024;
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 

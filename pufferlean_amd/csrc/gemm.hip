@@ -1324,181 +1324,6 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Ping-pong NT bf16 GEMM for long reductions (the MinGRU data gradient, k = 1536): 256x256 tile, one
-// block of 8 wavefronts per CU in two groups of four. Wave w runs on SIMD w % 4, so each SIMD holds one
-// wave of each group. The groups alternate between a matrix phase (the 16 MFMAs of one k-tile out of
-// registers) and a memory phase (the LDS fragment reads of a k-tile; group 0 also waits for and issues
-// the load-to-LDS copies), with a block barrier between phases: while one wave of a SIMD multiplies,
-// the other reads. Four LDS stages of 32 KB (128 KB, three k-tiles in flight). Per MFMA the 256x256 tile
-// moves 2/3 of the 256x128 tile's operand bytes from L2. Each wave's 128x64 product runs the same MFMA
-// sequence over k as k_gemm_nt_dma, so the results are bit-identical to it.
-// Measured against k_gemm_nt_dma<256, 128> in one process (us): 262144x512x1536 461.7 vs 491.3 (and 478.4
-// vs 512.8 on a slower box); 262144x1536x512 503.1 vs 487.6 (short k: with one block per CU nothing
-// overlaps the fill and the epilogue), so only reductions of k >= 1024 take it. Five stages (160 KB)
-// measured slower (480.1). Ablations of the data gradient (us): without the copies 258, without the LDS
-// reads 413, without the MFMAs 339: the copies are the largest part, though the same copies alone
-// stream an 805 MB operand from HBM into LDS at 5.5-6 TB/s.
-template <typename TC, bool S16>
-__global__ void __launch_bounds__(512, 1) k_gemm_nt_pp(GemmArgs g) {
-  constexpr int BM = 256, BN = 256, BK = 32, NSTG = 4, GT = 256;
-  using Lay = LdsLayout<BK>;
-  constexpr int WM = 128, WN = 64, SM = WM / 32, SN = WN / 32;
-  constexpr int A_EL = BM * BK, B_EL = BN * BK, STAGE_EL = A_EL + B_EL;
-  constexpr int IA = A_EL / 8 / GT, IB = B_EL / 8 / GT;
-  constexpr int PIPE_BYTES = NSTG * STAGE_EL * 2;
-  static_assert(BM * BN * 2 <= PIPE_BYTES, "bf16 staging");
-  static_assert(PIPE_BYTES <= kMaxLdsBytesOneBlock, "LDS budget");
-  constexpr int LDC = BN + 4, EPR = 64;  // fp32 staging: 4 passes of 64 rows (66.5 KB)
-  static_assert(EPR * LDC * 4 <= PIPE_BYTES && EPR == 2 * 32, "epilogue staging rows");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES];
-  uint16_t* const stages = reinterpret_cast<uint16_t*>(smem);
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp = wave >> 2;
-  const int wm0 = grp * WM, wn0 = (wave & 3) * WN;
-  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-  int bm, bn;
-  tile_coords(g, tm, tn, bm, bn);
-  const int m0 = bm * BM, n0 = bn * BN;
-  const int kend = g.K;
-  const int nk = (kend + BK - 1) / BK;
-  const gptr<uint16_t> A = (gptr<uint16_t>)g.A;
-  const gptr<uint16_t> B = (gptr<uint16_t>)g.B;
-  auto slot_chunk = [](int p, int& row, int& kc) {
-    const int pr = p >> 2;
-    row = pr ^ ((pr >> 3) & 3);
-    kc = (p & 3) ^ ((row >> 2) & 3);
-  };
-  const gptr<uint16_t> Ablk = A + (long)m0 * g.lda, Bblk = B + (long)n0 * g.ldb;
-  const int gtid = tid & (GT - 1);
-  int offA[IA], offB[IB];
-  uint32_t kcA = 0u, kcB = 0u, rowA = 0u, rowB = 0u;
-#pragma unroll
-  for (int i = 0; i < IA; i++) {
-    int r, kc;
-    slot_chunk(i * GT + gtid, r, kc);
-    offA[i] = r * (int)g.lda + kc * 8;
-    kcA |= (uint32_t)kc << (2 * i);
-    rowA |= (m0 + r < g.M ? 1u : 0u) << i;
-  }
-#pragma unroll
-  for (int i = 0; i < IB; i++) {
-    int r, kc;
-    slot_chunk(i * GT + gtid, r, kc);
-    offB[i] = r * (int)g.ldb + kc * 8;
-    kcB |= (uint32_t)kc << (2 * i);
-    rowB |= (n0 + r < g.N ? 1u : 0u) << i;
-  }
-  const int gw = wave & 3;
-  auto issue = [&](int st, int k0) {  // group 0 only
-    uint16_t* base = stages + st * STAGE_EL;
-#pragma unroll
-    for (int i = 0; i < IA; i++) {
-      const bool ok = ((rowA >> i) & 1u) && k0 + (int)((kcA >> (2 * i)) & 3u) * 8 < kend;
-      copy_to_lds(ok ? Ablk + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * GT + gw * 64) * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < IB; i++) {
-      const bool ok = ((rowB >> i) & 1u) && k0 + (int)((kcB >> (2 * i)) & 3u) * 8 < kend;
-      copy_to_lds(ok ? Bblk + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * GT + gw * 64) * 8);
-    }
-  };
-  floatx16 acc[SM][SN];
-#pragma unroll
-  for (int i = 0; i < SM; i++)
-#pragma unroll
-    for (int j = 0; j < SN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-  const int lr = lane & 31, lk = (lane >> 5) * 16;
-  struct Frag { uint4 a[SM]; uint4 b[SN]; };
-  auto rd = [&](Frag& f, int st, int koff) {
-    const uint16_t* sa = stages + st * STAGE_EL;
-    const uint16_t* sb = sa + A_EL;
-#pragma unroll
-    for (int i = 0; i < SM; i++) f.a[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(wm0 + i * 32 + lr, koff)]);
-#pragma unroll
-    for (int j = 0; j < SN; j++) f.b[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(wn0 + j * 32 + lr, koff)]);
-  };
-  auto mm = [&](const Frag& f) {
-#pragma unroll
-    for (int i = 0; i < SM; i++)
-#pragma unroll
-      for (int j = 0; j < SN; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
-                                                            __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
-  };
-  Frag F0, F1;
-  if (nk > 0) {
-    if (grp == 0) {
-      issue(0, 0);
-      issue(1, BK);
-      issue(2, 2 * BK);
-      issue(3, 3 * BK);
-      wait_vm<3 * (IA + IB)>();  // k-tile 0 has landed
-      rd(F0, 0, lk);
-      rd(F1, 0, lk + 8);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    barrier_mem();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll 1
-    for (int kt = 0; kt < nk; kt++) {
-      const int st = kt & (NSTG - 1);
-      // phase 1: group 0 multiplies k-tile kt, group 1 reads it
-      if (grp == 0) {
-        mm(F0);
-        mm(F1);
-      } else {
-        rd(F0, st, lk);
-        rd(F1, st, lk + 8);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage kt is read before group 0 refills it
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      barrier_mem();
-      __builtin_amdgcn_sched_barrier(0);
-      // phase 2: group 1 multiplies k-tile kt, group 0 reads k-tile kt + 1 and refills stage kt
-      if (grp == 1) {
-        mm(F0);
-        mm(F1);
-      } else {
-        wait_vm<2 * (IA + IB)>();  // k-tile kt + 1 has landed (kt + 2, kt + 3 in flight)
-        if (kt + 1 < nk) {
-          rd(F0, (kt + 1) & (NSTG - 1), lk);
-          rd(F1, (kt + 1) & (NSTG - 1), lk + 8);
-        }
-        issue(st, (kt + NSTG) * BK);  // past the end: the zero page
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      barrier_mem();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (grp == 0) wait_vm<0>();
-  }
-  barrier_mem();
-  if constexpr (S16) {
-    uint32_t* sT = reinterpret_cast<uint32_t*>(smem);
-    if (g.epi == PH_EPI_NONE) stage_bf16<PH_EPI_NONE, BN>(g, sT, acc, wm0, wn0, n0, lane);
-    else if (g.epi == PH_EPI_BIAS) stage_bf16<PH_EPI_BIAS, BN>(g, sT, acc, wm0, wn0, n0, lane);
-    else stage_bf16<PH_EPI_BIAS_RELU, BN>(g, sT, acc, wm0, wn0, n0, lane);
-    lds_barrier();
-    flush_bf16<BM, BN, 512>(g, sT, m0, n0, tid);
-  } else {
-    // Pass p stages sub-tile p of every wave (wave row 0 into staged rows [0, 32), row 1 into
-    // [32, 64)), then the block flushes them: C rows m0 + 32 p and m0 + 128 + 32 p.
-    float* sC = reinterpret_cast<float*>(smem);
-    auto pass = [&](auto P) {
-      constexpr int p = decltype(P)::value;
-      if (p > 0) lds_barrier();  // the previous pass's flush has read the staging area
-      stage_acc_part<p, 1, SM, SN, LDC>(sC, acc, grp * 32, wn0, lane);
-      lds_barrier();
-      flush_tile<TC, EPR, BN, 512, LDC>(g, sC, m0 + p * 32, n0, m0 + WM + p * 32);
-    };
-    static_for(pass, std::make_integer_sequence<int, SM>{});
-  }
-}
-
-// ------------------------------------------------------------------------------------------------
 // fp32-math kernel (fp32 inputs only).
 template <int BM, int BN, int BK, bool TA, bool TB, typename TC>
 __global__ void __launch_bounds__(256) k_gemm_f32(GemmArgs g) {
@@ -1700,12 +1525,6 @@ void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStrea
     if (s16) k_gemm_nt_dma<256, 64, uint16_t, true><<<grid, 256, 0, st>>>(g);
     else if (g.c_bf16) k_gemm_nt_dma<256, 64, uint16_t><<<grid, 256, 0, st>>>(g);
     else k_gemm_nt_dma<256, 64, float><<<grid, 256, 0, st>>>(g);
-  } else if (!ta && tb && grid.z == 1 && g.M % 256 == 0 && g.N % 256 == 0 && g.K >= 1024) {
-    // long reductions: the ping-pong 256x256 kernel, one block per CU
-    const dim3 g2((unsigned)((g.M / 256) * (g.N / 256)), 1, 1);
-    if (s16) k_gemm_nt_pp<uint16_t, true><<<g2, 512, 0, st>>>(g);
-    else if (g.c_bf16) k_gemm_nt_pp<uint16_t, false><<<g2, 512, 0, st>>>(g);
-    else k_gemm_nt_pp<float, false><<<g2, 512, 0, st>>>(g);
   } else if (!ta && tb) {
     if (s16) k_gemm_nt_dma<256, 128, uint16_t, true><<<grid, 256, 0, st>>>(g);
     else if (g.c_bf16) k_gemm_nt_dma<256, 128, uint16_t><<<grid, 256, 0, st>>>(g);

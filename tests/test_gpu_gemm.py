@@ -361,10 +361,10 @@ def test_gemm_tn_split_k_128x256_tiles(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("epi", ["none", "none_f32", "bias", "bias_relu", "axpby"])
-def test_gemm_long_k_nt_pingpong(gpu, epi):
-    """NT bf16 products with k >= 1024 and both output extents multiples of 256 (the MinGRU data gradient's
-    form) take the ping-pong 256x256 kernel: each epilogue against the f64 product of the bf16-rounded
-    operands on sampled rows (one bf16 output rounding: 4e-3; fp32 output: 1e-5)."""
+def test_gemm_long_k_nt(gpu, epi):
+    """NT bf16 products with a long reduction (the MinGRU data gradient's form, k = 1536) on the
+    load-to-LDS kernel: each epilogue against the f64 product of the bf16-rounded operands on sampled
+    rows (one bf16 output rounding: 4e-3; fp32 output: 1e-5)."""
     M, N, K = 32768, 512, 1536
     rs = np.random.default_rng(0xF00 + len(epi))
     a = rs.standard_normal((M, K), dtype=np.float32)
