@@ -6,7 +6,8 @@
 // FAST_16BF semantics) or fp32 MFMA (v_mfma_f32_32x32x2_f32).
 //
 // Block = 4 wavefronts in a 2x2 grid over a BM x BN tile; each wavefront owns (BM/2) x (BN/2) as
-// 32x32 MFMA sub-tiles. Operand tiles are staged through double-buffered LDS in a k-contiguous
+// 32x32 MFMA sub-tiles (the load-to-LDS NT kernel also runs 256x256 tiles on a 4x4 grid of 16
+// wavefronts, one block per CU). Operand tiles are staged through double-buffered LDS in a k-contiguous
 // [row][BK+pad] layout so every MFMA operand fetch is one 16-byte LDS read per lane. Sources that
 // are k-contiguous (X in the forward, W^T) are copied with 16-byte vector moves; m/n-contiguous
 // sources (the dgrad weight, both wgrad operands) are transposed while being written to LDS.
@@ -1145,12 +1146,16 @@ __device__ __forceinline__ void copy_to_lds(gptr<uint16_t> src, const uint16_t* 
 
 // S16: the launch takes the bf16-staged epilogue (stage_bf16_ok, decided on the host), so each
 // instantiation carries one epilogue and its registers.
-template <int BM, int BN, typename TC, bool S16 = false>
-__global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
-  constexpr int BK = 32, NT = 256, NSTG = 3;
+// WGM x WGN wavefronts (2 x 2: two blocks per CU; 4 x 4: one block of sixteen wavefronts per CU) and
+// NSTG k-tile stages in LDS (NSTG - 1 in flight while one is read).
+template <int BM, int BN, typename TC, bool S16 = false, int WGM = 2, int WGN = 2, int NSTG = 3>
+__global__ void __launch_bounds__(64 * WGM * WGN, WGM * WGN == 4 ? 2 : 1) k_gemm_nt_dma(GemmArgs g) {
+  constexpr int BK = 32, NT = 64 * WGM * WGN;
+  static_assert(NSTG >= 3, "stages");
+  static_assert(S16 || (WGM == 2 && WGN == 2) || WGM == 4, "fp32-staged epilogue layouts");
   using Lay = LdsLayout<BK>;
   static_assert(Lay::kSwz && Lay::kPitch == BK, "DMA slots follow the unpadded swizzled layout");
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int SM = WM / 32, SN = WN / 32;
   constexpr int IA = BM * BK / 8 / NT, IB = BN * BK / 8 / NT;  // DMA rounds per stage
   static_assert(IA * NT * 8 == BM * BK && IB * NT * 8 == BN * BK, "tile/threads");
@@ -1161,13 +1166,14 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
   constexpr int EPR = epilogue_rows(BM, LDC * 4, PIPE_BYTES);
   static_assert(EPR >= 32 && BM % EPR == 0, "epilogue staging rows");
   constexpr int C_BYTES = EPR * LDC * 4;
-  static_assert((PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES) <= kMaxLdsBytes, "LDS budget");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES];
+  constexpr int SMEM = PIPE_BYTES > C_BYTES ? PIPE_BYTES : C_BYTES;
+  static_assert(SMEM <= (WGM * WGN == 4 ? kMaxLdsBytes : 160 * 1024), "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   uint16_t* const stages = reinterpret_cast<uint16_t*>(smem);  // stage s: A at s*STAGE_EL, B after
   float* sC = reinterpret_cast<float*>(smem);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = (wave / 2) * WM, wn0 = (wave % 2) * WN;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   int bm, bn;
   tile_coords(g, tm, tn, bm, bn);
@@ -1256,11 +1262,11 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
   // overlap the matrix core instead of preceding it. The barrier sits between the two sub-steps of a
   // k-tile: the reads of kt's second half are done by then, and kt + 1's first half is read after it.
   if (nk > 0) {
-    issue(0, kbeg);
-    issue(1, kbeg + BK);
-    wait_vm<IA + IB>();  // k-tile 0 has landed (1 may be in flight)
+#pragma unroll
+    for (int s = 0; s < NSTG - 1; s++) issue(s, kbeg + s * BK);
+    wait_vm<(NSTG - 2) * (IA + IB)>();  // k-tile 0 has landed (1 .. NSTG - 2 may be in flight)
     barrier_mem();
-    issue(2, kbeg + 2 * BK);
+    issue(NSTG - 1, kbeg + (NSTG - 1) * BK);
     Frag X, Y;
     rd(X, 0, lk);
     int st = 0;  // stage of k-tile kt
@@ -1268,10 +1274,10 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
     for (int kt = 0; kt < nk - 1; kt++) {
       rd(Y, st, lk + 8);   // second sub-step of kt, read while the first is multiplied
       mm(X);
-      wait_vm<IA + IB>();  // this wave's copies of kt + 1 have landed and its reads of kt are done
-      barrier_mem();       // ... every wave's: the stage of kt is free for kt + 3
-      issue(st, kbeg + (kt + 3) * BK);
-      st = st == 2 ? 0 : st + 1;
+      wait_vm<(NSTG - 2) * (IA + IB)>();  // this wave's copies of kt + 1 have landed, its reads of kt are done
+      barrier_mem();       // ... every wave's: the stage of kt is free for kt + NSTG
+      issue(st, kbeg + (kt + NSTG) * BK);
+      st = st == NSTG - 1 ? 0 : st + 1;
       rd(X, st, lk);  // first sub-step of kt + 1, read while the second of kt is multiplied
       mm(Y);
       // issue order: products of X with the reads of Y between them, then (after the barrier) the
@@ -1302,6 +1308,17 @@ __global__ void __launch_bounds__(256, 2) k_gemm_nt_dma(GemmArgs g) {
     else stage_bf16<PH_EPI_BIAS_RELU, BN>(g, sT, acc, wm0, wn0, n0, lane);
     lds_barrier();
     flush_bf16<BM, BN, NT>(g, sT, m0, n0, tid);
+  } else if constexpr (WGM == 4) {
+    // one wavefront row per pass: staged rows [0, WM) are C rows m0 + p WM ..
+    static_assert(WM * LDC * 4 <= SMEM && WM % 8 == 0, "epilogue staging rows");
+    auto pass = [&](auto P) {
+      constexpr int p = decltype(P)::value;
+      if (p > 0) lds_barrier();  // the previous pass's flush has read the staging area
+      if (wave / WGN == p) stage_acc<SM, SN, LDC>(sC, acc, 0, wn0, lane);
+      lds_barrier();
+      flush_tile<TC, WM, BN, NT, LDC>(g, sC, m0 + p * WM, n0);
+    };
+    static_for(pass, std::make_integer_sequence<int, WGM>{});
   } else if constexpr (EPR == BM) {
     stage_acc<SM, SN, LDC>(sC, acc, wm0, wn0, lane);
     lds_barrier();
@@ -1753,10 +1770,22 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
     g.ws = (float*)scratch(d.ws_slot > 0 ? d.ws_slot : kSlotGemmWs, (size_t)splits * d.M * d.N * 4);
     if (!g.ws) return PH_ERR_NOMEM;
   }
-  const int bm = big ? 256 : (small ? 64 : 128), bn = big ? big_bn : (wide_n ? 256 : bm);
+  // Big NT bf16 products with 256-aligned N and no split: 256x256 tiles, sixteen 64x64 wavefronts in
+  // one block per CU, four k-tile stages (128 KB). Half the operand re-reads of 256x128 tiles and twice
+  // the wavefronts issuing copies per CU; the same MFMA sequence per element, so bit-identical to the
+  // 256x128 kernel. Inside the MinGRU step: data gradient 528 -> 503 us, layer forward 512-521 ->
+  // 505-517 us, encoder forward 114-119 -> 108-110 us (kernel traces, alternated builds on one box; five
+  // stages measured the same).
+  const bool w16 = big && big_bn == 128 && !d.trans_a && d.trans_b && splits == 1 && d.N % 256 == 0;
+  const int bm = big ? 256 : (small ? 64 : 128), bn = w16 ? 256 : (big ? big_bn : (wide_n ? 256 : bm));
   const unsigned tiles = (unsigned)(((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn));
   dim3 grid(tiles, 1, splits);
-  if (big) {
+  if (w16) {
+    if (g.c_bf16 && stage_bf16_ok(g, flush_vec<uint16_t>(g)))
+      k_gemm_nt_dma<256, 256, uint16_t, true, 4, 4, 4><<<grid, 1024, 0, st>>>(g);
+    else if (g.c_bf16) k_gemm_nt_dma<256, 256, uint16_t, false, 4, 4, 4><<<grid, 1024, 0, st>>>(g);
+    else k_gemm_nt_dma<256, 256, float, false, 4, 4, 4><<<grid, 1024, 0, st>>>(g);
+  } else if (big) {
     dispatch_big(g, bn, d.trans_a, d.trans_b, grid, st);
   } else if (wide_n) {
     launch_bf16<128, 256, 32, true, false, uint16_t, uint16_t>(g, grid, st);
