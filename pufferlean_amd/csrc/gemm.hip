@@ -1773,9 +1773,9 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   // Big NT bf16 products with 256-aligned N and no split: 256x256 tiles, sixteen 64x64 wavefronts in
   // one block per CU, four k-tile stages (128 KB). Half the operand re-reads of 256x128 tiles and twice
   // the wavefronts issuing copies per CU; the same MFMA sequence per element, so bit-identical to the
-  // 256x128 kernel. Inside the MinGRU step: data gradient 528 -> 503 us, layer forward 512-521 ->
-  // 505-517 us, encoder forward 114-119 -> 108-110 us (kernel traces, alternated builds on one box; five
-  // stages measured the same).
+  // 256x128 kernel. Back to back over rotating operand sets the data gradient goes 528 -> 502 us; inside
+  // the MinGRU step (kernel traces, alternated builds on one box) the data gradient 527 -> 523 us mean,
+  // the layer forward 518 -> 515 and the encoder forward 114.5 -> 110 (five stages measured the same).
   const bool w16 = big && big_bn == 128 && !d.trans_a && d.trans_b && splits == 1 && d.N % 256 == 0;
   const int bm = big ? 256 : (small ? 64 : 128), bn = w16 ? 256 : (big ? big_bn : (wide_n ? 256 : bm));
   const unsigned tiles = (unsigned)(((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn));
