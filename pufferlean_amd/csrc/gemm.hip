@@ -1146,11 +1146,37 @@ __device__ __forceinline__ void copy_to_lds(gptr<uint16_t> src, const uint16_t* 
 
 // S16: the launch takes the bf16-staged epilogue (stage_bf16_ok, decided on the host), so each
 // instantiation carries one epilogue and its registers.
+// The MFMA fragment of 32 columns c0.. (lane: column c0 + lane % 32) and 8 k-rows koff.. from a stage
+// stored [k][LD] with XOR-permuted 16-byte chunks. ds_read_b64_tr_b16 exchanges data within each group
+// of 16 lanes: lane j receives element j % 4 of the 8 bytes that lane 4q + j / 4 addressed, as its value
+// q (measured lane layout). So lane s of a group addresses k-row koff + 4h + s / 4 at columns
+// 4 (s % 4) .. + 3 of its 16, and lane j receives column j at k-rows koff + 4h + 0..3.
+typedef short ph_v4i16 __attribute__((ext_vector_type(4)));
+template <int LD>
+__device__ __forceinline__ uint4 rd_tr(const uint16_t* s, int c0, int koff, int lane) {
+  const int sl = lane & 15, cb = c0 + ((lane >> 4) & 1) * 16 + 4 * (sl & 3);
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int r = koff + 4 * h + (sl >> 2);
+    const int e = r * LD + ((((cb >> 3) ^ ((r & 3) << 2))) << 3) + (cb & 7);
+    const ph_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) ph_v4i16*)(__attribute__((address_space(3))) void*)(s + e));
+    w[2 * h] = (uint32_t)(uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16);
+    w[2 * h + 1] = (uint32_t)(uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // WGM x WGN wavefronts (2 x 2: two blocks per CU; 4 x 4: one block of sixteen wavefronts per CU) and
 // NSTG k-tile stages in LDS (NSTG - 1 in flight while one is read).
-template <int BM, int BN, typename TC, bool S16 = false, int WGM = 2, int WGN = 2, int NSTG = 3>
+// TN: A stored [K][M] and B stored [K][N] (the weight-gradient form): each stage holds BK k-rows of the
+// BM (BN) columns, the 16-byte chunks of a row XOR-permuted by the row's low two bits, and fragments are
+// read with the LDS transpose read (ds_read_b64_tr_b16, two per fragment).
+template <int BM, int BN, typename TC, bool S16 = false, int WGM = 2, int WGN = 2, int NSTG = 3, bool TN = false>
 __global__ void __launch_bounds__(64 * WGM * WGN, WGM * WGN == 4 ? 2 : 1) k_gemm_nt_dma(GemmArgs g) {
   constexpr int BK = 32, NT = 64 * WGM * WGN;
+  static_assert(!TN || (BM >= 128 && BN >= 128 && !S16), "transposed stages: 16+ chunks per row");
   static_assert(NSTG >= 3, "stages");
   static_assert(S16 || (WGM == 2 && WGN == 2) || WGM == 4, "fp32-staged epilogue layouts");
   using Lay = LdsLayout<BK>;
@@ -1195,37 +1221,68 @@ __global__ void __launch_bounds__(64 * WGM * WGN, WGM * WGN == 4 ? 2 : 1) k_gemm
   // Per round: the chunk's offset from the tile's first row (32-bit: 256 rows of a row-major operand),
   // its k offset (2 bits, x8) and whether its row is inside the matrix (1 bit); kept compact so the
   // accumulators and fragments fit two wavefronts per SIMD without spilling.
-  const gptr<uint16_t> Ablk = A + (long)m0 * g.lda, Bblk = B + (long)n0 * g.ldb;
+  // TN: the chunk's k-row in the stage (5 bits) and whether its 8 columns are inside the matrix
+  static_assert(!TN || (IA <= 6 && IB <= 6), "k-row fields");
+  const gptr<uint16_t> Ablk = A + (TN ? (long)m0 : (long)m0 * g.lda), Bblk = B + (TN ? (long)n0 : (long)n0 * g.ldb);
   int offA[IA], offB[IB];
   uint32_t kcA = 0u, kcB = 0u, rowA = 0u, rowB = 0u;
 #pragma unroll
   for (int i = 0; i < IA; i++) {
     int r, kc;
-    slot_chunk(i * NT + tid, r, kc);
-    offA[i] = r * (int)g.lda + kc * 8;
-    kcA |= (uint32_t)kc << (2 * i);
-    rowA |= (m0 + r < g.M ? 1u : 0u) << i;
+    if constexpr (TN) {
+      const int p = i * NT + tid;
+      r = p / (BM / 8);
+      kc = (p % (BM / 8)) ^ ((r & 3) << 2);  // column chunk
+      offA[i] = r * (int)g.lda + kc * 8;
+      kcA |= (uint32_t)r << (5 * i);
+      rowA |= (m0 + kc * 8 < g.M ? 1u : 0u) << i;
+    } else {
+      slot_chunk(i * NT + tid, r, kc);
+      offA[i] = r * (int)g.lda + kc * 8;
+      kcA |= (uint32_t)kc << (2 * i);
+      rowA |= (m0 + r < g.M ? 1u : 0u) << i;
+    }
   }
 #pragma unroll
   for (int i = 0; i < IB; i++) {
     int r, kc;
-    slot_chunk(i * NT + tid, r, kc);
-    offB[i] = r * (int)g.ldb + kc * 8;
-    kcB |= (uint32_t)kc << (2 * i);
-    rowB |= (n0 + r < g.N ? 1u : 0u) << i;
+    if constexpr (TN) {
+      const int p = i * NT + tid;
+      r = p / (BN / 8);
+      kc = (p % (BN / 8)) ^ ((r & 3) << 2);
+      offB[i] = r * (int)g.ldb + kc * 8;
+      kcB |= (uint32_t)r << (5 * i);
+      rowB |= (n0 + kc * 8 < g.N ? 1u : 0u) << i;
+    } else {
+      slot_chunk(i * NT + tid, r, kc);
+      offB[i] = r * (int)g.ldb + kc * 8;
+      kcB |= (uint32_t)kc << (2 * i);
+      rowB |= (n0 + r < g.N ? 1u : 0u) << i;
+    }
   }
   // copy the k-tile at k0 into stage st (a k-tile past the end copies zeros)
   auto issue = [&](int st, int k0) {
     uint16_t* base = stages + st * STAGE_EL;
 #pragma unroll
     for (int i = 0; i < IA; i++) {
-      const bool ok = ((rowA >> i) & 1u) && k0 + (int)((kcA >> (2 * i)) & 3u) * 8 < kend;
-      copy_to_lds(ok ? Ablk + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
+      if constexpr (TN) {
+        const bool ok = ((rowA >> i) & 1u) && k0 + (int)((kcA >> (5 * i)) & 31u) < kend;
+        copy_to_lds(ok ? Ablk + (offA[i] + (long)k0 * g.lda) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
+      } else {
+        const bool ok = ((rowA >> i) & 1u) && k0 + (int)((kcA >> (2 * i)) & 3u) * 8 < kend;
+        copy_to_lds(ok ? Ablk + (offA[i] + k0) : zero_page<uint16_t>(), base + (i * NT + wave * 64) * 8);
+      }
     }
 #pragma unroll
     for (int i = 0; i < IB; i++) {
-      const bool ok = ((rowB >> i) & 1u) && k0 + (int)((kcB >> (2 * i)) & 3u) * 8 < kend;
-      copy_to_lds(ok ? Bblk + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * NT + wave * 64) * 8);
+      if constexpr (TN) {
+        const bool ok = ((rowB >> i) & 1u) && k0 + (int)((kcB >> (5 * i)) & 31u) < kend;
+        copy_to_lds(ok ? Bblk + (offB[i] + (long)k0 * g.ldb) : zero_page<uint16_t>(),
+                    base + A_EL + (i * NT + wave * 64) * 8);
+      } else {
+        const bool ok = ((rowB >> i) & 1u) && k0 + (int)((kcB >> (2 * i)) & 3u) * 8 < kend;
+        copy_to_lds(ok ? Bblk + (offB[i] + k0) : zero_page<uint16_t>(), base + A_EL + (i * NT + wave * 64) * 8);
+      }
     }
   };
 
@@ -1243,10 +1300,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN, WGM * WGN == 4 ? 2 : 1) k_gemm
   auto rd = [&](Frag& f, int st, int koff) {
     const uint16_t* sa = stages + st * STAGE_EL;
     const uint16_t* sb = sa + A_EL;
+    if constexpr (TN) {
 #pragma unroll
-    for (int i = 0; i < SM; i++) f.a[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(wm0 + i * 32 + lr, koff)]);
+      for (int i = 0; i < SM; i++) f.a[i] = rd_tr<BM>(sa, wm0 + i * 32, koff, lane);
 #pragma unroll
-    for (int j = 0; j < SN; j++) f.b[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(wn0 + j * 32 + lr, koff)]);
+      for (int j = 0; j < SN; j++) f.b[j] = rd_tr<BN>(sb, wn0 + j * 32, koff, lane);
+    } else {
+#pragma unroll
+      for (int i = 0; i < SM; i++) f.a[i] = *reinterpret_cast<const uint4*>(&sa[Lay::off(wm0 + i * 32 + lr, koff)]);
+#pragma unroll
+      for (int j = 0; j < SN; j++) f.b[j] = *reinterpret_cast<const uint4*>(&sb[Lay::off(wn0 + j * 32 + lr, koff)]);
+    }
   };
   auto mm = [&](const Frag& f) {
 #pragma unroll
@@ -1536,7 +1600,13 @@ void dispatch_bf16_t(const GemmArgs& g, int ta, int tb, dim3 grid, hipStream_t s
 // 5 % faster on the policy shapes).
 void dispatch_big(const GemmArgs& g, int bn, int ta, int tb, dim3 grid, hipStream_t st) {
   const bool s16 = g.c_bf16 && stage_bf16_ok(g, flush_vec<uint16_t>(g));
-  if (bn == 256) {
+  if (bn == 256 && ta && !tb) {
+    // TN at 256x256 (the weight gradients): load-to-LDS copies of k-rows and transposing fragment reads,
+    // no register transposes. The same MFMA sequence per element as the register-staged kernel
+    // (bit-identical); the layer weight gradients 1536x512x262144 487 -> 364-373 us inside the step
+    if (g.c_bf16) k_gemm_nt_dma<256, 256, uint16_t, false, 4, 4, 4, true><<<grid, 1024, 0, st>>>(g);
+    else k_gemm_nt_dma<256, 256, float, false, 4, 4, 4, true><<<grid, 1024, 0, st>>>(g);
+  } else if (bn == 256) {
     dispatch_bf16_t<256, 256, 32, uint16_t, uint16_t>(g, ta, tb, grid, st);
   } else if (!ta && tb && bn == 64) {
     if (s16) k_gemm_nt_dma<256, 64, uint16_t, true><<<grid, 256, 0, st>>>(g);
@@ -1734,13 +1804,15 @@ int gemm(const PhGemmDesc& d_in, hipStream_t st) {
   int big_bn = !d.trans_a && d.trans_b && d.N <= 64 ? 64 : 128;
   if (!big && d.splits <= 0 && tiles128 < 128) {
     if (d.K >= 4096) {
-      // 256x256 splits when both output extents fill the tile and the reduction is long enough to
+      // 256x256 splits when the output fills the tile (TN products from 129 columns: their 256x256
+      // kernel copies k-rows, so a narrow tile wastes MFMA work but no operand traffic; the encoder's
+      // 512x136x262144 weight gradient 113 -> 70 us inside the step) and the reduction is long enough to
       // give every one of the 256 resident blocks >= 2048 of k; else 128x128 splits of >= 512
-      big = big_ok && d.M >= 256 && d.N >= 256 && d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
+      big = big_ok && d.M >= 256 && (d.N >= 256 || (d.trans_a && !d.trans_b && d.N > 128)) &&
+            d.K >= 2048L * (256 / (tiles256 > 0 ? tiles256 : 1));
       big_bn = 256;
-      // TN bf16 products 129..256 wide (the encoder's weight gradient with its bias column): 128x256
-      // tiles, one block per CU, so each split reads its rows of A once (512x136x262144: 120 -> 109 us
-      // against two 128-wide column tiles)
+      // TN bf16 products 129..256 wide that the 256x256 splits do not take (fewer than 256 rows or a
+      // shorter reduction): 128x256 tiles, one block per CU, so each split reads its rows of A once
       wide_n = !big && d.trans_a && !d.trans_b && big_ok && d.N > 128 && d.N <= 256;
       // 128x128 splits: two resident blocks per CU (512 blocks) for small outputs, one (256 blocks)
       // once the output has >= 16 tiles (512x512x16384: 32 -> 16 splits, 31.8 -> 26.4 us: half the
